@@ -1,0 +1,314 @@
+// Packed variable-length bidirectional attention for gfx950.
+//
+// Replaces esm::kernels::AttentionVarlen (reference
+// src/kernels/attention.cpp:99-144 AttentionVarlenRef and :770-811
+// AttentionVarlenAvx512): per sequence b (rows [cu[b], cu[b+1])), per head
+// h, out = softmax(q k^T) v with no mask inside the segment and no
+// attention across segments. Q arrives pre-scaled (ESM scales Q before
+// RoPE, reference src/model.cpp:975-988).
+//
+// MFMA path (head_dim 64): one workgroup per (sequence, head, 128-query
+// tile); its four waves each own 32 queries. Keys are processed in chunks
+// of 128 staged through LDS: K row-major (bf16), V transposed to [dim][key]
+// and converted to fp16. Each wave computes S^T = K Q^T with
+// v_mfma_f32_16x16x32_bf16, so every lane ends up holding probabilities for
+// one query and four consecutive keys per 16-key block -- exactly the B
+// operand layout of O^T = V^T P^T on v_mfma_f32_16x16x32_f16. Softmax is an
+// online (running max / running sum) fp32 softmax in base 2; the
+// probabilities are rounded to fp16 before both the PV product and the
+// running sum, so the normalisation uses the same weights as the product.
+//
+// fp32 path (any head_dim <= 128): one wave per (sequence, head, 64-query
+// tile), one lane per query; two passes over the keys (max, then
+// exp/sum/weighted V with a double-precision sum), the reference's order.
+#include <math.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace esm_gfx950 {
+namespace {
+
+constexpr int KC = 128;                 // keys per LDS chunk
+constexpr int kKPitch = 64 * 2 + 16;    // bytes per key row of K (bf16)
+constexpr int kVPitch = KC * 2 + 16;    // bytes per dim row of V^T (fp16)
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ uint16_t bf16_to_f16_bits(uint16_t b) {
+  return f32_to_f16_bits(bf16_bits_to_f32(b));
+}
+
+template <bool V_BF16>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, int ld, const int* __restrict__ cu,
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out,
+    float* tensor_absmax) {
+  __shared__ __attribute__((aligned(16))) uint8_t sK[KC * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t sVt[64 * kVPitch];
+
+  const AttnWork w = work[blockIdx.x];
+  const int start = cu[w.seq];
+  const int L = cu[w.seq + 1] - start;
+  const int hoff = w.head * 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int qbase = w.q0 + wave * 32;
+  const bool active = qbase < L;  // wave-uniform
+
+  bf16x8 qf[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int qi = qbase + qb * 16 + lr;
+    qi = qi < L ? qi : L - 1;
+    const uint16_t* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
+    qf[qb][0] = *reinterpret_cast<const bf16x8*>(qp + lg * 8);
+    qf[qb][1] = *reinterpret_cast<const bf16x8*>(qp + 32 + lg * 8);
+  }
+
+  f32x4 o[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrun[2] = {-INFINITY, -INFINITY};
+  float lrun[2] = {0.f, 0.f};
+
+  for (int kc0 = 0; kc0 < L; kc0 += KC) {
+    const int nkeys = min(KC, L - kc0);
+    __syncthreads();
+    // K chunk: KC rows x 128 bytes; rows past the sequence are zero.
+#pragma unroll
+    for (int i = 0; i < KC * 8 / 256; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      const int key = idx >> 3, c = idx & 7;
+      uint4 val = make_uint4(0u, 0u, 0u, 0u);
+      if (key < nkeys)
+        val = *reinterpret_cast<const uint4*>(k + static_cast<size_t>(start + kc0 + key) * ld + hoff + c * 8);
+      *reinterpret_cast<uint4*>(sK + key * kKPitch + c * 16) = val;
+    }
+    // V chunk transposed: each thread takes a key pair and 8 dims and
+    // writes 8 dwords (key pair packed) into V^T rows.
+#pragma unroll
+    for (int i = 0; i < KC * 4 / 256; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      const int kp = idx % (KC / 2), dg = idx / (KC / 2);
+      const int key0 = 2 * kp;
+      uint4 a = make_uint4(0u, 0u, 0u, 0u), b = a;
+      const uint16_t* vp = v + static_cast<size_t>(start + kc0 + key0) * ld + hoff + dg * 8;
+      if (key0 < nkeys) a = *reinterpret_cast<const uint4*>(vp);
+      if (key0 + 1 < nkeys) b = *reinterpret_cast<const uint4*>(vp + ld);
+      const uint16_t* ah = reinterpret_cast<const uint16_t*>(&a);
+      const uint16_t* bh = reinterpret_cast<const uint16_t*>(&b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t lo = ah[j], hi = bh[j];
+        if constexpr (V_BF16) {
+          lo = bf16_to_f16_bits(static_cast<uint16_t>(lo));
+          hi = bf16_to_f16_bits(static_cast<uint16_t>(hi));
+        }
+        *reinterpret_cast<uint32_t*>(sVt + (dg * 8 + j) * kVPitch + key0 * 2) = lo | (hi << 16);
+      }
+    }
+    __syncthreads();
+    if (!active) continue;
+
+    const int nkb = (nkeys + 15) >> 4;
+    f32x4 s[8][2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+      if (kb < nkb) {
+        const uint8_t* kp = sK + (kb * 16 + lr) * kKPitch + lg * 16;
+        const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kp);
+        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kp + 64);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[qb][1], acc, 0, 0, 0);
+        }
+      }
+    }
+
+    // Online softmax in base 2; lane holds keys kb*16 + 4*lg + i.
+    f16x4 pv[8][2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        if (kb < nkb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb * 16 + lg * 4 + i;
+            const float sv = key < nkeys ? s[kb][qb][i] * kLog2e : -INFINITY;
+            s[kb][qb][i] = sv;
+            cmax = fmaxf(cmax, sv);
+          }
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      const float mnew = fmaxf(mrun[qb], cmax);
+      const float alpha = exp2f(mrun[qb] - mnew);
+      mrun[qb] = mnew;
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        if (kb < nkb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const _Float16 ph = static_cast<_Float16>(exp2f(s[kb][qb][i] - mnew));
+            pv[kb][qb][i] = ph;
+            psum += static_cast<float>(ph);
+          }
+        }
+      }
+      lrun[qb] = lrun[qb] * alpha + psum;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+    }
+
+    // O^T += V^T P^T over key-block pairs.
+#pragma unroll
+    for (int kp = 0; kp < 4; ++kp) {
+      if (2 * kp < nkb) {
+        f16x8 pf[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const f16x4 a = pv[2 * kp][qb];
+          const f16x4 b = (2 * kp + 1 < nkb) ? pv[2 * kp + 1][qb] : f16x4{0, 0, 0, 0};
+          pf[qb] = f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const uint8_t* vr = sVt + (db * 16 + lr) * kVPitch;
+          const f16x4 va = *reinterpret_cast<const f16x4*>(vr + ((2 * kp) * 16 + lg * 4) * 2);
+          const f16x4 vb = *reinterpret_cast<const f16x4*>(vr + ((2 * kp + 1) * 16 + lg * 4) * 2);
+          const f16x8 vf = f16x8{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+            o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qb], o[qb][db], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  if (!active) return;
+  float amax = 0.f;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float lt = lrun[qb];
+    lt += __shfl_xor(lt, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    const float inv = 1.0f / lt;
+    const int qi = qbase + qb * 16 + lr;
+    if (qi < L) {
+      float* orow = out + static_cast<size_t>(start + qi) * ld_out + hoff + lg * 4;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const float4 r = make_float4(o[qb][db][0] * inv, o[qb][db][1] * inv,
+                                     o[qb][db][2] * inv, o[qb][db][3] * inv);
+        *reinterpret_cast<float4*>(orow + db * 16) = r;
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(r.x), fabsf(r.y)), fmaxf(fabsf(r.z), fabsf(r.w))));
+      }
+    }
+  }
+  if (tensor_absmax) {
+    amax = wave_max(amax);
+    if (lane == 0) atomic_max_nonneg(tensor_absmax, amax);
+  }
+}
+
+template <int DH_MAX>
+__global__ __launch_bounds__(64) void attn_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int ld, int dh, const int* __restrict__ cu,
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
+  const AttnWork w = work[blockIdx.x];
+  const int start = cu[w.seq];
+  const int L = cu[w.seq + 1] - start;
+  const int hoff = w.head * dh;
+  const int qi = w.q0 + static_cast<int>(threadIdx.x);
+  const bool valid = qi < L;
+  const int qc = valid ? qi : L - 1;
+
+  float qr[DH_MAX];
+  const float* qp = q + static_cast<size_t>(start + qc) * ld + hoff;
+#pragma unroll
+  for (int d = 0; d < DH_MAX; ++d) qr[d] = d < dh ? qp[d] : 0.f;
+
+  float mx = -INFINITY;
+  for (int j = 0; j < L; ++j) {
+    const float* kp = k + static_cast<size_t>(start + j) * ld + hoff;
+    float dot = 0.f;
+#pragma unroll
+    for (int d = 0; d < DH_MAX; ++d)
+      if (d < dh) dot += qr[d] * kp[d];
+    mx = fmaxf(mx, dot);
+  }
+  double sum = 0.0;
+  float acc[DH_MAX];
+#pragma unroll
+  for (int d = 0; d < DH_MAX; ++d) acc[d] = 0.f;
+  for (int j = 0; j < L; ++j) {
+    const float* kp = k + static_cast<size_t>(start + j) * ld + hoff;
+    float dot = 0.f;
+#pragma unroll
+    for (int d = 0; d < DH_MAX; ++d)
+      if (d < dh) dot += qr[d] * kp[d];
+    const float e = expf(dot - mx);
+    sum += e;
+    const float* vp = v + static_cast<size_t>(start + j) * ld + hoff;
+#pragma unroll
+    for (int d = 0; d < DH_MAX; ++d)
+      if (d < dh) acc[d] += e * vp[d];
+  }
+  if (!valid) return;
+  const float inv = sum > 0.0 ? static_cast<float>(1.0 / sum) : 0.f;
+  float* orow = out + static_cast<size_t>(start + qi) * ld_out + hoff;
+#pragma unroll
+  for (int d = 0; d < DH_MAX; ++d)
+    if (d < dh) orow[d] = acc[d] * inv;
+}
+
+}  // namespace
+
+hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
+                                 const uint16_t* v, int v_is_bf16, int ld,
+                                 const int* cu_seqlens, const AttnWork* work,
+                                 int num_work, float* out, int ld_out,
+                                 float* tensor_absmax, hipStream_t s) {
+  if (num_work <= 0) return hipSuccess;
+  const dim3 grid(num_work), block(256);
+  if (v_is_bf16) {
+    hipLaunchKernelGGL(attn_mfma_kernel<true>, grid, block, 0, s, q, k, v, ld,
+                       cu_seqlens, work, out, ld_out, tensor_absmax);
+  } else {
+    hipLaunchKernelGGL(attn_mfma_kernel<false>, grid, block, 0, s, q, k, v, ld,
+                       cu_seqlens, work, out, ld_out, tensor_absmax);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
+                                int ld, int head_dim, const int* cu_seqlens,
+                                const AttnWork* work, int num_work, float* out,
+                                int ld_out, hipStream_t s) {
+  if (num_work <= 0) return hipSuccess;
+  const dim3 grid(num_work), block(64);
+  if (head_dim <= 16) {
+    hipLaunchKernelGGL(attn_f32_kernel<16>, grid, block, 0, s, q, k, v, ld, head_dim, cu_seqlens, work, out, ld_out);
+  } else if (head_dim <= 32) {
+    hipLaunchKernelGGL(attn_f32_kernel<32>, grid, block, 0, s, q, k, v, ld, head_dim, cu_seqlens, work, out, ld_out);
+  } else if (head_dim <= 64) {
+    hipLaunchKernelGGL(attn_f32_kernel<64>, grid, block, 0, s, q, k, v, ld, head_dim, cu_seqlens, work, out, ld_out);
+  } else if (head_dim <= 128) {
+    hipLaunchKernelGGL(attn_f32_kernel<128>, grid, block, 0, s, q, k, v, ld, head_dim, cu_seqlens, work, out, ld_out);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace esm_gfx950

@@ -1,0 +1,1172 @@
+// C ABI of the gfx950 backend (declared in include/esm_gfx950.h): context
+// and stream, device weight cache, op-level entry points mirroring
+// esm::kernels::* and the device-resident packed forward that replaces
+// Model::ForwardPackedInto (reference src/model.cpp:1093-1255).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "esm_gfx950.h"
+#include "kernels.hpp"
+
+using namespace esm_gfx950;
+
+namespace {
+
+constexpr int kHeadDimMfma = 64;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+int pad16(int k) { return (k + 15) & ~15; }
+
+}  // namespace
+
+struct esm_gfx950_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::string arch;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  // Op-level scratch (grown on demand; the forward uses its own arena).
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
+  // Per-kernel timing of forward sites.
+  std::string timing_site;
+  bool timing = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+  size_t events_used = 0;
+
+  int fail(int code, const std::string& msg) {
+    err = msg;
+    return code;
+  }
+  int hip_fail(const char* what, hipError_t e) {
+    err = std::string(what) + ": " + hipGetErrorString(e);
+    return ESM_GFX950_HIP_ERROR;
+  }
+  // Returns a device scratch region of at least `bytes` bytes.
+  int get_scratch(size_t bytes, void** out) {
+    if (bytes > scratch_bytes) {
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return hip_fail("hipStreamSynchronize", e);
+      if (scratch) hipFree(scratch);
+      scratch = nullptr;
+      scratch_bytes = 0;
+      const size_t n = align_up(bytes, 1 << 20);
+      e = hipMalloc(&scratch, n);
+      if (e != hipSuccess) return hip_fail("hipMalloc(scratch)", e);
+      scratch_bytes = n;
+    }
+    *out = scratch;
+    return ESM_GFX950_OK;
+  }
+  bool site_timed(const char* site) const {
+    if (!timing) return false;
+    if (timing_site == site) return true;
+    return timing_site == "all_i8_gemm" && std::strcmp(site, "attention") != 0 &&
+           std::strcmp(site, "lm_dense") != 0;
+  }
+  int time_begin(const char* site, int* slot) {
+    *slot = -1;
+    if (!site_timed(site)) return ESM_GFX950_OK;
+    if (events_used == events.size()) {
+      hipEvent_t a, b;
+      if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
+        return fail(ESM_GFX950_HIP_ERROR, "hipEventCreate failed");
+      events.emplace_back(a, b);
+    }
+    *slot = static_cast<int>(events_used++);
+    hipError_t e = hipEventRecord(events[*slot].first, stream);
+    if (e != hipSuccess) return hip_fail("hipEventRecord", e);
+    return ESM_GFX950_OK;
+  }
+  int time_end(int slot) {
+    if (slot < 0) return ESM_GFX950_OK;
+    hipError_t e = hipEventRecord(events[slot].second, stream);
+    if (e != hipSuccess) return hip_fail("hipEventRecord", e);
+    return ESM_GFX950_OK;
+  }
+};
+
+struct esm_gfx950_weight {
+  int N = 0, K = 0, ldk = 0;
+  int8_t* data = nullptr;  // [N, ldk], zero past K
+  float* scales = nullptr;  // [N]
+};
+
+#define ESM_HIP(ctx, expr)                                   \
+  do {                                                       \
+    hipError_t e_ = (expr);                                  \
+    if (e_ != hipSuccess) return (ctx)->hip_fail(#expr, e_); \
+  } while (0)
+
+#define ESM_TRY(expr)                            \
+  do {                                           \
+    int rc_ = (expr);                            \
+    if (rc_ != ESM_GFX950_OK) return rc_;        \
+  } while (0)
+
+#define ESM_REQUIRE(ctx, cond, msg)                                   \
+  do {                                                                \
+    if (!(cond)) return (ctx)->fail(ESM_GFX950_INVALID_ARGUMENT, msg); \
+  } while (0)
+
+namespace {
+
+// BatchView validation (reference src/batch.cpp:8-46), same messages.
+int validate_batch(esm_gfx950_ctx* ctx, const int32_t* cu, int batch_size, long total) {
+  if (batch_size < 1) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "BatchView: batch_size must be >= 1");
+  if (!cu) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "BatchView: cu_seqlens is null");
+  if (cu[0] != 0) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "BatchView: cu_seqlens[0] must be 0");
+  for (int i = 1; i <= batch_size; ++i)
+    if (cu[i] < cu[i - 1])
+      return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "BatchView: cu_seqlens must be non-decreasing");
+  if (total >= 0 && cu[batch_size] != total)
+    return ctx->fail(ESM_GFX950_INVALID_ARGUMENT,
+                     "BatchView: cu_seqlens.back() (" + std::to_string(cu[batch_size]) +
+                         ") must equal packed_ids.size() (" + std::to_string(total) + ")");
+  return ESM_GFX950_OK;
+}
+
+// Work list for the attention kernels: (sequence, head, query tile), longest
+// sequences first so the long tiles start early and the short ones fill in.
+void build_work(const int32_t* cu, int B, int H, int qtile, std::vector<AttnWork>* out) {
+  std::vector<int> order(B);
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+    return (cu[a + 1] - cu[a]) > (cu[b + 1] - cu[b]);
+  });
+  out->clear();
+  for (int b : order) {
+    const int L = cu[b + 1] - cu[b];
+    for (int q0 = 0; q0 < L; q0 += qtile)
+      for (int h = 0; h < H; ++h) out->push_back(AttnWork{b, h, q0, 0});
+  }
+}
+
+size_t max_work_items(int B, int T, int H, int qtile) {
+  return static_cast<size_t>(H) * (static_cast<size_t>(B) + static_cast<size_t>(T) / qtile + 1);
+}
+
+// Position of every packed token inside its sequence.
+void build_pos(const int32_t* cu, int B, int32_t* pos) {
+  for (int b = 0; b < B; ++b)
+    for (int t = cu[b]; t < cu[b + 1]; ++t) pos[t] = t - cu[b];
+}
+
+// RopeBuildTables (reference src/kernels/rope_tables.cpp:14-29): same float
+// formula evaluated with the host C library.
+void rope_tables(int seq_len, int head_dim, float* cos_t, float* sin_t) {
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    const float exponent = static_cast<float>(2 * i) / static_cast<float>(head_dim);
+    const float inv_freq = std::pow(10000.0f, -exponent);
+    for (int t = 0; t < seq_len; ++t) {
+      const float angle = static_cast<float>(t) * inv_freq;
+      const float c = std::cos(angle);
+      const float s = std::sin(angle);
+      cos_t[t * head_dim + i] = c;
+      cos_t[t * head_dim + i + half] = c;
+      sin_t[t * head_dim + i] = s;
+      sin_t[t * head_dim + i + half] = s;
+    }
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ context
+extern "C" int esm_gfx950_init(int device, esm_gfx950_ctx** out) {
+  if (!out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= device || device < 0)
+    return ESM_GFX950_HIP_ERROR;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ESM_GFX950_HIP_ERROR;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ESM_GFX950_HIP_ERROR;
+  if (hipSetDevice(device) != hipSuccess) return ESM_GFX950_HIP_ERROR;
+  auto* ctx = new esm_gfx950_ctx();
+  ctx->device = device;
+  ctx->arch = prop.gcnArchName;
+  if (hipStreamCreate(&ctx->stream) != hipSuccess || hipEventCreate(&ctx->t0) != hipSuccess ||
+      hipEventCreate(&ctx->t1) != hipSuccess) {
+    delete ctx;
+    return ESM_GFX950_HIP_ERROR;
+  }
+  *out = ctx;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_destroy(esm_gfx950_ctx* ctx) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  if (ctx->scratch) hipFree(ctx->scratch);
+  for (auto& e : ctx->events) {
+    hipEventDestroy(e.first);
+    hipEventDestroy(e.second);
+  }
+  hipEventDestroy(ctx->t0);
+  hipEventDestroy(ctx->t1);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return ESM_GFX950_OK;
+}
+
+extern "C" const char* esm_gfx950_last_error(const esm_gfx950_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : "null context";
+}
+
+extern "C" const char* esm_gfx950_device_arch(const esm_gfx950_ctx* ctx) {
+  return ctx ? ctx->arch.c_str() : "";
+}
+
+extern "C" int esm_gfx950_sync(esm_gfx950_ctx* ctx) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_malloc(esm_gfx950_ctx* ctx, size_t bytes, void** dptr) {
+  if (!ctx || !dptr) return ESM_GFX950_INVALID_ARGUMENT;
+  *dptr = nullptr;
+  if (bytes == 0) bytes = 256;
+  ESM_HIP(ctx, hipMalloc(dptr, bytes));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_free(esm_gfx950_ctx* ctx, void* dptr) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (!dptr) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  ESM_HIP(ctx, hipFree(dptr));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_memcpy_h2d(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (bytes == 0) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_memcpy_d2h(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (bytes == 0) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_memcpy_d2d(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (bytes == 0) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_timer_start(esm_gfx950_ctx* ctx) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, hipEventRecord(ctx->t0, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_timer_stop(esm_gfx950_ctx* ctx, float* elapsed_ms) {
+  if (!ctx || !elapsed_ms) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, hipEventRecord(ctx->t1, ctx->stream));
+  ESM_HIP(ctx, hipEventSynchronize(ctx->t1));
+  ESM_HIP(ctx, hipEventElapsedTime(elapsed_ms, ctx->t0, ctx->t1));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, const char* site, int enable) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->timing = enable != 0 && site != nullptr;
+  ctx->timing_site = site ? site : "";
+  ctx->events_used = 0;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, int* launches, double* total_ms) {
+  if (!ctx || !launches || !total_ms) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  double sum = 0.0;
+  for (size_t i = 0; i < ctx->events_used; ++i) {
+    float ms = 0.f;
+    ESM_HIP(ctx, hipEventElapsedTime(&ms, ctx->events[i].first, ctx->events[i].second));
+    sum += ms;
+  }
+  *launches = static_cast<int>(ctx->events_used);
+  *total_ms = sum;
+  return ESM_GFX950_OK;
+}
+
+// ------------------------------------------------------------------ weights
+extern "C" int esm_gfx950_weight_upload_i8(esm_gfx950_ctx* ctx, const int8_t* packed, const float* scales,
+                                           int N, int K, esm_gfx950_weight** out) {
+  if (!ctx || !out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = nullptr;
+  ESM_REQUIRE(ctx, packed && scales && N > 0 && K > 0, "weight_upload_i8: bad arguments");
+  auto* w = new esm_gfx950_weight();
+  w->N = N;
+  w->K = K;
+  w->ldk = pad16(K);
+  std::vector<int8_t> host(static_cast<size_t>(N) * w->ldk, 0);
+  for (int n = 0; n < N; ++n)
+    std::memcpy(host.data() + static_cast<size_t>(n) * w->ldk, packed + static_cast<size_t>(n) * K, K);
+  hipError_t e = hipMalloc(&w->data, host.size());
+  if (e == hipSuccess) e = hipMalloc(&w->scales, static_cast<size_t>(N) * sizeof(float));
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->data, host.data(), host.size(), hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->scales, scales, static_cast<size_t>(N) * sizeof(float), hipMemcpyHostToDevice,
+                       ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    if (w->data) hipFree(w->data);
+    if (w->scales) hipFree(w->scales);
+    delete w;
+    return ctx->hip_fail("weight_upload_i8", e);
+  }
+  *out = w;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_weight_free(esm_gfx950_ctx* ctx, esm_gfx950_weight* w) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (!w) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  hipFree(w->data);
+  hipFree(w->scales);
+  delete w;
+  return ESM_GFX950_OK;
+}
+
+// ------------------------------------------------------------------ INT8 ops
+extern "C" int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int lda,
+                                      const esm_gfx950_weight* W, int M, int32_t* C) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, A && W && C && M >= 0, "gemm_i8_i32: bad arguments");
+  ESM_REQUIRE(ctx, lda >= W->K && lda % 16 == 0, "gemm_i8_i32: lda must be >= K and a multiple of 16");
+  GemmI8Args p;
+  p.A = A;
+  p.lda = lda;
+  p.W = W->data;
+  p.ldw = W->ldk;
+  p.M = M;
+  p.N = W->N;
+  p.K = W->ldk;
+  p.C_i32 = C;
+  p.ldc = W->N;
+  ESM_HIP(ctx, launch_gemm_i8(p, kEpiI32, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const float* a_scale,
+                                      const esm_gfx950_weight* W, const float* bias, float* C, int M,
+                                      int gelu) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, A && a_scale && W && C && M >= 0, "linear_i8_q: bad arguments");
+  ESM_REQUIRE(ctx, lda >= W->K && lda % 16 == 0, "linear_i8_q: lda must be >= K and a multiple of 16");
+  GemmI8Args p;
+  p.A = A;
+  p.lda = lda;
+  p.W = W->data;
+  p.ldw = W->ldk;
+  p.M = M;
+  p.N = W->N;
+  p.K = W->ldk;
+  p.C_f32 = C;
+  p.ldc = W->N;
+  p.a_scale = a_scale;
+  p.w_scale = W->scales;
+  p.bias = bias;
+  ESM_HIP(ctx, launch_gemm_i8(p, gelu ? kEpiF32Gelu : kEpiF32, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+namespace {
+int quantize_into(esm_gfx950_ctx* ctx, const float* x, int M, int K, int mode, int8_t* q, int ldq,
+                  float* scales, float* absmax_slot) {
+  if (mode == ESM_GFX950_ACT_PER_TOKEN) {
+    ESM_HIP(ctx, launch_quant_rows(x, 0, K, M, K, q, ldq, scales, ctx->stream));
+  } else if (mode == ESM_GFX950_ACT_PER_TENSOR) {
+    ESM_HIP(ctx, launch_fill_f32(absmax_slot, 1, 0.0f, ctx->stream));
+    ESM_HIP(ctx, launch_absmax(x, static_cast<size_t>(M) * K, absmax_slot, ctx->stream));
+    ESM_HIP(ctx, launch_quant_tensor(x, K, M, K, absmax_slot, q, ldq, scales, ctx->stream));
+  } else {
+    return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "unknown activation quantisation mode");
+  }
+  return ESM_GFX950_OK;
+}
+}  // namespace
+
+extern "C" int esm_gfx950_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int K, int mode,
+                                       int8_t* q, int ldq, float* scales) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, x && q && scales && M >= 0 && K > 0 && ldq >= K, "quantize_act: bad arguments");
+  void* s = nullptr;
+  ESM_TRY(ctx->get_scratch(256, &s));
+  return quantize_into(ctx, x, M, K, mode, q, ldq, scales, static_cast<float*>(s));
+}
+
+extern "C" int esm_gfx950_linear_i8(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
+                                    const float* bias, float* C, int M, int N, int K, int act_mode) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M > 0 && N > 0 && C) ESM_HIP(ctx, launch_fill_f32(C, static_cast<size_t>(M) * N, 0.0f, ctx->stream));
+    return ESM_GFX950_OK;
+  }
+  ESM_REQUIRE(ctx, A && W && C, "linear_i8: null pointer");
+  if (W->N != N || W->K != K)
+    return ctx->fail(ESM_GFX950_SHAPE_MISMATCH, "linear_i8: weight shape does not match N, K");
+  const int ldq = W->ldk;
+  const size_t qbytes = align_up(static_cast<size_t>(M) * ldq, 256);
+  const size_t sbytes = align_up(static_cast<size_t>(M) * sizeof(float), 256);
+  void* s = nullptr;
+  ESM_TRY(ctx->get_scratch(qbytes + sbytes + 256, &s));
+  auto* q = static_cast<int8_t*>(s);
+  auto* scales = reinterpret_cast<float*>(static_cast<char*>(s) + qbytes);
+  auto* amax = reinterpret_cast<float*>(static_cast<char*>(s) + qbytes + sbytes);
+  ESM_TRY(quantize_into(ctx, A, M, K, act_mode, q, ldq, scales, amax));
+  return esm_gfx950_linear_i8_q(ctx, q, ldq, scales, W, bias, C, M, 0);
+}
+
+// ------------------------------------------------------------------ fp32 ops
+extern "C" int esm_gfx950_linear_f32(esm_gfx950_ctx* ctx, const float* A, const float* W, const float* bias,
+                                     float* C, int M, int N, int K) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (M <= 0 || N <= 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, A && W && C && K >= 0, "linear_f32: bad arguments");
+  GemmF32Args p;
+  p.A = A;
+  p.lda = K;
+  p.W = W;
+  p.ldw = K;
+  p.bias = bias;
+  p.C = C;
+  p.ldc = N;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  ESM_HIP(ctx, launch_gemm_f32(p, kF32Store, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_layernorm(esm_gfx950_ctx* ctx, const float* x, const float* gamma,
+                                    const float* beta, float eps, float* out, int num_rows, int d) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, (x && gamma && beta && out) || num_rows <= 0, "layernorm: null pointer");
+  ESM_HIP(ctx, launch_layernorm(x, gamma, beta, eps, out, num_rows, d, nullptr, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_gelu(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, launch_gelu(x, out, n, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_residual_add(esm_gfx950_ctx* ctx, float* y, const float* x, size_t n) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, launch_residual_add(y, x, n, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_scale(esm_gfx950_ctx* ctx, float* x, size_t n, float scale) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_HIP(ctx, launch_scale(x, n, scale, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_rope_build_tables(int seq_len, int head_dim, float* cos_out, float* sin_out) {
+  if (seq_len < 0 || head_dim <= 0 || (seq_len > 0 && (!cos_out || !sin_out)))
+    return ESM_GFX950_INVALID_ARGUMENT;
+  rope_tables(seq_len, head_dim, cos_out, sin_out);
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_rope_apply_varlen(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
+                                            const int* cu_seqlens, int batch_size, int num_heads,
+                                            int head_dim) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu_seqlens, batch_size, -1));
+  ESM_REQUIRE(ctx, head_dim > 0 && head_dim % 2 == 0 && num_heads > 0, "rope: bad head shape");
+  const int T = cu_seqlens[batch_size];
+  if (T == 0) return ESM_GFX950_OK;
+  std::vector<int32_t> pos(T);
+  build_pos(cu_seqlens, batch_size, pos.data());
+  void* s = nullptr;
+  ESM_TRY(ctx->get_scratch(static_cast<size_t>(T) * 4, &s));
+  ESM_HIP(ctx, hipMemcpyAsync(s, pos.data(), static_cast<size_t>(T) * 4, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, launch_rope_f32(x, num_heads * head_dim, static_cast<int*>(s), T, num_heads, head_dim, cos, sin,
+                               head_dim, 1.0f, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+namespace {
+// Uploads cu_seqlens and the work list into op scratch (after `reserve`
+// bytes used by the caller) and returns device pointers.
+int stage_attention_meta(esm_gfx950_ctx* ctx, const int* cu, int B, int H, int qtile, size_t reserve,
+                         int** d_cu, AttnWork** d_work, int* nwork) {
+  std::vector<AttnWork> work;
+  build_work(cu, B, H, qtile, &work);
+  const size_t cu_bytes = align_up(static_cast<size_t>(B + 1) * 4, 256);
+  const size_t wbytes = work.size() * sizeof(AttnWork);
+  void* s = nullptr;
+  ESM_TRY(ctx->get_scratch(reserve + cu_bytes + wbytes + 256, &s));
+  char* base = static_cast<char*>(s) + reserve;
+  *d_cu = reinterpret_cast<int*>(base);
+  *d_work = reinterpret_cast<AttnWork*>(base + cu_bytes);
+  ESM_HIP(ctx, hipMemcpyAsync(*d_cu, cu, static_cast<size_t>(B + 1) * 4, hipMemcpyHostToDevice, ctx->stream));
+  if (wbytes)
+    ESM_HIP(ctx, hipMemcpyAsync(*d_work, work.data(), wbytes, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  *nwork = static_cast<int>(work.size());
+  return ESM_GFX950_OK;
+}
+}  // namespace
+
+extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
+                                           const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
+                                           float* out, int precision) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu_seqlens, batch_size, -1));
+  ESM_REQUIRE(ctx, num_heads > 0 && head_dim > 0, "attention_varlen: bad head shape");
+  const int T = cu_seqlens[batch_size];
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, q && k && v && out, "attention_varlen: null pointer");
+  const int ld = num_heads * head_dim;
+  if (precision == ESM_GFX950_ATTN_FP32) {
+    ESM_REQUIRE(ctx, head_dim <= 128, "attention_varlen: fp32 path supports head_dim <= 128");
+    int* d_cu;
+    AttnWork* d_work;
+    int nwork;
+    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnF32QTile, 0, &d_cu, &d_work, &nwork));
+    ESM_HIP(ctx, launch_attention_f32(q, k, v, ld, head_dim, d_cu, d_work, nwork, out, ld, ctx->stream));
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ESM_GFX950_OK;
+  }
+  if (precision != ESM_GFX950_ATTN_BF16_MFMA)
+    return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "attention_varlen: unknown precision");
+  ESM_REQUIRE(ctx, head_dim == kHeadDimMfma, "attention_varlen: the MFMA path needs head_dim == 64");
+  const size_t n = static_cast<size_t>(T) * ld;
+  const size_t cbytes = align_up(n * 2, 256);
+  int* d_cu;
+  AttnWork* d_work;
+  int nwork;
+  ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 3 * cbytes, &d_cu, &d_work,
+                               &nwork));
+  char* base = static_cast<char*>(ctx->scratch);
+  auto* qb = reinterpret_cast<uint16_t*>(base);
+  auto* kb = reinterpret_cast<uint16_t*>(base + cbytes);
+  auto* vb = reinterpret_cast<uint16_t*>(base + 2 * cbytes);
+  ESM_HIP(ctx, launch_cast_f32(q, n, qb, 1, ctx->stream));
+  ESM_HIP(ctx, launch_cast_f32(k, n, kb, 1, ctx->stream));
+  ESM_HIP(ctx, launch_cast_f32(v, n, vb, 0, ctx->stream));
+  ESM_HIP(ctx, launch_attention_mfma(qb, kb, vb, 0, ld, d_cu, d_work, nwork, out, ld, nullptr, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint16_t* q, const uint16_t* k,
+                                                const uint16_t* v, int v_is_fp16, const int* cu_seqlens,
+                                                int batch_size, int num_heads, float* out) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu_seqlens, batch_size, -1));
+  ESM_REQUIRE(ctx, num_heads > 0, "attention_varlen_bf16: bad head count");
+  const int T = cu_seqlens[batch_size];
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, q && k && v && out, "attention_varlen_bf16: null pointer");
+  int* d_cu;
+  AttnWork* d_work;
+  int nwork;
+  ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork));
+  const int ld = num_heads * kHeadDimMfma;
+  int slot;
+  ESM_TRY(ctx->time_begin("attention", &slot));
+  ESM_HIP(ctx, launch_attention_mfma(q, k, v, v_is_fp16 ? 0 : 1, ld, d_cu, d_work, nwork, out, ld, nullptr,
+                                     ctx->stream));
+  ESM_TRY(ctx->time_end(slot));
+  return ESM_GFX950_OK;
+}
+
+// -------------------------------------------------------------------- model
+namespace {
+
+struct DevLinear {
+  // int8 weights
+  int8_t* w8 = nullptr;
+  float* ws = nullptr;
+  // fp32 weights
+  float* w32 = nullptr;
+  float* bias = nullptr;
+  int N = 0, K = 0, ldk = 0;
+};
+
+struct DevLayer {
+  float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+  DevLinear qkv, out, fc1, fc2;
+};
+
+}  // namespace
+
+struct esm_gfx950_model {
+  esm_gfx950_model_config cfg{};
+  std::vector<void*> allocations;  // every weight allocation
+  float* embed = nullptr;
+  std::vector<DevLayer> layers;
+  float *final_ln_w = nullptr, *final_ln_b = nullptr;
+  float *lm_dense_w = nullptr, *lm_dense_b = nullptr;
+  float *lm_ln_w = nullptr, *lm_ln_b = nullptr;
+  float* dec_bias = nullptr;
+  // Arena (grown when T exceeds every earlier batch).
+  void* arena = nullptr;
+  size_t arena_bytes = 0;
+  int cap_T = 0, cap_B = 0, cap_L = 0;
+  // Pinned host staging for per-batch metadata.
+  void* meta_host = nullptr;
+  void* meta_dev = nullptr;
+  size_t meta_bytes = 0;
+  hipEvent_t meta_done = nullptr;
+  int rope_len = 0;  // rows currently in the device rope tables
+};
+
+namespace {
+
+int upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const void* src, size_t bytes, void** dst) {
+  *dst = nullptr;
+  if (!src) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "model_create: null weight pointer");
+  ESM_HIP(ctx, hipMalloc(dst, bytes));
+  m->allocations.push_back(*dst);
+  ESM_HIP(ctx, hipMemcpyAsync(*dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+template <typename T>
+int upload_f(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const T* src, size_t n, T** dst) {
+  void* p = nullptr;
+  int rc = upload(ctx, m, src, n * sizeof(T), &p);
+  *dst = static_cast<T*>(p);
+  return rc;
+}
+
+// Concatenates the given linears along N into one device weight.
+int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_linear_desc* const* parts,
+                  int nparts, int N_each, int K, bool int8, DevLinear* out) {
+  const int N = N_each * nparts;
+  out->N = N;
+  out->K = K;
+  out->ldk = int8 ? pad16(K) : K;
+  std::vector<float> bias(static_cast<size_t>(N));
+  for (int p = 0; p < nparts; ++p) {
+    if (!parts[p]->bias) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "model_create: null bias");
+    std::memcpy(bias.data() + static_cast<size_t>(p) * N_each, parts[p]->bias, N_each * sizeof(float));
+  }
+  ESM_TRY(upload_f(ctx, m, bias.data(), bias.size(), &out->bias));
+  if (int8) {
+    std::vector<int8_t> w(static_cast<size_t>(N) * out->ldk, 0);
+    std::vector<float> s(static_cast<size_t>(N));
+    for (int p = 0; p < nparts; ++p) {
+      if (!parts[p]->w_i8 || !parts[p]->w_scale)
+        return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "model_create: null int8 weight");
+      for (int n = 0; n < N_each; ++n)
+        std::memcpy(w.data() + static_cast<size_t>(p * N_each + n) * out->ldk,
+                    parts[p]->w_i8 + static_cast<size_t>(n) * K, K);
+      std::memcpy(s.data() + static_cast<size_t>(p) * N_each, parts[p]->w_scale, N_each * sizeof(float));
+    }
+    ESM_TRY(upload_f(ctx, m, w.data(), w.size(), &out->w8));
+    ESM_TRY(upload_f(ctx, m, s.data(), s.size(), &out->ws));
+  } else {
+    std::vector<float> w(static_cast<size_t>(N) * K);
+    for (int p = 0; p < nparts; ++p) {
+      if (!parts[p]->w_f32) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "model_create: null fp32 weight");
+      std::memcpy(w.data() + static_cast<size_t>(p) * N_each * K, parts[p]->w_f32,
+                  static_cast<size_t>(N_each) * K * sizeof(float));
+    }
+    ESM_TRY(upload_f(ctx, m, w.data(), w.size(), &out->w32));
+  }
+  return ESM_GFX950_OK;
+}
+
+void free_model(esm_gfx950_model* m) {
+  for (void* p : m->allocations) hipFree(p);
+  if (m->arena) hipFree(m->arena);
+  if (m->meta_dev) hipFree(m->meta_dev);
+  if (m->meta_host) hipHostFree(m->meta_host);
+  if (m->meta_done) hipEventDestroy(m->meta_done);
+  delete m;
+}
+
+}  // namespace
+
+extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_model_desc* desc,
+                                       esm_gfx950_model** out) {
+  if (!ctx || !desc || !out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = nullptr;
+  const auto& c = desc->cfg;
+  ESM_REQUIRE(ctx, c.num_layers >= 0 && c.hidden_size > 0 && c.num_heads > 0 && c.head_dim > 0 &&
+                       c.num_heads * c.head_dim == c.hidden_size && c.intermediate_size > 0 && c.vocab_size > 0,
+              "model_create: inconsistent config");
+  ESM_REQUIRE(ctx, c.head_dim % 2 == 0 && c.head_dim <= 128, "model_create: head_dim must be even and <= 128");
+  ESM_REQUIRE(ctx, c.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR || c.act_quant_mode == ESM_GFX950_ACT_PER_TOKEN,
+              "model_create: unknown act_quant_mode");
+  if (c.weights_int8) {
+    ESM_REQUIRE(ctx, c.hidden_size % 16 == 0 && c.intermediate_size % 16 == 0,
+                "model_create: W8A8 needs hidden and intermediate sizes divisible by 16");
+    ESM_REQUIRE(ctx, c.attention_fp32 || c.head_dim == kHeadDimMfma,
+                "model_create: MFMA attention needs head_dim 64 (set attention_fp32)");
+    ESM_REQUIRE(ctx, c.hidden_size % 4 == 0 && c.hidden_size <= 2560,
+                "model_create: fused LayerNorm+quant supports hidden_size % 4 == 0 and <= 2560");
+  }
+  ESM_REQUIRE(ctx, desc->layers || c.num_layers == 0, "model_create: null layers");
+  auto* m = new esm_gfx950_model();
+  m->cfg = c;
+  const int d = c.hidden_size, f = c.intermediate_size, V = c.vocab_size;
+  const bool i8 = c.weights_int8 != 0;
+  int rc = ESM_GFX950_OK;
+  auto step = [&](int r) {
+    if (rc == ESM_GFX950_OK) rc = r;
+    return rc == ESM_GFX950_OK;
+  };
+  step(upload_f(ctx, m, desc->embed, static_cast<size_t>(V) * d, &m->embed));
+  m->layers.resize(c.num_layers);
+  for (int i = 0; i < c.num_layers && rc == ESM_GFX950_OK; ++i) {
+    const auto& L = desc->layers[i];
+    DevLayer& D = m->layers[i];
+    step(upload_f(ctx, m, L.attn_ln_w, d, &D.ln1_w));
+    step(upload_f(ctx, m, L.attn_ln_b, d, &D.ln1_b));
+    step(upload_f(ctx, m, L.ffn_ln_w, d, &D.ln2_w));
+    step(upload_f(ctx, m, L.ffn_ln_b, d, &D.ln2_b));
+    const esm_gfx950_linear_desc* qkv[3] = {&L.q, &L.k, &L.v};
+    const esm_gfx950_linear_desc* o1[1] = {&L.out};
+    const esm_gfx950_linear_desc* f1[1] = {&L.fc1};
+    const esm_gfx950_linear_desc* f2[1] = {&L.fc2};
+    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, qkv, 3, d, d, i8, &D.qkv));
+    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, o1, 1, d, d, i8, &D.out));
+    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, f1, 1, f, d, i8, &D.fc1));
+    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, f2, 1, d, f, i8, &D.fc2));
+  }
+  step(upload_f(ctx, m, desc->final_ln_w, d, &m->final_ln_w));
+  step(upload_f(ctx, m, desc->final_ln_b, d, &m->final_ln_b));
+  step(upload_f(ctx, m, desc->lm_dense_w, static_cast<size_t>(d) * d, &m->lm_dense_w));
+  step(upload_f(ctx, m, desc->lm_dense_b, d, &m->lm_dense_b));
+  step(upload_f(ctx, m, desc->lm_ln_w, d, &m->lm_ln_w));
+  step(upload_f(ctx, m, desc->lm_ln_b, d, &m->lm_ln_b));
+  step(upload_f(ctx, m, desc->lm_decoder_bias, V, &m->dec_bias));
+  if (rc == ESM_GFX950_OK && hipEventCreateWithFlags(&m->meta_done, hipEventDisableTiming) != hipSuccess)
+    rc = ctx->fail(ESM_GFX950_HIP_ERROR, "hipEventCreate failed");
+  if (rc != ESM_GFX950_OK) {
+    hipStreamSynchronize(ctx->stream);
+    free_model(m);
+    return rc;
+  }
+  *out = m;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (!model) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  free_model(model);
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int act_mode) {
+  if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, act_mode == ESM_GFX950_ACT_PER_TENSOR || act_mode == ESM_GFX950_ACT_PER_TOKEN,
+              "model_set_act_mode: unknown mode");
+  model->cfg.act_quant_mode = act_mode;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes) {
+  if (!model || !bytes) return ESM_GFX950_INVALID_ARGUMENT;
+  *bytes = model->arena_bytes + model->meta_bytes;
+  return ESM_GFX950_OK;
+}
+
+namespace {
+
+// Arena layout for T tokens (every region 256-byte aligned).
+struct Arena {
+  float* hidden;     // [T, d]
+  float* ln;         // [T, d]   fp32 LN output / final LN
+  int8_t* xq;        // [T, max(d, ffn) padded]
+  float* xs;         // [T] activation scales
+  uint16_t* qb;      // [T, d] bf16 Q
+  uint16_t* kb;      // [T, d] bf16 K
+  uint16_t* vb;      // [T, d] fp16 V
+  float* qkv;        // [T, 3d] fp32 (fp32 paths)
+  float* attn;       // [T, d]
+  float* inter;      // [T, ffn]
+  float* lm_a;       // [T, d]
+  float* logits;     // [T, V]
+  float* absmax;     // scratch scalars
+  size_t bytes;
+};
+
+Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
+  const size_t d = c.hidden_size, f = c.intermediate_size, V = c.vocab_size;
+  const size_t Ts = static_cast<size_t>(T);
+  const size_t wq = std::max<size_t>(pad16(c.hidden_size), pad16(c.intermediate_size));
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes, 256);
+    return p;
+  };
+  Arena a;
+  a.hidden = reinterpret_cast<float*>(take(Ts * d * 4));
+  a.ln = reinterpret_cast<float*>(take(Ts * d * 4));
+  a.xq = reinterpret_cast<int8_t*>(take(Ts * wq));
+  a.xs = reinterpret_cast<float*>(take(Ts * 4));
+  a.qb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
+  a.kb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
+  a.vb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
+  const bool need_qkv_f32 = !c.weights_int8 || c.attention_fp32;
+  a.qkv = reinterpret_cast<float*>(take(need_qkv_f32 ? Ts * 3 * d * 4 : 0));
+  a.attn = reinterpret_cast<float*>(take(Ts * d * 4));
+  a.inter = reinterpret_cast<float*>(take(Ts * f * 4));
+  a.lm_a = reinterpret_cast<float*>(take(Ts * d * 4));
+  a.logits = reinterpret_cast<float*>(take(Ts * V * 4));
+  a.absmax = reinterpret_cast<float*>(take(256));
+  a.bytes = off;
+  return a;
+}
+
+struct Meta {
+  int32_t* ids;
+  float* tok_scale;
+  int32_t* pos;
+  int32_t* cu;
+  AttnWork* work;
+  float* cos_t;
+  float* sin_t;
+  size_t bytes;
+};
+
+Meta meta_layout(int T, int B, int maxL, int H, int dh, char* base) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* p = base ? base + off : nullptr;
+    off += align_up(bytes, 256);
+    return p;
+  };
+  Meta m;
+  m.ids = reinterpret_cast<int32_t*>(take(static_cast<size_t>(T) * 4));
+  m.tok_scale = reinterpret_cast<float*>(take(static_cast<size_t>(T) * 4));
+  m.pos = reinterpret_cast<int32_t*>(take(static_cast<size_t>(T) * 4));
+  m.cu = reinterpret_cast<int32_t*>(take(static_cast<size_t>(B + 1) * 4));
+  const size_t nw = std::max(max_work_items(B, T, H, kAttnMfmaQTile), max_work_items(B, T, H, kAttnF32QTile));
+  m.work = reinterpret_cast<AttnWork*>(take(nw * sizeof(AttnWork)));
+  m.cos_t = reinterpret_cast<float*>(take(static_cast<size_t>(maxL) * dh * 4));
+  m.sin_t = reinterpret_cast<float*>(take(static_cast<size_t>(maxL) * dh * 4));
+  m.bytes = off;
+  return m;
+}
+
+template <typename P>
+P shift(P p, const char* from, const char* to) {
+  return reinterpret_cast<P>(const_cast<char*>(to) + (reinterpret_cast<const char*>(p) - from));
+}
+
+// One pre-LN encoder layer on the device (reference TransformerBlock,
+// src/model.cpp:932-1066): LN -> QKV -> Q-scale -> RoPE -> attention ->
+// out-proj -> residual -> LN -> fc1 -> GELU -> fc2 -> residual.
+int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, const Arena& a, const Meta& md,
+               int T, int nwork) {
+  const auto& c = m->cfg;
+  const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
+  const int ldq_d = pad16(d), ldq_f = pad16(f);
+  const bool tok = c.act_quant_mode == ESM_GFX950_ACT_PER_TOKEN;
+  hipStream_t s = ctx->stream;
+  const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
+  int slot;
+
+  // attn LN + activation quant
+  if (tok) {
+    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d, a.xs, s));
+  } else {
+    ESM_HIP(ctx, launch_fill_f32(a.absmax, 1, 0.0f, s));
+    ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
+    ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax, a.xq, ldq_d, a.xs, s));
+  }
+
+  // QKV projection (one GEMM over the concatenated [3d, d] weight)
+  GemmI8Args g;
+  g.A = a.xq;
+  g.lda = ldq_d;
+  g.W = L.qkv.w8;
+  g.ldw = L.qkv.ldk;
+  g.M = T;
+  g.N = 3 * d;
+  g.K = L.qkv.ldk;
+  g.a_scale = a.xs;
+  g.w_scale = L.qkv.ws;
+  g.bias = L.qkv.bias;
+  ESM_TRY(ctx->time_begin("qkv", &slot));
+  if (c.attention_fp32) {
+    g.C_f32 = a.qkv;
+    g.ldc = 3 * d;
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+  } else {
+    g.q_out = a.qb;
+    g.k_out = a.kb;
+    g.v_out = a.vb;
+    g.d_model = d;
+    g.pos = md.pos;
+    g.rope_cos = md.cos_t;
+    g.rope_sin = md.sin_t;
+    g.q_scale = q_scale;
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvRope, s));
+  }
+  ESM_TRY(ctx->time_end(slot));
+
+  // attention
+  float* amax_attn = tok ? nullptr : a.absmax + 1;
+  if (!tok) ESM_HIP(ctx, launch_fill_f32(a.absmax + 1, 1, 0.0f, s));
+  ESM_TRY(ctx->time_begin("attention", &slot));
+  if (c.attention_fp32) {
+    ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+    ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+    ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d,
+                                      s));
+    if (!tok) ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
+  } else {
+    ESM_HIP(ctx, launch_attention_mfma(a.qb, a.kb, a.vb, 0, d, md.cu, md.work, nwork, a.attn, d, amax_attn, s));
+  }
+  ESM_TRY(ctx->time_end(slot));
+  if (tok) {
+    ESM_HIP(ctx, launch_quant_rows(a.attn, 0, d, T, d, a.xq, ldq_d, a.xs, s));
+  } else {
+    ESM_HIP(ctx, launch_quant_tensor(a.attn, d, T, d, amax_attn, a.xq, ldq_d, a.xs, s));
+  }
+
+  // out-proj + residual
+  g = GemmI8Args();
+  g.A = a.xq;
+  g.lda = ldq_d;
+  g.W = L.out.w8;
+  g.ldw = L.out.ldk;
+  g.M = T;
+  g.N = d;
+  g.K = L.out.ldk;
+  g.a_scale = a.xs;
+  g.w_scale = L.out.ws;
+  g.bias = L.out.bias;
+  g.C_f32 = a.hidden;
+  g.ldc = d;
+  ESM_TRY(ctx->time_begin("out", &slot));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
+  ESM_TRY(ctx->time_end(slot));
+
+  // ffn LN + quant
+  if (tok) {
+    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d, a.xs, s));
+  } else {
+    ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
+    ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2, s));
+    ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax + 2, a.xq, ldq_d, a.xs, s));
+  }
+
+  // fc1 + GELU
+  g = GemmI8Args();
+  g.A = a.xq;
+  g.lda = ldq_d;
+  g.W = L.fc1.w8;
+  g.ldw = L.fc1.ldk;
+  g.M = T;
+  g.N = f;
+  g.K = L.fc1.ldk;
+  g.a_scale = a.xs;
+  g.w_scale = L.fc1.ws;
+  g.bias = L.fc1.bias;
+  g.C_f32 = a.inter;
+  g.ldc = f;
+  if (!tok) {
+    ESM_HIP(ctx, launch_fill_f32(a.absmax + 3, 1, 0.0f, s));
+    g.tensor_absmax = a.absmax + 3;
+  }
+  ESM_TRY(ctx->time_begin("fc1", &slot));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Gelu, s));
+  ESM_TRY(ctx->time_end(slot));
+  if (tok) {
+    ESM_HIP(ctx, launch_quant_rows(a.inter, 0, f, T, f, a.xq, ldq_f, a.xs, s));
+  } else {
+    ESM_HIP(ctx, launch_quant_tensor(a.inter, f, T, f, a.absmax + 3, a.xq, ldq_f, a.xs, s));
+  }
+
+  // fc2 + residual
+  g = GemmI8Args();
+  g.A = a.xq;
+  g.lda = ldq_f;
+  g.W = L.fc2.w8;
+  g.ldw = L.fc2.ldk;
+  g.M = T;
+  g.N = d;
+  g.K = L.fc2.ldk;
+  g.a_scale = a.xs;
+  g.w_scale = L.fc2.ws;
+  g.bias = L.fc2.bias;
+  g.C_f32 = a.hidden;
+  g.ldc = d;
+  ESM_TRY(ctx->time_begin("fc2", &slot));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
+  ESM_TRY(ctx->time_end(slot));
+  return ESM_GFX950_OK;
+}
+
+int f32_linear(esm_gfx950_ctx* ctx, const float* A, const DevLinear& W, float* C, int M, int epi) {
+  GemmF32Args p;
+  p.A = A;
+  p.lda = W.K;
+  p.W = W.w32;
+  p.ldw = W.K;
+  p.bias = W.bias;
+  p.C = C;
+  p.ldc = W.N;
+  p.M = M;
+  p.N = W.N;
+  p.K = W.K;
+  ESM_HIP(ctx, launch_gemm_f32(p, epi, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, const Arena& a, const Meta& md,
+              int T, int nwork) {
+  const auto& c = m->cfg;
+  const int d = c.hidden_size, H = c.num_heads, dh = c.head_dim;
+  hipStream_t s = ctx->stream;
+  const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
+  ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  ESM_TRY(f32_linear(ctx, a.ln, L.qkv, a.qkv, T, kF32Store));
+  ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+  ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+  ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d, s));
+  ESM_TRY(f32_linear(ctx, a.attn, L.out, a.hidden, T, kF32Resid));
+  ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  ESM_TRY(f32_linear(ctx, a.ln, L.fc1, a.inter, T, kF32Gelu));
+  ESM_TRY(f32_linear(ctx, a.inter, L.fc2, a.hidden, T, kF32Resid));
+  return ESM_GFX950_OK;
+}
+
+constexpr float kTokenDropoutMaskRatioTrain = 0.15f * 0.8f;
+
+}  // namespace
+
+extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                         const int32_t* cu, int B, int T, float* logits, int logits_on_device) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu, B, T));
+  const auto& c = m->cfg;
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, ids && logits, "forward_packed: null ids or logits");
+  const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
+  for (int t = 0; t < T; ++t)
+    if (ids[t] < 0 || ids[t] >= V)
+      return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_packed: token id out of range at " + std::to_string(t));
+  int maxL = 0;
+  for (int b = 0; b < B; ++b) maxL = std::max(maxL, cu[b + 1] - cu[b]);
+
+  // Grow the arena and metadata buffers only when this batch exceeds them.
+  if (T > m->cap_T || B > m->cap_B || maxL > m->cap_L) {
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const int nT = std::max(T, m->cap_T), nB = std::max(B, m->cap_B), nL = std::max(maxL, m->cap_L);
+    if (m->arena) hipFree(m->arena);
+    if (m->meta_dev) hipFree(m->meta_dev);
+    if (m->meta_host) hipHostFree(m->meta_host);
+    m->arena = m->meta_dev = m->meta_host = nullptr;
+    m->arena_bytes = m->meta_bytes = 0;
+    m->cap_T = m->cap_B = m->cap_L = 0;
+    const Arena probe = layout(c, nT, nullptr);
+    const Meta mprobe = meta_layout(nT, nB, nL, H, dh, nullptr);
+    ESM_HIP(ctx, hipMalloc(&m->arena, probe.bytes));
+    m->arena_bytes = probe.bytes;
+    ESM_HIP(ctx, hipMalloc(&m->meta_dev, mprobe.bytes));
+    ESM_HIP(ctx, hipHostMalloc(&m->meta_host, mprobe.bytes, hipHostMallocDefault));
+    m->meta_bytes = mprobe.bytes;
+    m->cap_T = nT;
+    m->cap_B = nB;
+    m->cap_L = nL;
+    m->rope_len = 0;
+  }
+  const Arena a = layout(c, m->cap_T, static_cast<char*>(m->arena));
+  const Meta mh = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_host));
+  const Meta md = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_dev));
+
+  // Host metadata: ids, per-token embedding scale (Embed, model.cpp:737-778),
+  // positions, cu_seqlens, attention work list, rope tables.
+  ESM_HIP(ctx, hipEventSynchronize(m->meta_done));
+  std::memcpy(mh.ids, ids, static_cast<size_t>(T) * 4);
+  for (int b = 0; b < B; ++b) {
+    int src_len = 0, masks = 0;
+    for (int t = cu[b]; t < cu[b + 1]; ++t) {
+      ++src_len;
+      if (ids[t] == c.mask_token_id) ++masks;
+    }
+    const float ratio = src_len > 0 ? static_cast<float>(masks) / static_cast<float>(src_len) : 0.0f;
+    const float scale = (1.0f - kTokenDropoutMaskRatioTrain) / std::max(1.0f - ratio, 1e-12f);
+    for (int t = cu[b]; t < cu[b + 1]; ++t) mh.tok_scale[t] = scale;
+  }
+  build_pos(cu, B, mh.pos);
+  std::memcpy(mh.cu, cu, static_cast<size_t>(B + 1) * 4);
+  const bool mfma_attn = c.weights_int8 && !c.attention_fp32;
+  std::vector<AttnWork> work;
+  build_work(cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
+  std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));
+  const bool new_tables = m->rope_len < maxL;
+  if (new_tables) rope_tables(m->cap_L, dh, mh.cos_t, mh.sin_t);
+  const size_t upto = reinterpret_cast<const char*>(mh.cos_t) - static_cast<const char*>(m->meta_host);
+  ESM_HIP(ctx, hipMemcpyAsync(m->meta_dev, m->meta_host, new_tables ? m->meta_bytes : upto, hipMemcpyHostToDevice,
+                              ctx->stream));
+  ESM_HIP(ctx, hipEventRecord(m->meta_done, ctx->stream));
+  if (new_tables) m->rope_len = m->cap_L;
+  const int nwork = static_cast<int>(work.size());
+
+  hipStream_t s = ctx->stream;
+  ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
+  for (const DevLayer& L : m->layers) {
+    if (c.weights_int8) {
+      ESM_TRY(layer_int8(ctx, m, L, a, md, T, nwork));
+    } else {
+      ESM_TRY(layer_f32(ctx, m, L, a, md, T, nwork));
+    }
+  }
+  // Final LN and lm head: dense -> GELU -> LN -> tied decoder + bias
+  // (reference src/model.cpp:1181-1239).
+  ESM_HIP(ctx, launch_layernorm(a.hidden, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  DevLinear dense;
+  dense.w32 = m->lm_dense_w;
+  dense.bias = m->lm_dense_b;
+  dense.N = d;
+  dense.K = d;
+  int slot;
+  ESM_TRY(ctx->time_begin("lm_dense", &slot));
+  ESM_TRY(f32_linear(ctx, a.ln, dense, a.lm_a, T, kF32Gelu));
+  ESM_TRY(ctx->time_end(slot));
+  ESM_HIP(ctx, launch_layernorm(a.lm_a, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr, s));
+  DevLinear dec;
+  dec.w32 = m->embed;
+  dec.bias = m->dec_bias;
+  dec.N = V;
+  dec.K = d;
+  float* dst = logits_on_device ? logits : a.logits;
+  ESM_TRY(f32_linear(ctx, a.attn, dec, dst, T, kF32Store));
+  if (!logits_on_device) {
+    ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * V * 4, hipMemcpyDeviceToHost, s));
+    ESM_HIP(ctx, hipStreamSynchronize(s));
+  }
+  return ESM_GFX950_OK;
+}

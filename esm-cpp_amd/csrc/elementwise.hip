@@ -1,0 +1,416 @@
+// HBM-bound row and elementwise kernels of the packed ESM-2 encoder path:
+// LayerNorm (optionally fused with per-token int8 quantisation), activation
+// quantisation (per token or per tensor), absmax, GELU, residual add, Q
+// scale, rotary embedding, token embedding and dtype casts.
+//
+// Reference counterparts: LayerNormRef src/kernels/layernorm.cpp:23-44,
+// activation quant src/kernels/gemm_int8.cpp:391-508 and
+// src/quant/pack.cpp:119-147, GeluRef src/kernels/gelu.cpp:30-35,
+// ResidualAddInplaceRef / ScaleInplaceRef src/kernels/residual.cpp:23-29,
+// RopeApplyVarlenRef src/kernels/rope.cpp:47-70, Embed src/model.cpp:737-778.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace esm_gfx950 {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wave per row, 4 waves per block
+
+// Activation scale rule of the reference prefix (gemm_int8.cpp:434,476):
+// absmax/127, or 1 when the input is all zero.
+__device__ __forceinline__ float act_scale_from_absmax(float amax) {
+  return amax > 0.0f ? amax / 127.0f : 1.0f;
+}
+
+// ---- LayerNorm with the row cached in registers (d % 4 == 0, d <= NV*256).
+template <int NV, bool QUANT>
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ out,
+    int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
+    float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * d;
+  float4 v[NV];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < d) {
+      v[j] = *reinterpret_cast<const float4*>(xr + c);
+      sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    } else {
+      v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(d);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < d) {
+      const float a = v[j].x - mean, b = v[j].y - mean, e = v[j].z - mean, f = v[j].w - mean;
+      sq += (a * a + b * b) + (e * e + f * f);
+    }
+  }
+  const float var = wave_sum(sq) / static_cast<float>(d);
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < d) {
+      const float4 g = *reinterpret_cast<const float4*>(gamma + c);
+      const float4 b = *reinterpret_cast<const float4*>(beta + c);
+      float4 y;
+      y.x = (v[j].x - mean) * inv_std * g.x + b.x;
+      y.y = (v[j].y - mean) * inv_std * g.y + b.y;
+      y.z = (v[j].z - mean) * inv_std * g.z + b.z;
+      y.w = (v[j].w - mean) * inv_std * g.w + b.w;
+      v[j] = y;
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+      if constexpr (!QUANT) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = y;
+    }
+  }
+  if constexpr (QUANT) {
+    const float scale = act_scale_from_absmax(wave_max(amax));
+    const float inv = 1.0f / scale;
+    int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = (j * 64 + lane) * 4;
+      if (c < d) {
+        const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
+        const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
+        const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
+        const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
+        *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      }
+    }
+    for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
+    if (lane == 0) scales[row] = scale;
+  } else if (tensor_absmax) {
+    amax = wave_max(amax);
+    if (lane == 0) atomic_max_nonneg(tensor_absmax, amax);
+  }
+}
+
+// ---- Generic LayerNorm for any d (three passes over the row in cache).
+__global__ __launch_bounds__(256) void layernorm_any_kernel(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ out,
+    int rows, int d, float* tensor_absmax) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * d;
+  float sum = 0.f;
+  for (int c = lane; c < d; c += 64) sum += xr[c];
+  const float mean = wave_sum(sum) / static_cast<float>(d);
+  float sq = 0.f;
+  for (int c = lane; c < d; c += 64) {
+    const float a = xr[c] - mean;
+    sq += a * a;
+  }
+  const float var = wave_sum(sq) / static_cast<float>(d);
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  float amax = 0.f;
+  float* yr = out + static_cast<size_t>(row) * d;
+  for (int c = lane; c < d; c += 64) {
+    const float y = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+    yr[c] = y;
+    amax = fmaxf(amax, fabsf(y));
+  }
+  if (tensor_absmax) {
+    amax = wave_max(amax);
+    if (lane == 0) atomic_max_nonneg(tensor_absmax, amax);
+  }
+}
+
+template <int KIND>
+__device__ __forceinline__ float load_as_f32(const void* p, size_t i) {
+  if constexpr (KIND == 0) return static_cast<const float*>(p)[i];
+  if constexpr (KIND == 1) return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// ---- Per-row quantisation: one wave per row.
+template <int KIND>
+__global__ __launch_bounds__(256) void quant_rows_kernel(
+    const void* __restrict__ x, int ldx, int rows, int cols,
+    int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const size_t base = static_cast<size_t>(row) * ldx;
+  float amax = 0.f;
+  for (int c = lane; c < cols; c += 64) amax = fmaxf(amax, fabsf(load_as_f32<KIND>(x, base + c)));
+  const float scale = act_scale_from_absmax(wave_max(amax));
+  const float inv = 1.0f / scale;
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+  for (int c = lane; c < cols; c += 64) qr[c] = static_cast<int8_t>(quant_i8(load_as_f32<KIND>(x, base + c), inv));
+  for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
+  if (lane == 0) scales[row] = scale;
+}
+
+// Vectorised fp32 per-row quantisation (cols % 4 == 0, cols <= NV*256).
+template <int NV>
+__global__ __launch_bounds__(256) void quant_rows_vec_kernel(
+    const float* __restrict__ x, int ldx, int rows, int cols,
+    int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * ldx;
+  float4 v[NV];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      v[j] = *reinterpret_cast<const float4*>(xr + c);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+  }
+  const float scale = act_scale_from_absmax(wave_max(amax));
+  const float inv = 1.0f / scale;
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
+      const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
+      const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
+      const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
+      *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+  }
+  for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
+  if (lane == 0) scales[row] = scale;
+}
+
+// ---- Per-tensor quantisation with a device-resident absmax.
+__global__ __launch_bounds__(256) void quant_tensor_kernel(
+    const float* __restrict__ x, int ldx, int rows, int cols,
+    const float* __restrict__ absmax, int8_t* __restrict__ q, int ldq,
+    float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float scale = act_scale_from_absmax(*absmax);
+  const float inv = 1.0f / scale;
+  const float* xr = x + static_cast<size_t>(row) * ldx;
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+  for (int c = lane; c < cols; c += 64) qr[c] = static_cast<int8_t>(quant_i8(xr[c], inv));
+  for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
+  if (lane == 0) scales[row] = scale;
+}
+
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x,
+                                                     size_t n, float* absmax) {
+  float m = 0.f;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    m = fmaxf(m, fabsf(x[i]));
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) atomic_max_nonneg(absmax, m);
+}
+
+__global__ void fill_kernel(float* x, size_t n, float v) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    x[i] = v;
+}
+
+__global__ void gelu_kernel(const float* __restrict__ x, float* __restrict__ out, size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[i] = gelu_erf(x[i]);
+}
+
+__global__ void residual_kernel(float* __restrict__ y, const float* __restrict__ x, size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    y[i] += x[i];
+}
+
+__global__ void scale_kernel(float* __restrict__ x, size_t n, float s) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    x[i] *= s;
+}
+
+// One thread per (token, head, i < head_dim/2) rotary pair.
+__global__ void rope_f32_kernel(float* __restrict__ x, int ld, const int* __restrict__ pos,
+                                int T, int heads, int dh, const float* __restrict__ cos_tab,
+                                const float* __restrict__ sin_tab, int tab_ld, float pre_scale) {
+  const int half = dh / 2;
+  const size_t total = static_cast<size_t>(T) * heads * half;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int c = static_cast<int>(i % half);
+    const size_t th = i / half;
+    const int h = static_cast<int>(th % heads);
+    const int t = static_cast<int>(th / heads);
+    const int p = pos[t];
+    float* xr = x + static_cast<size_t>(t) * ld + static_cast<size_t>(h) * dh;
+    const float* cr = cos_tab + static_cast<size_t>(p) * tab_ld;
+    const float* sr = sin_tab + static_cast<size_t>(p) * tab_ld;
+    const float x1 = xr[c] * pre_scale, x2 = xr[c + half] * pre_scale;
+    xr[c] = x1 * cr[c] - x2 * sr[c];
+    xr[c + half] = x2 * cr[c + half] + x1 * sr[c + half];
+  }
+}
+
+__global__ void embed_kernel(const int* __restrict__ ids, const float* __restrict__ tok_scale,
+                             const float* __restrict__ embed, int T, int d, int mask_id,
+                             float* __restrict__ out) {
+  const size_t total = static_cast<size_t>(T) * d;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const int t = static_cast<int>(i / d);
+    const int c = static_cast<int>(i % d);
+    const int id = ids[t];
+    const float s = tok_scale[t];
+    out[i] = (id == mask_id || s == 0.0f) ? 0.0f : embed[static_cast<size_t>(id) * d + c] * s;
+  }
+}
+
+__global__ void cast_kernel(const float* __restrict__ x, size_t n, uint16_t* __restrict__ out,
+                            int to_bf16) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[i] = to_bf16 ? f32_to_bf16_bits(x[i]) : f32_to_f16_bits(x[i]);
+}
+
+inline dim3 grid_for(size_t n, int block = 256) {
+  size_t g = (n + block - 1) / block;
+  if (g > 65536) g = 65536;
+  if (g == 0) g = 1;
+  return dim3(static_cast<unsigned>(g));
+}
+
+inline dim3 rows_grid(int rows) { return dim3((rows + kRowsPerBlock - 1) / kRowsPerBlock); }
+
+}  // namespace
+
+hipError_t launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
+                            float* out, int rows, int d, float* tensor_absmax, hipStream_t s) {
+  if (rows <= 0 || d <= 0) return hipSuccess;
+  const dim3 g = rows_grid(rows), b(256);
+  if (d % 4 == 0 && d <= 1280) {
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, false>), g, b, 0, s, x, gamma, beta, eps, out, rows, d,
+                       tensor_absmax, nullptr, 0, nullptr);
+  } else if (d % 4 == 0 && d <= 2560) {
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, false>), g, b, 0, s, x, gamma, beta, eps, out, rows, d,
+                       tensor_absmax, nullptr, 0, nullptr);
+  } else {
+    hipLaunchKernelGGL(layernorm_any_kernel, g, b, 0, s, x, gamma, beta, eps, out, rows, d, tensor_absmax);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_layernorm_quant(const float* x, const float* gamma, const float* beta, float eps,
+                                  int rows, int d, int8_t* q, int ldq, float* scales, hipStream_t s) {
+  if (rows <= 0 || d <= 0) return hipSuccess;
+  if (d % 4 != 0 || d > 2560) return hipErrorInvalidValue;
+  const dim3 g = rows_grid(rows), b(256);
+  if (d <= 1280) {
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, true>), g, b, 0, s, x, gamma, beta, eps, nullptr, rows, d,
+                       nullptr, q, ldq, scales);
+  } else {
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, gamma, beta, eps, nullptr, rows, d,
+                       nullptr, q, ldq, scales);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const void* x, int src_kind, int ldx, int rows, int cols, int8_t* q,
+                             int ldq, float* scales, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  const dim3 g = rows_grid(rows), b(256);
+  if (src_kind == 0 && cols % 4 == 0 && ldx % 4 == 0 && cols <= 1280) {
+    hipLaunchKernelGGL(quant_rows_vec_kernel<5>, g, b, 0, s, static_cast<const float*>(x), ldx, rows, cols, q,
+                       ldq, scales);
+  } else if (src_kind == 0 && cols % 4 == 0 && ldx % 4 == 0 && cols <= 5120) {
+    hipLaunchKernelGGL(quant_rows_vec_kernel<20>, g, b, 0, s, static_cast<const float*>(x), ldx, rows, cols, q,
+                       ldq, scales);
+  } else if (src_kind == 0) {
+    hipLaunchKernelGGL(quant_rows_kernel<0>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  } else if (src_kind == 1) {
+    hipLaunchKernelGGL(quant_rows_kernel<1>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  } else {
+    hipLaunchKernelGGL(quant_rows_kernel<2>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols, const float* absmax,
+                               int8_t* q, int ldq, float* scales, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(quant_tensor_kernel, rows_grid(rows), dim3(256), 0, s, x, ldx, rows, cols, absmax, q,
+                     ldq, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  size_t g = (n + 255) / 256;
+  if (g > 4096) g = 4096;
+  hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float* x, size_t n, float v, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_kernel, grid_for(n), dim3(256), 0, s, x, n, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu(const float* x, float* out, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(gelu_kernel, grid_for(n), dim3(256), 0, s, x, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_residual_add(float* y, const float* x, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(residual_kernel, grid_for(n), dim3(256), 0, s, y, x, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_scale(float* x, size_t n, float scale, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(scale_kernel, grid_for(n), dim3(256), 0, s, x, n, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_f32(float* x, int ld, const int* pos, int T, int heads, int head_dim,
+                           const float* cos_tab, const float* sin_tab, int tab_ld, float pre_scale,
+                           hipStream_t s) {
+  const size_t n = static_cast<size_t>(T) * heads * (head_dim / 2);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_f32_kernel, grid_for(n), dim3(256), 0, s, x, ld, pos, T, heads, head_dim, cos_tab,
+                     sin_tab, tab_ld, pre_scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const int* ids, const float* tok_scale, const float* embed, int T, int d,
+                        int mask_token_id, float* out, hipStream_t s) {
+  const size_t n = static_cast<size_t>(T) * d;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(embed_kernel, grid_for(n), dim3(256), 0, s, ids, tok_scale, embed, T, d, mask_token_id,
+                     out);
+  return hipGetLastError();
+}
+
+hipError_t launch_cast_f32(const float* x, size_t n, uint16_t* out, int to_bf16, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(cast_kernel, grid_for(n), dim3(256), 0, s, x, n, out, to_bf16);
+  return hipGetLastError();
+}
+
+}  // namespace esm_gfx950

@@ -1,0 +1,133 @@
+// Kernel launch interface shared by the gfx950 translation units. Every
+// launcher enqueues on the given stream and returns the launch status; no
+// launcher allocates memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace esm_gfx950 {
+
+// ---------------------------------------------------------------- INT8 GEMM
+// C[m, n] = sum_k A[m, k] * W[n, k]  (int8 x int8 -> int32), then one of the
+// epilogues below. A is row-major [M, lda], W row-major [N, ldw]; K must be a
+// multiple of 16 (callers zero-pad rows to that width).
+enum GemmEpilogue : int {
+  kEpiI32 = 0,        // C_i32[m*ldc + n] = acc
+  kEpiF32 = 1,        // C_f32 = fma(acc, a_scale[m]*w_scale[n], bias[n])
+  kEpiF32Gelu = 2,    // C_f32 = gelu(...) (+ optional absmax outputs)
+  kEpiF32Resid = 3,   // C_f32 += fma(...)   (residual add into hidden)
+  kEpiQkvRope = 4,    // split Q|K|V, Q*q_scale, RoPE on Q and K, bf16/fp16 out
+  kEpiF32GeluQ = 5,   // gelu(...) -> fp16 store + per-row absmax (atomic)
+};
+
+struct GemmI8Args {
+  const int8_t* A = nullptr;
+  int lda = 0;
+  const int8_t* W = nullptr;
+  int ldw = 0;
+  int M = 0, N = 0, K = 0;
+  int32_t* C_i32 = nullptr;
+  float* C_f32 = nullptr;
+  uint16_t* C_f16 = nullptr;
+  int ldc = 0;
+  const float* a_scale = nullptr;  // [M]
+  const float* w_scale = nullptr;  // [N]
+  const float* bias = nullptr;     // [N] or null
+  float* row_absmax = nullptr;     // [M] (atomic max of |out|) or null
+  float* tensor_absmax = nullptr;  // scalar (atomic max of |out|) or null
+  // kEpiQkvRope
+  uint16_t* q_out = nullptr;  // bf16 [M, d_model]
+  uint16_t* k_out = nullptr;  // bf16 [M, d_model]
+  uint16_t* v_out = nullptr;  // fp16 [M, d_model]
+  int d_model = 0;
+  const int* pos = nullptr;          // [M] position inside the sequence
+  const float* rope_cos = nullptr;   // [max_len, 32]
+  const float* rope_sin = nullptr;   // [max_len, 32]
+  float q_scale = 1.0f;
+};
+
+hipError_t launch_gemm_i8(const GemmI8Args& p, int epilogue, hipStream_t s);
+
+// ---------------------------------------------------------------- FP32 GEMM
+enum GemmF32Epilogue : int {
+  kF32Store = 0,   // C = A W^T + bias
+  kF32Gelu = 1,    // C = gelu(A W^T + bias)
+  kF32Resid = 2,   // C += A W^T + bias
+};
+struct GemmF32Args {
+  const float* A = nullptr;
+  int lda = 0;
+  const float* W = nullptr;
+  int ldw = 0;
+  const float* bias = nullptr;
+  float* C = nullptr;
+  int ldc = 0;
+  int M = 0, N = 0, K = 0;
+};
+hipError_t launch_gemm_f32(const GemmF32Args& p, int epilogue, hipStream_t s);
+
+// ------------------------------------------------------------- attention
+// One work item per (sequence, head, query tile); built on the host from
+// cu_seqlens, longest sequences first.
+struct AttnWork {
+  int seq;
+  int head;
+  int q0;
+  int pad;
+};
+// bf16 Q/K (QK^T on bf16 MFMA), V as bf16 or fp16 (PV on fp16 MFMA with
+// fp16 probabilities), fp32 online softmax, head_dim 64.
+// q/k/v rows: token t, head h at base + t*ld + h*64.
+hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
+                                 const uint16_t* v, int v_is_bf16, int ld,
+                                 const int* cu_seqlens, const AttnWork* work,
+                                 int num_work, float* out, int ld_out,
+                                 float* tensor_absmax, hipStream_t s);
+// Exact fp32 path for any head_dim <= 128 (one thread per query).
+hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
+                                int ld, int head_dim, const int* cu_seqlens,
+                                const AttnWork* work, int num_work, float* out,
+                                int ld_out, hipStream_t s);
+constexpr int kAttnMfmaQTile = 128;
+constexpr int kAttnF32QTile = 64;
+
+// ------------------------------------------------------------ elementwise
+hipError_t launch_layernorm(const float* x, const float* gamma,
+                            const float* beta, float eps, float* out,
+                            int rows, int d, float* tensor_absmax,
+                            hipStream_t s);
+// LayerNorm fused with per-token symmetric int8 quantisation.
+hipError_t launch_layernorm_quant(const float* x, const float* gamma,
+                                  const float* beta, float eps, int rows,
+                                  int d, int8_t* q, int ldq, float* scales,
+                                  hipStream_t s);
+// Per-row (per-token) quantisation. src_kind: 0 fp32, 1 fp16, 2 bf16.
+hipError_t launch_quant_rows(const void* x, int src_kind, int ldx, int rows,
+                             int cols, int8_t* q, int ldq, float* scales,
+                             hipStream_t s);
+// Per-tensor quantisation with scale = absmax/127 (absmax read on device).
+hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols,
+                               const float* absmax, int8_t* q, int ldq,
+                               float* scales, hipStream_t s);
+hipError_t launch_absmax(const float* x, size_t n, float* absmax,
+                         hipStream_t s);
+hipError_t launch_fill_f32(float* x, size_t n, float v, hipStream_t s);
+hipError_t launch_gelu(const float* x, float* out, size_t n, hipStream_t s);
+hipError_t launch_residual_add(float* y, const float* x, size_t n,
+                               hipStream_t s);
+hipError_t launch_scale(float* x, size_t n, float scale, hipStream_t s);
+// In-place RoPE on fp32 rows: x[t*ld + h*dh + i] for h < heads, each value
+// first multiplied by pre_scale (the Q scale; 1 for K).
+hipError_t launch_rope_f32(float* x, int ld, const int* pos, int T, int heads,
+                           int head_dim, const float* cos_tab,
+                           const float* sin_tab, int tab_ld, float pre_scale,
+                           hipStream_t s);
+hipError_t launch_embed(const int* ids, const float* tok_scale,
+                        const float* embed, int T, int d, int mask_token_id,
+                        float* out, hipStream_t s);
+// fp32 -> bf16 / fp16 conversion (for the MFMA attention op).
+hipError_t launch_cast_f32(const float* x, size_t n, uint16_t* out,
+                           int to_bf16, hipStream_t s);
+
+}  // namespace esm_gfx950

@@ -1,0 +1,372 @@
+"""ctypes binding of the gfx950 C ABI (include/esm_gfx950.h).
+
+The binding holds no compute: every array operation is a call into
+libesm_gfx950.so. Loading fails loudly when the library is missing; there
+is no CPU fallback. Device memory comes from the library itself
+(esm_gfx950_malloc), so the process carries a single HIP runtime.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libesm_gfx950.so")
+
+OK = 0
+ACT_PER_TENSOR = 0
+ACT_PER_TOKEN = 1
+ATTN_FP32 = 0
+ATTN_BF16_MFMA = 1
+
+# Every symbol the header declares (checked by the CPU test suite).
+EXPORTED = [
+    "esm_gfx950_init", "esm_gfx950_destroy", "esm_gfx950_last_error", "esm_gfx950_device_arch",
+    "esm_gfx950_sync", "esm_gfx950_malloc", "esm_gfx950_free", "esm_gfx950_memcpy_h2d",
+    "esm_gfx950_memcpy_d2h", "esm_gfx950_memcpy_d2d", "esm_gfx950_timer_start", "esm_gfx950_timer_stop",
+    "esm_gfx950_kernel_timing", "esm_gfx950_kernel_timing_query", "esm_gfx950_weight_upload_i8",
+    "esm_gfx950_weight_free", "esm_gfx950_gemm_i8_i32", "esm_gfx950_linear_i8_q", "esm_gfx950_quantize_act",
+    "esm_gfx950_linear_i8", "esm_gfx950_linear_f32", "esm_gfx950_layernorm", "esm_gfx950_gelu",
+    "esm_gfx950_residual_add", "esm_gfx950_scale", "esm_gfx950_rope_build_tables",
+    "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
+    "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
+    "esm_gfx950_forward_packed", "esm_gfx950_model_arena_bytes",
+]
+
+
+class Gfx950Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"esm_gfx950 error {code}: {msg}")
+        self.code = code
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Loads libesm_gfx950.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not built (run python esm-cpp_amd/build.py)")
+    lib = C.CDLL(path)
+    vp, i32, sz, f32 = C.c_void_p, C.c_int, C.c_size_t, C.c_float
+    sig = {
+        "esm_gfx950_init": (i32, [i32, C.POINTER(vp)]),
+        "esm_gfx950_destroy": (i32, [vp]),
+        "esm_gfx950_last_error": (C.c_char_p, [vp]),
+        "esm_gfx950_device_arch": (C.c_char_p, [vp]),
+        "esm_gfx950_sync": (i32, [vp]),
+        "esm_gfx950_malloc": (i32, [vp, sz, C.POINTER(vp)]),
+        "esm_gfx950_free": (i32, [vp, vp]),
+        "esm_gfx950_memcpy_h2d": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_memcpy_d2h": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_memcpy_d2d": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_timer_start": (i32, [vp]),
+        "esm_gfx950_timer_stop": (i32, [vp, C.POINTER(f32)]),
+        "esm_gfx950_kernel_timing": (i32, [vp, C.c_char_p, i32]),
+        "esm_gfx950_kernel_timing_query": (i32, [vp, C.POINTER(i32), C.POINTER(C.c_double)]),
+        "esm_gfx950_weight_upload_i8": (i32, [vp, vp, vp, i32, i32, C.POINTER(vp)]),
+        "esm_gfx950_weight_free": (i32, [vp, vp]),
+        "esm_gfx950_gemm_i8_i32": (i32, [vp, vp, i32, vp, i32, vp]),
+        "esm_gfx950_linear_i8_q": (i32, [vp, vp, i32, vp, vp, vp, vp, i32, i32]),
+        "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
+        "esm_gfx950_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+        "esm_gfx950_linear_f32": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+        "esm_gfx950_layernorm": (i32, [vp, vp, vp, vp, f32, vp, i32, i32]),
+        "esm_gfx950_gelu": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_residual_add": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_scale": (i32, [vp, vp, sz, f32]),
+        "esm_gfx950_rope_build_tables": (i32, [i32, i32, vp, vp]),
+        "esm_gfx950_rope_apply_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+        "esm_gfx950_attention_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp, i32]),
+        "esm_gfx950_attention_varlen_bf16": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, vp]),
+        "esm_gfx950_model_create": (i32, [vp, vp, C.POINTER(vp)]),
+        "esm_gfx950_model_free": (i32, [vp, vp]),
+        "esm_gfx950_model_set_act_mode": (i32, [vp, vp, i32]),
+        "esm_gfx950_forward_packed": (i32, [vp, vp, vp, vp, i32, i32, vp, i32]),
+        "esm_gfx950_model_arena_bytes": (i32, [vp, C.POINTER(sz)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    return C.c_void_p(a.ctypes.data)
+
+
+def rope_build_tables(seq_len: int, head_dim: int):
+    """RopeBuildTables on the host (reference formula)."""
+    lib = load_library()
+    cos = np.zeros((max(seq_len, 1), head_dim), np.float32)
+    sin = np.zeros_like(cos)
+    rc = lib.esm_gfx950_rope_build_tables(seq_len, head_dim, _ptr(cos), _ptr(sin))
+    if rc != OK:
+        raise Gfx950Error(rc, "rope_build_tables")
+    return cos[:seq_len], sin[:seq_len]
+
+
+class DeviceArray:
+    """A device allocation with a numpy dtype and shape."""
+
+    def __init__(self, dev: "Device", shape, dtype):
+        self.dev = dev
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        dev._check(dev.lib.esm_gfx950_malloc(dev.ctx, max(self.nbytes, 1), C.byref(p)))
+        self.ptr = p
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            self.dev._check(self.dev.lib.esm_gfx950_memcpy_d2h(self.dev.ctx, _ptr(out), self.ptr, self.nbytes))
+        return out
+
+    def upload(self, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        if self.nbytes:
+            self.dev._check(self.dev.lib.esm_gfx950_memcpy_h2d(self.dev.ctx, self.ptr, _ptr(a), self.nbytes))
+        return self
+
+    def free(self):
+        if self.ptr:
+            self.dev.lib.esm_gfx950_free(self.dev.ctx, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.dev.ctx:
+                self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    def __init__(self, dev: "Device", packed: np.ndarray, scales: np.ndarray):
+        packed = np.ascontiguousarray(packed, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        N, K = packed.shape
+        h = C.c_void_p()
+        dev._check(dev.lib.esm_gfx950_weight_upload_i8(dev.ctx, _ptr(packed), _ptr(scales), N, K, C.byref(h)))
+        self.dev, self.handle, self.N, self.K = dev, h, N, K
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.esm_gfx950_weight_free(self.dev.ctx, self.handle)
+            self.handle = None
+
+
+class Device:
+    """One gfx950 context (one HIP stream)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        ctx = C.c_void_p()
+        rc = self.lib.esm_gfx950_init(device, C.byref(ctx))
+        if rc != OK:
+            raise Gfx950Error(rc, "esm_gfx950_init failed (no gfx950 device?)")
+        self.ctx = ctx
+        self.arch = self.lib.esm_gfx950_device_arch(ctx).decode()
+
+    def _check(self, rc: int):
+        if rc != OK:
+            raise Gfx950Error(rc, self.lib.esm_gfx950_last_error(self.ctx).decode())
+
+    def close(self):
+        if self.ctx:
+            self.lib.esm_gfx950_destroy(self.ctx)
+            self.ctx = None
+
+    # -------------------------------------------------------------- memory
+    def empty(self, shape, dtype) -> DeviceArray:
+        return DeviceArray(self, shape, dtype)
+
+    def array(self, a: np.ndarray, dtype=None) -> DeviceArray:
+        a = np.ascontiguousarray(a, dtype=dtype)
+        return DeviceArray(self, a.shape, a.dtype).upload(a)
+
+    def sync(self):
+        self._check(self.lib.esm_gfx950_sync(self.ctx))
+
+    def timer_start(self):
+        self._check(self.lib.esm_gfx950_timer_start(self.ctx))
+
+    def timer_stop(self) -> float:
+        ms = C.c_float()
+        self._check(self.lib.esm_gfx950_timer_stop(self.ctx, C.byref(ms)))
+        return float(ms.value)
+
+    def kernel_timing(self, site: Optional[str], enable: bool = True):
+        self._check(self.lib.esm_gfx950_kernel_timing(self.ctx, site.encode() if site else None, int(enable)))
+
+    def kernel_timing_query(self):
+        n, ms = C.c_int(), C.c_double()
+        self._check(self.lib.esm_gfx950_kernel_timing_query(self.ctx, C.byref(n), C.byref(ms)))
+        return int(n.value), float(ms.value)
+
+    # ------------------------------------------------------------------ ops
+    def weight_i8(self, packed: np.ndarray, scales: np.ndarray) -> Weight:
+        return Weight(self, packed, scales)
+
+    def gemm_i8_i32(self, A: DeviceArray, lda: int, W: Weight, M: int, C_out: DeviceArray):
+        self._check(self.lib.esm_gfx950_gemm_i8_i32(self.ctx, A.ptr, lda, W.handle, M, C_out.ptr))
+
+    def linear_i8_q(self, A: DeviceArray, lda: int, a_scale: DeviceArray, W: Weight, bias: Optional[DeviceArray],
+                    C_out: DeviceArray, M: int, gelu: bool = False):
+        self._check(self.lib.esm_gfx950_linear_i8_q(self.ctx, A.ptr, lda, a_scale.ptr, W.handle,
+                                                    bias.ptr if bias is not None else None, C_out.ptr, M, int(gelu)))
+
+    def quantize_act(self, x: DeviceArray, M: int, K: int, mode: int, q: DeviceArray, ldq: int, scales: DeviceArray):
+        self._check(self.lib.esm_gfx950_quantize_act(self.ctx, x.ptr, M, K, mode, q.ptr, ldq, scales.ptr))
+
+    def linear_i8(self, A: DeviceArray, W: Weight, bias: Optional[DeviceArray], C_out: DeviceArray, M: int, N: int,
+                  K: int, mode: int):
+        self._check(self.lib.esm_gfx950_linear_i8(self.ctx, A.ptr, W.handle, bias.ptr if bias is not None else None,
+                                                  C_out.ptr, M, N, K, mode))
+
+    def linear_f32(self, A, W, bias, C_out, M, N, K):
+        self._check(self.lib.esm_gfx950_linear_f32(self.ctx, A.ptr, W.ptr, bias.ptr if bias is not None else None,
+                                                   C_out.ptr, M, N, K))
+
+    def layernorm(self, x, gamma, beta, eps, out, rows, d):
+        self._check(self.lib.esm_gfx950_layernorm(self.ctx, x.ptr, gamma.ptr, beta.ptr, eps, out.ptr, rows, d))
+
+    def gelu(self, x, out, n):
+        self._check(self.lib.esm_gfx950_gelu(self.ctx, x.ptr, out.ptr, n))
+
+    def residual_add(self, y, x, n):
+        self._check(self.lib.esm_gfx950_residual_add(self.ctx, y.ptr, x.ptr, n))
+
+    def scale(self, x, n, s):
+        self._check(self.lib.esm_gfx950_scale(self.ctx, x.ptr, n, s))
+
+    def rope_apply_varlen(self, x, cos, sin, cu: np.ndarray, H: int, dh: int):
+        cu = np.ascontiguousarray(cu, np.int32)
+        self._check(self.lib.esm_gfx950_rope_apply_varlen(self.ctx, x.ptr, cos.ptr, sin.ptr, _ptr(cu), len(cu) - 1,
+                                                          H, dh))
+
+    def attention_varlen(self, q, k, v, cu: np.ndarray, H: int, dh: int, out, precision: int = ATTN_FP32):
+        cu = np.ascontiguousarray(cu, np.int32)
+        self._check(self.lib.esm_gfx950_attention_varlen(self.ctx, q.ptr, k.ptr, v.ptr, _ptr(cu), len(cu) - 1, H, dh,
+                                                         out.ptr, precision))
+
+    def attention_varlen_bf16(self, q, k, v, cu: np.ndarray, H: int, out, v_is_fp16: bool = False):
+        cu = np.ascontiguousarray(cu, np.int32)
+        self._check(self.lib.esm_gfx950_attention_varlen_bf16(self.ctx, q.ptr, k.ptr, v.ptr, int(v_is_fp16),
+                                                              _ptr(cu), len(cu) - 1, H, out.ptr))
+
+
+# ------------------------------------------------------------------ model
+class _ModelConfig(C.Structure):
+    _fields_ = [("num_layers", C.c_int), ("hidden_size", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int),
+                ("intermediate_size", C.c_int), ("vocab_size", C.c_int), ("layer_norm_eps", C.c_float),
+                ("mask_token_id", C.c_int), ("weights_int8", C.c_int), ("act_quant_mode", C.c_int),
+                ("attention_fp32", C.c_int)]
+
+
+class _LinearDesc(C.Structure):
+    _fields_ = [("w_f32", C.c_void_p), ("w_i8", C.c_void_p), ("w_scale", C.c_void_p), ("bias", C.c_void_p)]
+
+
+class _LayerDesc(C.Structure):
+    _fields_ = [("attn_ln_w", C.c_void_p), ("attn_ln_b", C.c_void_p), ("q", _LinearDesc), ("k", _LinearDesc),
+                ("v", _LinearDesc), ("out", _LinearDesc), ("ffn_ln_w", C.c_void_p), ("ffn_ln_b", C.c_void_p),
+                ("fc1", _LinearDesc), ("fc2", _LinearDesc)]
+
+
+class _ModelDesc(C.Structure):
+    _fields_ = [("cfg", _ModelConfig), ("embed", C.c_void_p), ("layers", C.POINTER(_LayerDesc)),
+                ("final_ln_w", C.c_void_p), ("final_ln_b", C.c_void_p), ("lm_dense_w", C.c_void_p),
+                ("lm_dense_b", C.c_void_p), ("lm_ln_w", C.c_void_p), ("lm_ln_b", C.c_void_p),
+                ("lm_decoder_bias", C.c_void_p)]
+
+
+class Model:
+    """Device-resident packed ESM-2 encoder (esm_gfx950_model).
+
+    `weights` is an esm_gfx950.synthetic.EsmWeights (fp32 tensors plus, for
+    W8A8, the per-channel int8 packs).
+    """
+
+    def __init__(self, dev: Device, weights, int8: bool, act_mode: int = ACT_PER_TOKEN, attention_fp32: bool = False):
+        cfg = weights.cfg
+        keep: List[np.ndarray] = []
+
+        def p(a):
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+            return a.ctypes.data
+
+        def lin(name, i):
+            d = _LinearDesc()
+            d.bias = p(weights.f32[f"layers.{i}.{name}.bias"].astype(np.float32))
+            if int8:
+                q, s = weights.i8[f"layers.{i}.{name}"]
+                d.w_i8 = p(q)
+                d.w_scale = p(s)
+            else:
+                d.w_f32 = p(weights.f32[f"layers.{i}.{name}.weight"].astype(np.float32))
+            return d
+
+        layers = (_LayerDesc * max(cfg.num_layers, 1))()
+        for i in range(cfg.num_layers):
+            L = layers[i]
+            L.attn_ln_w = p(weights.f32[f"layers.{i}.attn_ln.weight"])
+            L.attn_ln_b = p(weights.f32[f"layers.{i}.attn_ln.bias"])
+            L.ffn_ln_w = p(weights.f32[f"layers.{i}.ffn_ln.weight"])
+            L.ffn_ln_b = p(weights.f32[f"layers.{i}.ffn_ln.bias"])
+            L.q, L.k, L.v, L.out = lin("q", i), lin("k", i), lin("v", i), lin("out", i)
+            L.fc1, L.fc2 = lin("fc1", i), lin("fc2", i)
+        desc = _ModelDesc()
+        desc.cfg = _ModelConfig(cfg.num_layers, cfg.hidden_size, cfg.num_heads, cfg.head_dim, cfg.intermediate_size,
+                                cfg.vocab_size, cfg.layer_norm_eps, cfg.mask_token_id, int(int8), act_mode,
+                                int(attention_fp32))
+        f = weights.f32
+        desc.embed = p(f["embed"])
+        desc.layers = layers
+        desc.final_ln_w, desc.final_ln_b = p(f["final_ln.weight"]), p(f["final_ln.bias"])
+        desc.lm_dense_w, desc.lm_dense_b = p(f["lm_head.dense.weight"]), p(f["lm_head.dense.bias"])
+        desc.lm_ln_w, desc.lm_ln_b = p(f["lm_head.ln.weight"]), p(f["lm_head.ln.bias"])
+        desc.lm_decoder_bias = p(f["lm_head.decoder.bias"])
+        h = C.c_void_p()
+        dev._check(dev.lib.esm_gfx950_model_create(dev.ctx, C.byref(desc), C.byref(h)))
+        self.dev, self.handle, self.cfg = dev, h, cfg
+
+    def set_act_mode(self, mode: int):
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))
+
+    def forward_packed(self, ids: np.ndarray, cu: np.ndarray, out: Optional[DeviceArray] = None):
+        """Packed forward; returns host logits [T, vocab] or fills `out` on device."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        cu = np.ascontiguousarray(cu, np.int32)
+        T = int(ids.shape[0])
+        if out is None:
+            logits = np.empty((T, self.cfg.vocab_size), np.float32)
+            self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
+                                                                   len(cu) - 1, T, _ptr(logits), 0))
+            return logits
+        self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
+                                                               len(cu) - 1, T, out.ptr, 1))
+        return out
+
+    def arena_bytes(self) -> int:
+        n = C.c_size_t()
+        self.dev._check(self.dev.lib.esm_gfx950_model_arena_bytes(self.handle, C.byref(n)))
+        return int(n.value)
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.esm_gfx950_model_free(self.dev.ctx, self.handle)
+            self.handle = None

@@ -1,0 +1,244 @@
+/*
+ * esm_gfx950.h -- C ABI of the MI355X (gfx950) backend for the packed ESM-2
+ * encoder hot path of esm.cpp: varlen attention with rotary Q/K and the W8A8
+ * INT8 linear layers around it.
+ *
+ * Plain C: opaque handles, plain pointers and sizes, int status codes. No
+ * HIP or C++ types appear in the signatures, so the reference's C++ host
+ * (src/kernels/dispatch.cpp) can bind it from a new `case Isa::Gfx950:` arm,
+ * and Python can bind it with ctypes.
+ *
+ * Conventions
+ *  - Every call returns ESM_GFX950_OK (0) or a status code that mirrors
+ *    esm::StatusCode (reference include/esm_cpp/status.h:9-36);
+ *    esm_gfx950_last_error() gives the message. Nothing fails silently and
+ *    nothing falls back to a CPU path.
+ *  - Tensor arguments of the op-level entry points are DEVICE pointers
+ *    (esm_gfx950_malloc or any hipMalloc'd memory); batch descriptions
+ *    (token ids, cu_seqlens) are HOST arrays, as in the reference's
+ *    BatchView (include/esm_cpp/batch.h:16-36).
+ *  - A context owns one HIP stream. Calls are stream-ordered and return
+ *    after enqueue; esm_gfx950_sync() waits. One context = one forward in
+ *    flight, the reference Model's threading contract
+ *    (include/esm_cpp/model.h:176-181).
+ *  - Layouts are the reference's: row-major, W as [N, K] (out, in),
+ *    q/k/v token-major [T, H, head_dim], attention out [T, H*head_dim].
+ */
+#ifndef ESM_GFX950_H_
+#define ESM_GFX950_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: values of esm::StatusCode (status.h:9-17) plus kHipError. */
+enum {
+  ESM_GFX950_OK = 0,
+  ESM_GFX950_INVALID_ARGUMENT = 1,
+  ESM_GFX950_OUT_OF_RANGE = 2,
+  ESM_GFX950_NOT_FOUND = 3,
+  ESM_GFX950_IO_ERROR = 4,
+  ESM_GFX950_SHAPE_MISMATCH = 5,
+  ESM_GFX950_INTERNAL = 6,
+  ESM_GFX950_HIP_ERROR = 7
+};
+
+/* Activation quantisation granularity for W8A8 linears.
+ * PER_TENSOR reproduces the reference's dynamic per-tensor scale
+ * (src/kernels/gemm_int8.cpp:391-508: scale = max|A|/127 over the whole
+ * [M,K] input, 1 when all zero); PER_TOKEN uses one such scale per row. */
+enum { ESM_GFX950_ACT_PER_TENSOR = 0, ESM_GFX950_ACT_PER_TOKEN = 1 };
+
+/* Attention arithmetic for esm_gfx950_attention_varlen. */
+enum { ESM_GFX950_ATTN_FP32 = 0, ESM_GFX950_ATTN_BF16_MFMA = 1 };
+
+typedef struct esm_gfx950_ctx esm_gfx950_ctx;
+typedef struct esm_gfx950_weight esm_gfx950_weight;
+typedef struct esm_gfx950_model esm_gfx950_model;
+
+/* ---------------------------------------------------------------- context
+ * Device selection replaces the ISA probe (reference
+ * src/kernels/cpu_features.cpp:69-87, 130-135): a successful init is what
+ * makes the gfx950 arm selectable. Fails with ESM_GFX950_HIP_ERROR when no
+ * gfx950 device is present. */
+int esm_gfx950_init(int device, esm_gfx950_ctx** out);
+int esm_gfx950_destroy(esm_gfx950_ctx* ctx);
+const char* esm_gfx950_last_error(const esm_gfx950_ctx* ctx);
+/* Device name (gcnArchName) of the context's device. */
+const char* esm_gfx950_device_arch(const esm_gfx950_ctx* ctx);
+int esm_gfx950_sync(esm_gfx950_ctx* ctx);
+
+/* Device memory and copies (plumbing for callers without their own HIP). */
+int esm_gfx950_malloc(esm_gfx950_ctx* ctx, size_t bytes, void** dptr);
+int esm_gfx950_free(esm_gfx950_ctx* ctx, void* dptr);
+int esm_gfx950_memcpy_h2d(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes);
+int esm_gfx950_memcpy_d2h(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes);
+int esm_gfx950_memcpy_d2d(esm_gfx950_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* Stream-ordered timer: start/stop record HIP events on the context stream;
+ * elapsed is read after the stop event completes. */
+int esm_gfx950_timer_start(esm_gfx950_ctx* ctx);
+int esm_gfx950_timer_stop(esm_gfx950_ctx* ctx, float* elapsed_ms);
+
+/* Per-kernel timing: while enabled, the launches of the named GEMM site
+ * ("qkv", "out", "fc1", "fc2", "lm_dense", "attention" or "all_i8_gemm")
+ * inside esm_gfx950_forward_packed are bracketed by HIP events on the
+ * context stream. Query returns the number of launches and their summed
+ * duration since the last reset. */
+int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, const char* site, int enable);
+int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, int* launches, double* total_ms);
+
+/* ------------------------------------------------------- weights (L2 pack)
+ * Upload a per-channel symmetric INT8 weight: packed [N, K] int8 in
+ * [-127, 127] and per_channel_scales [N] (host pointers) -- the
+ * esm::quant::QuantizedTensor contents (reference include/esm_cpp/quant.h:
+ * 17-56, produced by Quantize src/quant/pack.cpp:149-177). Builds the
+ * device-resident gfx950 cache (rows padded to a 16-byte K pitch), the
+ * analogue of BuildKernelCache (pack.cpp:107-117). */
+int esm_gfx950_weight_upload_i8(esm_gfx950_ctx* ctx, const int8_t* packed, const float* scales,
+                                int N, int K, esm_gfx950_weight** out);
+int esm_gfx950_weight_free(esm_gfx950_ctx* ctx, esm_gfx950_weight* w);
+
+/* --------------------------------------------------------------- INT8 ops
+ * Raw int32 accumulators: C[m, n] = sum_k A[m, k] * W[n, k]. A is int8
+ * [M, lda] (lda >= K, lda % 16 == 0), C int32 [M, N]. The bit-exact check
+ * of the W8A8 inner product; no reference twin forms int32 (LinearInt8Ref
+ * src/kernels/gemm_int8.cpp:49-64 is W8A16), so parity is the closed form. */
+int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const esm_gfx950_weight* W,
+                           int M, int32_t* C);
+
+/* Quantised-activation linear: out = fma(float(acc), a_scale[m] * w_scale[n], bias[n]),
+ * optionally followed by GELU (gelu != 0). The dequant expression of
+ * FinalizeStore16 (gemm_int8.cpp:109-126) with a per-row activation scale.
+ * A int8 [M, lda], a_scale fp32 [M], bias fp32 [N] or NULL, C fp32 [M, N]. */
+int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const float* a_scale,
+                           const esm_gfx950_weight* W, const float* bias, float* C, int M, int gelu);
+
+/* Activation quantisation: x fp32 [M, K] -> q int8 [M, ldq] (zero padded
+ * past K) and scales fp32 [M] (all equal in PER_TENSOR mode). Reference
+ * QuantizeActPrefixAvx512 (gemm_int8.cpp:391-508) / QuantizeActivation-
+ * SymmetricRef (src/quant/pack.cpp:134-147). */
+int esm_gfx950_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int K, int mode, int8_t* q,
+                            int ldq, float* scales);
+
+/* esm::kernels::LinearInt8 (include/esm_cpp/kernels.h:56-57,
+ * dispatch.cpp:80-103): fp32 A [M, K] -> activation quant (mode) -> INT8
+ * GEMM -> dequant + bias -> fp32 C [M, N]. M, N or K <= 0 zeroes C as the
+ * reference does (gemm_int8.cpp:513-520). */
+int esm_gfx950_linear_i8(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
+                         const float* bias, float* C, int M, int N, int K, int act_mode);
+
+/* ----------------------------------------------------------- FP32 / misc ops
+ * esm::kernels::Linear (kernels.h:19-20; LinearRef gemm_fp32.cpp:33-46):
+ * C[M, N] = A[M, K] W[N, K]^T + bias (bias may be NULL). */
+int esm_gfx950_linear_f32(esm_gfx950_ctx* ctx, const float* A, const float* W, const float* bias,
+                          float* C, int M, int N, int K);
+/* esm::kernels::LayerNorm (kernels.h:32-33; LayerNormRef layernorm.cpp:23-44). */
+int esm_gfx950_layernorm(esm_gfx950_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                         float eps, float* out, int num_rows, int d);
+/* esm::kernels::Gelu (kernels.h:35; GeluRef gelu.cpp:30-35), exact erf form. */
+int esm_gfx950_gelu(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n);
+/* esm::kernels::ResidualAddInplace (kernels.h:24): y[i] += x[i]. */
+int esm_gfx950_residual_add(esm_gfx950_ctx* ctx, float* y, const float* x, size_t n);
+/* esm::kernels::ScaleInplace (kernels.h:29): x[i] *= scale. */
+int esm_gfx950_scale(esm_gfx950_ctx* ctx, float* x, size_t n, float scale);
+
+/* esm::kernels::RopeBuildTables (kernels.h:67; rope_tables.cpp:14-29),
+ * host-side: cos/sin [seq_len, head_dim] half-then-half tables written to
+ * HOST memory with the reference formula. */
+int esm_gfx950_rope_build_tables(int seq_len, int head_dim, float* cos_out, float* sin_out);
+/* esm::kernels::RopeApplyVarlen (kernels.h:84-92; rope.cpp:47-70):
+ * x fp32 [T, H, head_dim] rotated in place with device tables cos/sin
+ * [max_seqlen, head_dim]; positions restart at each cu_seqlens boundary.
+ * cu_seqlens is a HOST array of batch_size + 1 entries. */
+int esm_gfx950_rope_apply_varlen(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
+                                 const int* cu_seqlens, int batch_size, int num_heads, int head_dim);
+
+/* esm::kernels::AttentionVarlen (kernels.h:104-121; AttentionVarlenRef
+ * attention.cpp:99-144): q, k, v fp32 [T, H, head_dim] (Q pre-scaled),
+ * out fp32 [T, H*head_dim]. precision FP32 is the exact path (any
+ * head_dim <= 128); BF16_MFMA rounds q/k to bf16 and v to fp16 on device
+ * and runs the MFMA kernel (head_dim == 64). cu_seqlens is a HOST array. */
+int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
+                                const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
+                                float* out, int precision);
+/* The MFMA kernel on bf16 inputs: q, k, v bf16 bits [T, H, 64] (v may be
+ * fp16 when v_is_fp16 != 0), out fp32 [T, H*64]. cu_seqlens HOST. */
+int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint16_t* q, const uint16_t* k,
+                                     const uint16_t* v, int v_is_fp16, const int* cu_seqlens,
+                                     int batch_size, int num_heads, float* out);
+
+/* ------------------------------------------------------------------ model
+ * Forward-level fast path: the device-resident replacement of
+ * Model::ForwardPackedInto (reference src/model.cpp:1093-1255, layer body
+ * TransformerBlock :932-1066). Host pointers in the descriptors are read
+ * once at create time; weights then live on the device. */
+typedef struct {
+  int num_layers;
+  int hidden_size;
+  int num_heads;
+  int head_dim;
+  int intermediate_size;
+  int vocab_size;
+  float layer_norm_eps;
+  int mask_token_id;   /* 32 for ESM-2 (src/tokenizer.cpp:12-17) */
+  int weights_int8;    /* 1: W8A8 layer linears; 0: fp32 layer linears */
+  int act_quant_mode;  /* ESM_GFX950_ACT_PER_TENSOR / _PER_TOKEN */
+  int attention_fp32;  /* W8A8 models: 1 = fp32 Q/K/V + exact fp32 attention,
+                          0 = bf16 Q/K, fp16 V, MFMA attention (default) */
+} esm_gfx950_model_config;
+
+typedef struct {
+  const float* w_f32;    /* [N, K] fp32 (weights_int8 == 0) */
+  const int8_t* w_i8;    /* [N, K] int8 (weights_int8 == 1) */
+  const float* w_scale;  /* [N] per-channel scales (weights_int8 == 1) */
+  const float* bias;     /* [N] */
+} esm_gfx950_linear_desc;
+
+typedef struct {
+  const float* attn_ln_w;
+  const float* attn_ln_b;
+  esm_gfx950_linear_desc q, k, v, out;
+  const float* ffn_ln_w;
+  const float* ffn_ln_b;
+  esm_gfx950_linear_desc fc1, fc2;
+} esm_gfx950_layer_desc;
+
+typedef struct {
+  esm_gfx950_model_config cfg;
+  const float* embed;                  /* [vocab, hidden]; also the tied decoder */
+  const esm_gfx950_layer_desc* layers; /* [num_layers] */
+  const float* final_ln_w;
+  const float* final_ln_b;
+  const float* lm_dense_w;             /* [hidden, hidden] fp32 */
+  const float* lm_dense_b;
+  const float* lm_ln_w;
+  const float* lm_ln_b;
+  const float* lm_decoder_bias;        /* [vocab] */
+} esm_gfx950_model_desc;
+
+int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_model_desc* desc,
+                            esm_gfx950_model** out);
+int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model);
+/* Switch the activation quantisation mode of a W8A8 model. */
+int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int act_mode);
+
+/* Packed forward. ids [T] and cu_seqlens [batch_size + 1] are HOST arrays
+ * validated like BatchView (batch.cpp:8-46); masks are not supported (all
+ * tokens real). logits fp32 [T, vocab] is written to DEVICE memory when
+ * logits_on_device != 0, else to HOST memory (the call then synchronises).
+ * The device arena grows only when T exceeds every earlier batch. */
+int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                              const int32_t* cu_seqlens, int batch_size, int total_tokens,
+                              float* logits, int logits_on_device);
+/* Bytes currently held by the model's device arena (for zero-growth checks). */
+int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESM_GFX950_H_ */

@@ -1,0 +1,355 @@
+"""ctypes wrappers of the CPU checkers: lib/liboracle.so (the C restatement)
+and _ref/libesmref.so (the reference's own kernels, built by the Makefile).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "lib", "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libesmref.so")
+
+vp, i32, sz, f32 = C.c_void_p, C.c_int, C.c_size_t, C.c_float
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class _OrModel(C.Structure):
+    _fields_ = [("num_layers", i32), ("hidden", i32), ("heads", i32), ("head_dim", i32), ("ffn", i32),
+                ("vocab", i32), ("eps", f32), ("mask_token_id", i32), ("weights_int8", i32),
+                ("act_per_token", i32), ("embed", vp), ("ln1_w", C.POINTER(vp)), ("ln1_b", C.POINTER(vp)),
+                ("ln2_w", C.POINTER(vp)), ("ln2_b", C.POINTER(vp)), ("w_f32", C.POINTER(vp)),
+                ("w_i8", C.POINTER(vp)), ("w_scale", C.POINTER(vp)), ("bias", C.POINTER(vp)),
+                ("final_ln_w", vp), ("final_ln_b", vp), ("lm_dense_w", vp), ("lm_dense_b", vp),
+                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp)]
+
+
+LINEARS = ("q", "k", "v", "out", "fc1", "fc2")
+
+
+def make_or_model(weights, int8: bool, per_token: bool):
+    """Builds the or_model descriptor (and keeps its arrays alive)."""
+    cfg = weights.cfg
+    keep = []
+
+    def p(a):
+        a = np.ascontiguousarray(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    L = cfg.num_layers
+    arr = lambda n: (vp * max(n, 1))()
+    ln1w, ln1b, ln2w, ln2b = arr(L), arr(L), arr(L), arr(L)
+    wf, wi, ws, bs = arr(6 * L), arr(6 * L), arr(6 * L), arr(6 * L)
+    F = weights.f32
+    for i in range(L):
+        ln1w[i] = p(F[f"layers.{i}.attn_ln.weight"])
+        ln1b[i] = p(F[f"layers.{i}.attn_ln.bias"])
+        ln2w[i] = p(F[f"layers.{i}.ffn_ln.weight"])
+        ln2b[i] = p(F[f"layers.{i}.ffn_ln.bias"])
+        for j, n in enumerate(LINEARS):
+            bs[i * 6 + j] = p(F[f"layers.{i}.{n}.bias"])
+            if int8:
+                q, s = weights.i8[f"layers.{i}.{n}"]
+                wi[i * 6 + j] = p(q)
+                ws[i * 6 + j] = p(s)
+            else:
+                wf[i * 6 + j] = p(F[f"layers.{i}.{n}.weight"])
+    m = _OrModel()
+    m.num_layers, m.hidden, m.heads, m.head_dim = L, cfg.hidden_size, cfg.num_heads, cfg.head_dim
+    m.ffn, m.vocab, m.eps, m.mask_token_id = cfg.intermediate_size, cfg.vocab_size, cfg.layer_norm_eps, \
+        cfg.mask_token_id
+    m.weights_int8, m.act_per_token = int(int8), int(per_token)
+    m.embed = p(F["embed"])
+    m.ln1_w, m.ln1_b, m.ln2_w, m.ln2_b = ln1w, ln1b, ln2w, ln2b
+    m.w_f32, m.w_i8, m.w_scale, m.bias = wf, wi, ws, bs
+    m.final_ln_w, m.final_ln_b = p(F["final_ln.weight"]), p(F["final_ln.bias"])
+    m.lm_dense_w, m.lm_dense_b = p(F["lm_head.dense.weight"]), p(F["lm_head.dense.bias"])
+    m.lm_ln_w, m.lm_ln_b = p(F["lm_head.ln.weight"]), p(F["lm_head.ln.bias"])
+    m.lm_decoder_bias = p(F["lm_head.decoder.bias"])
+    keep.extend([ln1w, ln1b, ln2w, ln2b, wf, wi, ws, bs])
+    return m, keep
+
+
+class Oracle:
+    """The C restatement (liboracle.so)."""
+
+    def __init__(self, path: str = ORACLE_LIB):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle)")
+        lib = C.CDLL(path)
+        sig = {
+            "or_gemm_i8_i32": [vp, i32, vp, i32, i32, i32, i32, vp],
+            "or_quant_act_tensor": [vp, sz, vp, vp],
+            "or_quant_act_rows": [vp, i32, i32, vp, vp],
+            "or_dequant": [vp, vp, vp, vp, i32, i32, i32, vp],
+            "or_quantize_weight": [vp, i32, i32, vp, vp],
+            "or_linear_int8_w8a16": [vp, vp, vp, vp, vp, i32, i32, i32],
+            "or_linear_f32": [vp, vp, vp, vp, i32, i32, i32],
+            "or_layernorm": [vp, vp, vp, f32, vp, i32, i32],
+            "or_gelu": [vp, vp, sz],
+            "or_rope_tables": [i32, i32, vp, vp],
+            "or_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
+            "or_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
+            "or_forward_packed": [C.POINTER(_OrModel), vp, vp, i32, i32, vp],
+        }
+        for name, args in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = i32 if name == "or_forward_packed" else None
+        self.lib = lib
+
+    def gemm_i8_i32(self, A, W):
+        A, W = _c(A, np.int8), _c(W, np.int8)
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.int32)
+        self.lib.or_gemm_i8_i32(_p(A), K, _p(W), K, M, N, K, _p(out))
+        return out
+
+    def quant_act_tensor(self, x):
+        x = _c(x, np.float32)
+        q = np.empty(x.shape, np.int8)
+        s = C.c_float()
+        self.lib.or_quant_act_tensor(_p(x), x.size, _p(q), C.byref(s))
+        return q, float(s.value)
+
+    def quant_act_rows(self, x):
+        x = _c(x, np.float32)
+        M, K = x.shape
+        q = np.empty((M, K), np.int8)
+        s = np.empty(M, np.float32)
+        self.lib.or_quant_act_rows(_p(x), M, K, _p(q), _p(s))
+        return q, s
+
+    def dequant(self, acc, a_scale, w_scale, bias, gelu=False):
+        acc = _c(acc, np.int32)
+        M, N = acc.shape
+        out = np.empty((M, N), np.float32)
+        a_scale, w_scale = _c(a_scale, np.float32), _c(w_scale, np.float32)
+        bias = None if bias is None else _c(bias, np.float32)
+        self.lib.or_dequant(_p(acc), _p(a_scale), _p(w_scale), _p(bias), M, N, int(gelu), _p(out))
+        return out
+
+    def quantize_weight(self, W):
+        W = _c(W, np.float32)
+        N, K = W.shape
+        q = np.empty((N, K), np.int8)
+        s = np.empty(N, np.float32)
+        self.lib.or_quantize_weight(_p(W), N, K, _p(q), _p(s))
+        return q, s
+
+    def linear_int8_w8a16(self, A, q, s, bias):
+        A = _c(A, np.float32)
+        M, K = A.shape
+        N = q.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.or_linear_int8_w8a16(_p(A), _p(_c(q, np.int8)), _p(_c(s, np.float32)),
+                                      _p(None if bias is None else _c(bias, np.float32)), _p(out), M, N, K)
+        return out
+
+    def linear_f32(self, A, W, bias):
+        A, W = _c(A, np.float32), _c(W, np.float32)
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.or_linear_f32(_p(A), _p(W), _p(None if bias is None else _c(bias, np.float32)), _p(out), M, N, K)
+        return out
+
+    def layernorm(self, x, g, b, eps=1e-5):
+        x = _c(x, np.float32)
+        rows, d = x.shape
+        out = np.empty_like(x)
+        self.lib.or_layernorm(_p(x), _p(_c(g, np.float32)), _p(_c(b, np.float32)), eps, _p(out), rows, d)
+        return out
+
+    def gelu(self, x):
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.or_gelu(_p(x), _p(out), x.size)
+        return out
+
+    def rope_tables(self, L, dh):
+        c = np.zeros((max(L, 1), dh), np.float32)
+        s = np.zeros_like(c)
+        self.lib.or_rope_tables(L, dh, _p(c), _p(s))
+        return c[:L], s[:L]
+
+    def rope_varlen(self, x, cos, sin, cu, H, dh):
+        x = np.array(x, np.float32, copy=True, order="C")
+        cu = _c(cu, np.int32)
+        self.lib.or_rope_varlen(_p(x), _p(_c(cos, np.float32)), _p(_c(sin, np.float32)), _p(cu), len(cu) - 1, H, dh)
+        return x
+
+    def attention_varlen(self, q, k, v, cu, H, dh):
+        q, k, v, cu = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32), _c(cu, np.int32)
+        out = np.zeros((int(cu[-1]), H * dh), np.float32)
+        self.lib.or_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
+        return out
+
+    def forward_packed(self, weights, batch, int8: bool, per_token: bool):
+        m, keep = make_or_model(weights, int8, per_token)
+        T = batch.total_tokens
+        logits = np.empty((T, weights.cfg.vocab_size), np.float32)
+        rc = self.lib.or_forward_packed(C.byref(m), _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
+                                        len(batch.cu) - 1, T, _p(logits))
+        if rc != 0:
+            raise MemoryError("or_forward_packed")
+        return logits
+
+
+class RefLib:
+    """The reference's own kernels (oracle/_ref/libesmref.so)."""
+
+    def __init__(self, path: str = REF_LIB, threads: Optional[int] = None):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle ref)")
+        if threads is not None:
+            os.environ["ESM_NUM_THREADS"] = str(threads)
+        lib = C.CDLL(path)
+        sig = {
+            "esmref_isa": (C.c_char_p, []),
+            "esmref_host_isa": (C.c_char_p, []),
+            "esmref_quantize": (None, [vp, i32, i32, vp, vp]),
+            "esmref_linear_int8": (None, [vp, vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_linear_int8_ref": (None, [vp, vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_has_avx512_prefix": (i32, []),
+            "esmref_quant_act_prefix": (None, [vp, sz, vp, vp]),
+            "esmref_linear_vnni": (None, [vp, vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_linear": (None, [vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_linear_ref": (None, [vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_layernorm_ref": (None, [vp, vp, vp, f32, vp, i32, i32]),
+            "esmref_layernorm": (None, [vp, vp, vp, f32, vp, i32, i32]),
+            "esmref_gelu_ref": (None, [vp, vp, sz]),
+            "esmref_gelu": (None, [vp, vp, sz]),
+            "esmref_rope_tables": (None, [i32, i32, vp, vp]),
+            "esmref_rope_varlen_ref": (None, [vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_attention_varlen_ref": (None, [vp, vp, vp, vp, i32, i32, i32, vp]),
+            "esmref_attention_varlen": (None, [vp, vp, vp, vp, i32, i32, i32, vp]),
+            "esmref_model_create": (vp, [C.POINTER(_OrModel)]),
+            "esmref_model_free": (None, [vp]),
+            "esmref_forward_packed": (i32, [vp, vp, vp, i32, i32, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        self.lib = lib
+
+    def isa(self) -> str:
+        return self.lib.esmref_isa().decode()
+
+    def host_isa(self) -> str:
+        return self.lib.esmref_host_isa().decode()
+
+    def quantize(self, W):
+        W = _c(W, np.float32)
+        N, K = W.shape
+        q = np.empty((N, K), np.int8)
+        s = np.empty(N, np.float32)
+        self.lib.esmref_quantize(_p(W), N, K, _p(q), _p(s))
+        return q, s
+
+    def _lin8(self, fn, A, q, s, bias):
+        A = _c(A, np.float32)
+        M, K = A.shape
+        N = q.shape[0]
+        out = np.empty((M, N), np.float32)
+        fn(_p(A), _p(_c(q, np.int8)), _p(_c(s, np.float32)), _p(None if bias is None else _c(bias, np.float32)),
+           _p(out), M, N, K)
+        return out
+
+    def linear_int8(self, A, q, s, bias):
+        return self._lin8(self.lib.esmref_linear_int8, A, q, s, bias)
+
+    def linear_int8_ref(self, A, q, s, bias):
+        return self._lin8(self.lib.esmref_linear_int8_ref, A, q, s, bias)
+
+    def linear_vnni(self, A, q, s, bias):
+        return self._lin8(self.lib.esmref_linear_vnni, A, q, s, bias)
+
+    def quant_act_prefix(self, A):
+        A = _c(A, np.float32)
+        q = np.empty(A.shape, np.uint8)
+        s = C.c_float()
+        self.lib.esmref_quant_act_prefix(_p(A), A.size, _p(q), C.byref(s))
+        return q, float(s.value)
+
+    def linear_ref(self, A, W, bias):
+        A, W = _c(A, np.float32), _c(W, np.float32)
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.esmref_linear_ref(_p(A), _p(W), _p(None if bias is None else _c(bias, np.float32)), _p(out), M, N, K)
+        return out
+
+    def layernorm_ref(self, x, g, b, eps=1e-5):
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.esmref_layernorm_ref(_p(x), _p(_c(g, np.float32)), _p(_c(b, np.float32)), eps, _p(out), *x.shape)
+        return out
+
+    def gelu_ref(self, x):
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.esmref_gelu_ref(_p(x), _p(out), x.size)
+        return out
+
+    def rope_tables(self, L, dh):
+        c = np.zeros((max(L, 1), dh), np.float32)
+        s = np.zeros_like(c)
+        self.lib.esmref_rope_tables(L, dh, _p(c), _p(s))
+        return c[:L], s[:L]
+
+    def rope_varlen_ref(self, x, cos, sin, cu, H, dh):
+        x = np.array(x, np.float32, copy=True, order="C")
+        cu = _c(cu, np.int32)
+        self.lib.esmref_rope_varlen_ref(_p(x), _p(_c(cos, np.float32)), _p(_c(sin, np.float32)), _p(cu),
+                                        len(cu) - 1, H, dh)
+        return x
+
+    def attention_varlen_ref(self, q, k, v, cu, H, dh):
+        q, k, v, cu = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32), _c(cu, np.int32)
+        out = np.zeros((int(cu[-1]), H * dh), np.float32)
+        self.lib.esmref_attention_varlen_ref(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
+        return out
+
+    def attention_varlen(self, q, k, v, cu, H, dh):
+        q, k, v, cu = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32), _c(cu, np.int32)
+        out = np.zeros((int(cu[-1]), H * dh), np.float32)
+        self.lib.esmref_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
+        return out
+
+
+class RefModel:
+    """Reference CPU forward (reference kernels, restated ForwardPackedInto)."""
+
+    def __init__(self, ref: RefLib, weights, int8: bool):
+        m, keep = make_or_model(weights, int8, per_token=False)
+        self.ref, self.cfg = ref, weights.cfg
+        self.handle = ref.lib.esmref_model_create(C.byref(m))
+
+    def forward_packed(self, batch):
+        T = batch.total_tokens
+        logits = np.empty((T, self.cfg.vocab_size), np.float32)
+        self.ref.lib.esmref_forward_packed(self.handle, _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
+                                           len(batch.cu) - 1, T, _p(logits))
+        return logits
+
+    def free(self):
+        if self.handle:
+            self.ref.lib.esmref_model_free(self.handle)
+            self.handle = None

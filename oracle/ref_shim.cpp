@@ -1,0 +1,249 @@
+// ref_shim.cpp -- C-linkage wrappers around the reference's own kernel
+// facade (esm::kernels::*, esm::quant::*), compiled from the unmodified
+// reference sources under /root/reference by oracle/Makefile into
+// oracle/_ref/libesmref.so.
+//
+// TEST INFRASTRUCTURE ONLY: used by tests/ to pin the oracle and by
+// bench.py's cpu_baseline leg to time the reference CPU path; the product
+// never loads it.
+//
+// The reference's Model::ForwardPackedInto lives in src/model.cpp, which
+// includes a header that CMake generates at configure time
+// (esm_cpp/artifact_trace_sha.h from cmake/artifact_trace_sha.h.in), so it
+// is not buildable from its sources alone. esmref_forward_packed below
+// restates its call sequence (src/model.cpp:932-1066 TransformerBlock,
+// :1093-1255 ForwardPackedInto) over the reference's own kernel facade.
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "esm_cpp/cpu_features.h"
+#include "esm_cpp/kernels.h"
+#include "esm_cpp/quant.h"
+#include "oracle.h"
+
+namespace esm::kernels {
+// Defined in the AVX-512 TU of gemm_int8.cpp (x86 builds).
+void QuantizeActPrefixAvx512(const float* A, std::size_t MK, std::uint8_t* a_u8, float* act_scale_out);
+void LinearVnni(const float* A, const esm::quant::QuantizedTensor& W, const float* bias, float* C, int M, int N,
+                int K);
+void AttentionVarlenAvx512(const float* q, const float* k, const float* v, const int* cu_seqlens, int batch_size,
+                           int num_heads, int head_dim, float* out);
+}  // namespace esm::kernels
+
+namespace {
+
+esm::quant::QuantizedTensor make_qt(const int8_t* packed, const float* scales, int N, int K) {
+  esm::quant::QuantizedTensor qt;
+  qt.N = N;
+  qt.K = K;
+  qt.packed.assign(packed, packed + static_cast<size_t>(N) * K);
+  qt.per_channel_scales.assign(scales, scales + N);
+  esm::quant::BuildKernelCache(&qt);
+  return qt;
+}
+
+struct RefLayer {
+  std::vector<float> ln1_w, ln1_b, ln2_w, ln2_b;
+  esm::quant::QuantizedTensor w8[6];
+  std::vector<float> w32[6];
+  std::vector<float> bias[6];
+  int N[6], K[6];
+};
+
+struct RefModel {
+  or_model cfg{};
+  std::vector<float> embed, final_ln_w, final_ln_b, lm_dense_w, lm_dense_b, lm_ln_w, lm_ln_b, dec_b;
+  std::vector<RefLayer> layers;
+};
+
+std::vector<float> vec(const float* p, size_t n) { return std::vector<float>(p, p + n); }
+
+}  // namespace
+
+extern "C" {
+
+const char* esmref_isa() {
+  static std::string s;
+  s = std::string(esm::IsaToString(esm::CurrentIsa()));
+  return s.c_str();
+}
+
+const char* esmref_host_isa() {
+  static std::string s;
+  s = std::string(esm::IsaToString(esm::HostIsa()));
+  return s.c_str();
+}
+
+void esmref_quantize(const float* W, int N, int K, int8_t* q, float* scales) {
+  esm::quant::QuantizedTensor qt;
+  esm::quant::Quantize(W, N, K, &qt);
+  std::memcpy(q, qt.packed.data(), qt.packed.size());
+  std::memcpy(scales, qt.per_channel_scales.data(), qt.per_channel_scales.size() * sizeof(float));
+}
+
+void esmref_linear_int8(const float* A, const int8_t* packed, const float* scales, const float* bias, float* C, int M,
+                        int N, int K) {
+  auto qt = make_qt(packed, scales, N, K);
+  esm::kernels::LinearInt8(A, qt, bias, C, M, N, K);
+}
+
+void esmref_linear_int8_ref(const float* A, const int8_t* packed, const float* scales, const float* bias, float* C,
+                            int M, int N, int K) {
+  auto qt = make_qt(packed, scales, N, K);
+  esm::kernels::LinearInt8Ref(A, qt, bias, C, M, N, K);
+}
+
+int esmref_has_avx512_prefix() {
+#if defined(__x86_64__)
+  return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") ? 1 : 0;
+#else
+  return 0;
+#endif
+}
+
+// QuantizeActPrefixAvx512 (gemm_int8.cpp:391-508): u8 with zero-point 128.
+void esmref_quant_act_prefix(const float* A, size_t MK, uint8_t* q, float* scale) {
+  esm::kernels::QuantizeActPrefixAvx512(A, MK, q, scale);
+}
+
+void esmref_linear_vnni(const float* A, const int8_t* packed, const float* scales, const float* bias, float* C, int M,
+                        int N, int K) {
+  auto qt = make_qt(packed, scales, N, K);
+  esm::kernels::LinearVnni(A, qt, bias, C, M, N, K);
+}
+
+void esmref_linear(const float* A, const float* W, const float* bias, float* C, int M, int N, int K) {
+  esm::kernels::Linear(A, W, bias, C, M, N, K);
+}
+void esmref_linear_ref(const float* A, const float* W, const float* bias, float* C, int M, int N, int K) {
+  esm::kernels::LinearRef(A, W, bias, C, M, N, K);
+}
+void esmref_layernorm_ref(const float* x, const float* g, const float* b, float eps, float* out, int rows, int d) {
+  esm::kernels::LayerNormRef(x, g, b, eps, out, rows, d);
+}
+void esmref_layernorm(const float* x, const float* g, const float* b, float eps, float* out, int rows, int d) {
+  esm::kernels::LayerNorm(x, g, b, eps, out, rows, d);
+}
+void esmref_gelu_ref(const float* x, float* out, size_t n) { esm::kernels::GeluRef(x, out, n); }
+void esmref_gelu(const float* x, float* out, size_t n) { esm::kernels::Gelu(x, out, n); }
+void esmref_rope_tables(int L, int dh, float* c, float* s) { esm::kernels::RopeBuildTables(L, dh, c, s); }
+void esmref_rope_varlen_ref(float* x, const float* c, const float* s, const int* cu, int B, int H, int dh) {
+  esm::kernels::RopeApplyVarlenRef(x, c, s, cu, B, H, dh);
+}
+void esmref_attention_varlen_ref(const float* q, const float* k, const float* v, const int* cu, int B, int H, int dh,
+                                 float* out) {
+  esm::kernels::AttentionVarlenRef(q, k, v, cu, B, H, dh, out);
+}
+void esmref_attention_varlen(const float* q, const float* k, const float* v, const int* cu, int B, int H, int dh,
+                             float* out) {
+  esm::kernels::AttentionVarlen(q, k, v, cu, B, H, dh, out);
+}
+
+// ---------------------------------------------------------------- model
+void* esmref_model_create(const or_model* m) {
+  auto* r = new RefModel();
+  r->cfg = *m;
+  const int d = m->hidden, f = m->ffn, V = m->vocab;
+  r->embed = vec(m->embed, static_cast<size_t>(V) * d);
+  r->layers.resize(m->num_layers);
+  const int Ns[6] = {d, d, d, d, f, d};
+  const int Ks[6] = {d, d, d, d, d, f};
+  for (int l = 0; l < m->num_layers; ++l) {
+    RefLayer& L = r->layers[l];
+    L.ln1_w = vec(m->ln1_w[l], d);
+    L.ln1_b = vec(m->ln1_b[l], d);
+    L.ln2_w = vec(m->ln2_w[l], d);
+    L.ln2_b = vec(m->ln2_b[l], d);
+    for (int j = 0; j < 6; ++j) {
+      const int idx = l * 6 + j;
+      L.N[j] = Ns[j];
+      L.K[j] = Ks[j];
+      L.bias[j] = vec(m->bias[idx], Ns[j]);
+      if (m->weights_int8) {
+        L.w8[j] = make_qt(m->w_i8[idx], m->w_scale[idx], Ns[j], Ks[j]);
+      } else {
+        L.w32[j] = vec(m->w_f32[idx], static_cast<size_t>(Ns[j]) * Ks[j]);
+      }
+    }
+  }
+  r->final_ln_w = vec(m->final_ln_w, d);
+  r->final_ln_b = vec(m->final_ln_b, d);
+  r->lm_dense_w = vec(m->lm_dense_w, static_cast<size_t>(d) * d);
+  r->lm_dense_b = vec(m->lm_dense_b, d);
+  r->lm_ln_w = vec(m->lm_ln_w, d);
+  r->lm_ln_b = vec(m->lm_ln_b, d);
+  r->dec_b = vec(m->lm_decoder_bias, V);
+  return r;
+}
+
+void esmref_model_free(void* h) { delete static_cast<RefModel*>(h); }
+
+// Restated ForwardPackedInto over the reference facade. Returns 0.
+int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B, int T, float* logits) {
+  auto* r = static_cast<RefModel*>(h);
+  const or_model& c = r->cfg;
+  const int d = c.hidden, H = c.heads, dh = c.head_dim, f = c.ffn, V = c.vocab;
+  const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * f;
+  int maxL = 0;
+  for (int b = 0; b < B; ++b) maxL = std::max(maxL, cu[b + 1] - cu[b]);
+  std::vector<float> hidden(Td), ln(Td), qkv(3 * Td), cs(static_cast<size_t>(maxL) * dh),
+      sn(static_cast<size_t>(maxL) * dh), attn(Td), proj(Td), inter(Tf), inter_g(Tf);
+  // Embed (model.cpp:737-778).
+  const float k_drop = 0.15f * 0.8f;
+  for (int b = 0; b < B; ++b) {
+    int src_len = 0, masks = 0;
+    for (int t = cu[b]; t < cu[b + 1]; ++t) {
+      ++src_len;
+      if (ids[t] == c.mask_token_id) ++masks;
+    }
+    const float ratio = src_len > 0 ? static_cast<float>(masks) / static_cast<float>(src_len) : 0.0f;
+    const float scale = (1.0f - k_drop) / std::max(1.0f - ratio, 1e-12f);
+    for (int t = cu[b]; t < cu[b + 1]; ++t) {
+      const float* row = r->embed.data() + static_cast<size_t>(ids[t]) * d;
+      float* o = hidden.data() + static_cast<size_t>(t) * d;
+      for (int i = 0; i < d; ++i) o[i] = ids[t] == c.mask_token_id ? 0.0f : row[i] * scale;
+    }
+  }
+  auto linear = [&](const RefLayer& L, int j, const float* A, float* C, int M) {
+    if (c.weights_int8) {
+      esm::kernels::LinearInt8(A, L.w8[j], L.bias[j].data(), C, M, L.N[j], L.K[j]);
+    } else {
+      esm::kernels::Linear(A, L.w32[j].data(), L.bias[j].data(), C, M, L.N[j], L.K[j]);
+    }
+  };
+  for (const RefLayer& L : r->layers) {
+    float* q = qkv.data();
+    float* k = qkv.data() + Td;
+    float* v = qkv.data() + 2 * Td;
+    esm::kernels::LayerNorm(hidden.data(), L.ln1_w.data(), L.ln1_b.data(), c.eps, ln.data(), T, d);
+    linear(L, 0, ln.data(), q, T);
+    linear(L, 1, ln.data(), k, T);
+    linear(L, 2, ln.data(), v, T);
+    const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
+    esm::kernels::ScaleInplace(q, Td, q_scale);
+    esm::kernels::RopeBuildTables(maxL, dh, cs.data(), sn.data());
+    esm::kernels::RopeApplyVarlen(q, cs.data(), sn.data(), cu, B, H, dh);
+    esm::kernels::RopeApplyVarlen(k, cs.data(), sn.data(), cu, B, H, dh);
+    esm::kernels::AttentionVarlen(q, k, v, cu, B, H, dh, attn.data());
+    linear(L, 3, attn.data(), proj.data(), T);
+    esm::kernels::ResidualAddInplace(hidden.data(), proj.data(), Td);
+    esm::kernels::LayerNorm(hidden.data(), L.ln2_w.data(), L.ln2_b.data(), c.eps, ln.data(), T, d);
+    linear(L, 4, ln.data(), inter.data(), T);
+    esm::kernels::Gelu(inter.data(), inter_g.data(), Tf);
+    linear(L, 5, inter_g.data(), proj.data(), T);
+    esm::kernels::ResidualAddInplace(hidden.data(), proj.data(), Td);
+  }
+  esm::kernels::LayerNorm(hidden.data(), r->final_ln_w.data(), r->final_ln_b.data(), c.eps, ln.data(), T, d);
+  esm::kernels::Linear(ln.data(), r->lm_dense_w.data(), r->lm_dense_b.data(), proj.data(), T, d, d);
+  esm::kernels::Gelu(proj.data(), attn.data(), Td);
+  esm::kernels::LayerNorm(attn.data(), r->lm_ln_w.data(), r->lm_ln_b.data(), c.eps, ln.data(), T, d);
+  esm::kernels::Linear(ln.data(), r->embed.data(), r->dec_b.data(), logits, T, V, d);
+  return 0;
+}
+
+}  // extern "C"

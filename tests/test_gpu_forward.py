@@ -1,0 +1,134 @@
+"""Packed ESM-2 forward on gfx950 against the restated CPU forward.
+
+* Config 1 (8M, all fp32): logits within rtol = atol = 1e-5 of the oracle.
+* W8A8 (650M-shaped layers): per-tensor mode (the reference's dynamic
+  activation scale) and per-token mode against the oracle's same-mode
+  forward, logit correlation >= 0.9999 and argmax agreement; exact fp32
+  attention (attention_fp32) and the bf16/fp16 MFMA attention both.
+* Packed == serial (tests/python/test_forward_packed.py:42-69), per-sequence
+  token-dropout scale (:85-117), cu_seqlens validation (:120-128), zero
+  arena growth for a smaller batch (:131-149).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+import esm_gfx950 as eg
+from esm_gfx950 import synthetic as syn
+
+
+def corr(a, b):
+    a = a.ravel().astype(np.float64)
+    b = b.ravel().astype(np.float64)
+    return float(np.corrcoef(a, b)[0, 1])
+
+
+@pytest.fixture(scope="module")
+def w8m():
+    return syn.make_weights(syn.ESM2_8M, seed=20261201 + 1, int8=False)
+
+
+@pytest.fixture(scope="module")
+def w650_small():
+    cfg = syn.ESM2_650M.with_layers(2)
+    return syn.make_weights(cfg, seed=20261201 + 4, int8=True, keep_f32_linears=False)
+
+
+@pytest.fixture(scope="module")
+def small_batch():
+    return syn.batch_from_lengths([130, 61, 250, 2, 97, 200], seed=7)
+
+
+def test_config1_fp32_forward(dev, oracle, w8m):
+    batch = syn.config1_batch()
+    m = eg.Model(dev, w8m, int8=False)
+    got = m.forward_packed(batch.ids, batch.cu)
+    want = oracle.forward_packed(w8m, batch, int8=False, per_token=False)
+    m.free()
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+@pytest.mark.parametrize("attn_fp32", [True, False])
+def test_w8a8_forward_vs_oracle(dev, oracle, w650_small, small_batch, per_token, attn_fp32):
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w650_small, int8=True, act_mode=mode, attention_fp32=attn_fp32)
+    got = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.free()
+    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token)
+    assert np.all(np.isfinite(got))
+    c = corr(got, want)
+    agree = float(np.mean(np.argmax(got, 1) == np.argmax(want, 1)))
+    assert c >= 0.9999, c
+    assert agree >= 0.99, agree
+
+
+def test_packed_equals_serial(dev, w650_small, small_batch):
+    """Per-token mode keeps every row independent, so packing changes nothing."""
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    packed = m.forward_packed(small_batch.ids, small_batch.cu)
+    cu = small_batch.cu
+    for b in range(len(cu) - 1):
+        ids = small_batch.ids[cu[b]:cu[b + 1]]
+        solo = m.forward_packed(ids, np.array([0, len(ids)], np.int32))
+        np.testing.assert_allclose(packed[cu[b]:cu[b + 1]], solo, rtol=1e-4, atol=1e-4)
+    m.free()
+
+
+def test_token_dropout_scale(dev, oracle, w8m):
+    """Mask tokens zero their row and rescale their own sequence only."""
+    a = syn.batch_from_lengths([40, 30, 50], seed=9)
+    ids = a.ids.copy()
+    ids[3:9] = syn.MASK  # 6 masks in sequence 0
+    ids[a.cu[2] + 5] = syn.MASK  # 1 mask in sequence 2
+    batch = syn.PackedBatch(ids, a.cu, a.lengths)
+    m = eg.Model(dev, w8m, int8=False)
+    got = m.forward_packed(batch.ids, batch.cu)
+    m.free()
+    want = oracle.forward_packed(w8m, batch, int8=False, per_token=False)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_batch_validation(dev, w8m):
+    m = eg.Model(dev, w8m, int8=False)
+    ids = np.full(10, 5, np.int32)
+    with pytest.raises(eg.Gfx950Error, match="cu_seqlens\\[0\\] must be 0"):
+        m.forward_packed(ids, np.array([1, 10], np.int32))
+    with pytest.raises(eg.Gfx950Error, match="must equal packed_ids.size"):
+        m.forward_packed(ids, np.array([0, 4, 9], np.int32))
+    with pytest.raises(eg.Gfx950Error, match="non-decreasing"):
+        m.forward_packed(ids, np.array([0, 6, 4, 10], np.int32))
+    bad = ids.copy()
+    bad[3] = 40
+    with pytest.raises(eg.Gfx950Error, match="out of range"):
+        m.forward_packed(bad, np.array([0, 10], np.int32))
+    m.free()
+
+
+def test_arena_zero_growth(dev, w650_small, small_batch):
+    m = eg.Model(dev, w650_small, int8=True)
+    m.forward_packed(small_batch.ids, small_batch.cu)
+    before = m.arena_bytes()
+    sub = small_batch.subset([0, 1, 3])
+    m.forward_packed(sub.ids, sub.cu)
+    m.forward_packed(small_batch.ids, small_batch.cu)
+    assert m.arena_bytes() == before
+    m.free()
+
+
+def test_config4_varlen_full_forward_properties(dev):
+    """650M W8A8, the 256-sequence varlen batch: finite logits, and packed
+    == serial for sampled sequences (per-token mode)."""
+    w = syn.make_weights(syn.ESM2_650M, seed=20261201 + 4, int8=True)
+    batch = syn.config4_varlen_batch()
+    m = eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    logits = m.forward_packed(batch.ids, batch.cu)
+    assert logits.shape == (batch.total_tokens, 33)
+    assert np.all(np.isfinite(logits))
+    for b in (0, 17, int(np.argmax(batch.lengths)), 255):
+        s0, s1 = int(batch.cu[b]), int(batch.cu[b + 1])
+        solo = m.forward_packed(batch.ids[s0:s1], np.array([0, s1 - s0], np.int32))
+        np.testing.assert_allclose(logits[s0:s1], solo, rtol=1e-4, atol=1e-4)
+    m.free()

@@ -1,0 +1,142 @@
+"""W8A8 INT8 GEMM on gfx950 against the CPU oracle.
+
+Bar: int32 accumulators bit-exact (closed form sum_k a*w); dequant epilogue
+bit-exact (same fmaf expression); GELU epilogue within 1e-5 (device erff vs
+host erff).
+"""
+import numpy as np
+import pytest
+
+from conftest import rng
+
+pytestmark = pytest.mark.gpu
+
+import esm_gfx950 as eg
+
+
+def _pad(a, ld):
+    out = np.zeros((a.shape[0], ld), a.dtype)
+    out[:, :a.shape[1]] = a
+    return out
+
+
+def _i8(r, shape):
+    return r.integers(-127, 128, size=shape, dtype=np.int8)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (1, 16, 16), (37, 64, 64), (5, 9, 17), (130, 260, 48), (300, 1280, 1280), (257, 3840, 1280),
+    (129, 1280, 5120), (64, 5120, 1280), (31, 2560, 10240),
+])
+def test_int32_bit_exact(dev, oracle, M, N, K):
+    r = rng(1000 + M + N + K)
+    A = _i8(r, (M, K))
+    W = _i8(r, (N, K))
+    lda = (K + 15) // 16 * 16
+    w = dev.weight_i8(W, np.ones(N, np.float32))
+    dA = dev.array(_pad(A, lda))
+    dC = dev.empty((M, N), np.int32)
+    dev.gemm_i8_i32(dA, lda, w, M, dC)
+    got = dC.numpy()
+    want = oracle.gemm_i8_i32(A, W)
+    assert np.array_equal(got, want)
+    w.free()
+
+
+def test_int32_extremes(dev, oracle):
+    # All +-127 / -127 operands: the largest |acc| a K=5120 product can form.
+    M, N, K = 64, 128, 5120
+    A = np.full((M, K), 127, np.int8)
+    A[1::2] = -127
+    W = np.full((N, K), -127, np.int8)
+    W[::3] = 127
+    w = dev.weight_i8(W, np.ones(N, np.float32))
+    dA = dev.array(A)
+    dC = dev.empty((M, N), np.int32)
+    dev.gemm_i8_i32(dA, K, w, M, dC)
+    assert np.array_equal(dC.numpy(), oracle.gemm_i8_i32(A, W))
+    w.free()
+
+
+def test_config3_full_size_rows(dev, oracle):
+    """Config 3 shape [30700 x 1280] x [5120 x 1280]^T: int32 bit-exact on a
+    row sample, dequant+bias+GELU within 1e-5 on the same rows."""
+    M, N, K = 30700, 5120, 1280
+    r = rng(3)
+    A = _i8(r, (M, K))
+    W = _i8(r, (N, K))
+    a_scale = r.uniform(0.005, 0.05, size=M).astype(np.float32)
+    w_scale = r.uniform(0.005, 0.05, size=N).astype(np.float32)
+    bias = (r.standard_normal(N) * 0.02).astype(np.float32)
+    w = dev.weight_i8(W, w_scale)
+    dA = dev.array(A)
+    dC = dev.empty((M, N), np.int32)
+    dev.gemm_i8_i32(dA, K, w, M, dC)
+    acc = dC.numpy()
+    rows = np.unique(np.concatenate([r.choice(M, 48, replace=False), [0, M - 1, 30591, 30592]]))
+    want = oracle.gemm_i8_i32(A[rows], W)
+    assert np.array_equal(acc[rows], want)
+
+    ds = dev.array(a_scale)
+    db = dev.array(bias)
+    dY = dev.empty((M, N), np.float32)
+    dev.linear_i8_q(dA, K, ds, w, db, dY, M, gelu=True)
+    y = dY.numpy()
+    ref = oracle.dequant(want, a_scale[rows], w_scale, bias, gelu=True)
+    np.testing.assert_allclose(y[rows], ref, rtol=1e-5, atol=1e-5)
+    # dequant without GELU is the same fmaf on both sides: bit-exact
+    dev.linear_i8_q(dA, K, ds, w, db, dY, M, gelu=False)
+    y0 = dY.numpy()
+    assert np.array_equal(y0[rows], oracle.dequant(want, a_scale[rows], w_scale, bias, gelu=False))
+    w.free()
+
+
+@pytest.mark.parametrize("mode", [eg.ACT_PER_TENSOR, eg.ACT_PER_TOKEN])
+@pytest.mark.parametrize("M,N,K", [(18, 1280, 1280), (96, 320, 320), (257, 5120, 1280), (64, 1280, 5120), (7, 33, 17)])
+def test_linear_int8_facade(dev, oracle, mode, M, N, K):
+    """esm_gfx950_linear_i8 == oracle quant -> int32 GEMM -> dequant, bit-exact."""
+    r = rng(77 + M + N + K + mode)
+    A = r.uniform(-1, 1, size=(M, K)).astype(np.float32)
+    Wf = r.uniform(-1, 1, size=(N, K)).astype(np.float32)
+    q, s = oracle.quantize_weight(Wf)
+    bias = r.uniform(-1, 1, size=N).astype(np.float32)
+    w = dev.weight_i8(q, s)
+    dA, db, dC = dev.array(A), dev.array(bias), dev.empty((M, N), np.float32)
+    dev.linear_i8(dA, w, db, dC, M, N, K, mode)
+    got = dC.numpy()
+    if mode == eg.ACT_PER_TENSOR:
+        aq, sc = oracle.quant_act_tensor(A)
+        scales = np.full(M, sc, np.float32)
+    else:
+        aq, scales = oracle.quant_act_rows(A)
+    want = oracle.dequant(oracle.gemm_i8_i32(aq, q), scales, s, bias)
+    assert np.array_equal(got, want)
+    w.free()
+
+
+def test_linear_int8_zero_sizes(dev):
+    """M, N or K <= 0 zeroes C (reference gemm_int8.cpp:513-520)."""
+    w = dev.weight_i8(np.ones((4, 16), np.int8), np.ones(4, np.float32))
+    dC = dev.array(np.full((3, 4), 5.0, np.float32))
+    dA = dev.array(np.ones((3, 16), np.float32))
+    dev.linear_i8(dA, w, None, dC, 3, 4, 0, eg.ACT_PER_TENSOR)
+    assert np.all(dC.numpy() == 0.0)
+    w.free()
+
+
+@pytest.mark.parametrize("mode", [eg.ACT_PER_TENSOR, eg.ACT_PER_TOKEN])
+def test_quantize_act(dev, oracle, mode):
+    r = rng(5 + mode)
+    M, K = 333, 1280
+    x = (r.standard_normal((M, K)) * r.uniform(0.1, 10, size=(M, 1))).astype(np.float32)
+    x[7] = 0.0  # all-zero row: per-token scale 1
+    ldq = K
+    dx, dq, ds = dev.array(x), dev.empty((M, ldq), np.int8), dev.empty((M,), np.float32)
+    dev.quantize_act(dx, M, K, mode, dq, ldq, ds)
+    if mode == eg.ACT_PER_TENSOR:
+        q, s = oracle.quant_act_tensor(x)
+        s = np.full(M, s, np.float32)
+    else:
+        q, s = oracle.quant_act_rows(x)
+    assert np.array_equal(dq.numpy(), q)
+    assert np.array_equal(ds.numpy(), s)
