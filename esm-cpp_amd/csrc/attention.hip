@@ -9,9 +9,9 @@
 //
 // MFMA path (head_dim 64): one workgroup per (sequence, head, 128-query
 // tile); its four waves each own 32 queries. Keys are processed in chunks
-// of 128 staged through LDS: K row-major (bf16), V transposed to [dim][key]
-// and converted to fp16. Each wave computes S^T = K Q^T with
-// v_mfma_f32_16x16x32_bf16, so every lane ends up holding probabilities for
+// of 128 staged through LDS: K row-major (bf16 or fp16), V transposed to
+// [dim][key] and converted to fp16. Each wave computes S^T = K Q^T with
+// v_mfma_f32_16x16x32_{bf16,f16}, so every lane ends up holding probabilities for
 // one query and four consecutive keys per 16-key block -- exactly the B
 // operand layout of O^T = V^T P^T on v_mfma_f32_16x16x32_f16. Softmax is an
 // online (running max / running sum) fp32 softmax in base 2; the
@@ -38,7 +38,27 @@ __device__ __forceinline__ uint16_t bf16_to_f16_bits(uint16_t b) {
   return f32_to_f16_bits(bf16_bits_to_f32(b));
 }
 
-template <bool V_BF16>
+// Q/K operand type of S^T = K Q^T: bf16 (v_mfma_f32_16x16x32_bf16) or fp16
+// (v_mfma_f32_16x16x32_f16), same rate; fp16 carries three more mantissa
+// bits for the O(1) values attention sees.
+template <bool F16>
+struct QKOps;
+template <>
+struct QKOps<false> {
+  using vec = bf16x8;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct QKOps<true> {
+  using vec = f16x8;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <bool QK_F16, bool V_BF16>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int ld, const int* __restrict__ cu,
@@ -57,14 +77,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   const int qbase = w.q0 + wave * 32;
   const bool active = qbase < L;  // wave-uniform
 
-  bf16x8 qf[2][2];
+  using QK = QKOps<QK_F16>;
+  using qvec = typename QK::vec;
+  qvec qf[2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     int qi = qbase + qb * 16 + lr;
     qi = qi < L ? qi : L - 1;
     const uint16_t* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
-    qf[qb][0] = *reinterpret_cast<const bf16x8*>(qp + lg * 8);
-    qf[qb][1] = *reinterpret_cast<const bf16x8*>(qp + 32 + lg * 8);
+    qf[qb][0] = *reinterpret_cast<const qvec*>(qp + lg * 8);
+    qf[qb][1] = *reinterpret_cast<const qvec*>(qp + 32 + lg * 8);
   }
 
   f32x4 o[2][4];
@@ -120,12 +142,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     for (int kb = 0; kb < 8; ++kb) {
       if (kb < nkb) {
         const uint8_t* kp = sK + (kb * 16 + lr) * kKPitch + lg * 16;
-        const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(kp);
-        const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(kp + 64);
+        const qvec k0 = *reinterpret_cast<const qvec*>(kp);
+        const qvec k1 = *reinterpret_cast<const qvec*>(kp + 64);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-          f32x4 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          s[kb][qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[qb][1], acc, 0, 0, 0);
+          f32x4 acc = QK::mma(k0, qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+          s[kb][qb] = QK::mma(k1, qf[qb][1], acc);
         }
       }
     }
@@ -275,19 +297,22 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
 }  // namespace
 
 hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
-                                 const uint16_t* v, int v_is_bf16, int ld,
-                                 const int* cu_seqlens, const AttnWork* work,
-                                 int num_work, float* out, int ld_out,
-                                 float* tensor_absmax, hipStream_t s) {
+                                 const uint16_t* v, int qk_is_fp16, int v_is_bf16,
+                                 int ld, const int* cu_seqlens,
+                                 const AttnWork* work, int num_work, float* out,
+                                 int ld_out, float* tensor_absmax,
+                                 hipStream_t s) {
   if (num_work <= 0) return hipSuccess;
   const dim3 grid(num_work), block(256);
-  if (v_is_bf16) {
-    hipLaunchKernelGGL(attn_mfma_kernel<true>, grid, block, 0, s, q, k, v, ld,
-                       cu_seqlens, work, out, ld_out, tensor_absmax);
+#define ESM_ATTN_LAUNCH(QF, VB)                                                  \
+  hipLaunchKernelGGL((attn_mfma_kernel<QF, VB>), grid, block, 0, s, q, k, v, ld, \
+                     cu_seqlens, work, out, ld_out, tensor_absmax)
+  if (qk_is_fp16) {
+    if (v_is_bf16) ESM_ATTN_LAUNCH(true, true); else ESM_ATTN_LAUNCH(true, false);
   } else {
-    hipLaunchKernelGGL(attn_mfma_kernel<false>, grid, block, 0, s, q, k, v, ld,
-                       cu_seqlens, work, out, ld_out, tensor_absmax);
+    if (v_is_bf16) ESM_ATTN_LAUNCH(false, true); else ESM_ATTN_LAUNCH(false, false);
   }
+#undef ESM_ATTN_LAUNCH
   return hipGetLastError();
 }
 

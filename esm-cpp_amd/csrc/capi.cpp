@@ -35,10 +35,11 @@ struct esm_gfx950_ctx {
   // Op-level scratch (grown on demand; the forward uses its own arena).
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
-  // Per-kernel timing of forward sites.
-  std::string timing_site;
+  // Per-site kernel timing: each timed launch is bracketed by two events
+  // recorded on the context stream; site_of[i] names the launch's site.
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> events;
+  std::vector<std::string> site_of;
   size_t events_used = 0;
 
   int fail(int code, const std::string& msg) {
@@ -65,22 +66,18 @@ struct esm_gfx950_ctx {
     *out = scratch;
     return ESM_GFX950_OK;
   }
-  bool site_timed(const char* site) const {
-    if (!timing) return false;
-    if (timing_site == site) return true;
-    return timing_site == "all_i8_gemm" && std::strcmp(site, "attention") != 0 &&
-           std::strcmp(site, "lm_dense") != 0;
-  }
   int time_begin(const char* site, int* slot) {
     *slot = -1;
-    if (!site_timed(site)) return ESM_GFX950_OK;
+    if (!timing) return ESM_GFX950_OK;
     if (events_used == events.size()) {
       hipEvent_t a, b;
       if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
         return fail(ESM_GFX950_HIP_ERROR, "hipEventCreate failed");
       events.emplace_back(a, b);
+      site_of.emplace_back();
     }
     *slot = static_cast<int>(events_used++);
+    site_of[*slot] = site;
     hipError_t e = hipEventRecord(events[*slot].first, stream);
     if (e != hipSuccess) return hip_fail("hipEventRecord", e);
     return ESM_GFX950_OK;
@@ -286,25 +283,28 @@ extern "C" int esm_gfx950_timer_stop(esm_gfx950_ctx* ctx, float* elapsed_ms) {
   return ESM_GFX950_OK;
 }
 
-extern "C" int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, const char* site, int enable) {
+extern "C" int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, int enable) {
   if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  ctx->timing = enable != 0 && site != nullptr;
-  ctx->timing_site = site ? site : "";
+  ctx->timing = enable != 0;
   ctx->events_used = 0;
   return ESM_GFX950_OK;
 }
 
-extern "C" int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, int* launches, double* total_ms) {
-  if (!ctx || !launches || !total_ms) return ESM_GFX950_INVALID_ARGUMENT;
+extern "C" int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, const char* site, int* launches,
+                                              double* total_ms) {
+  if (!ctx || !site || !launches || !total_ms) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   double sum = 0.0;
+  int n = 0;
   for (size_t i = 0; i < ctx->events_used; ++i) {
+    if (ctx->site_of[i] != site) continue;
     float ms = 0.f;
     ESM_HIP(ctx, hipEventElapsedTime(&ms, ctx->events[i].first, ctx->events[i].second));
     sum += ms;
+    ++n;
   }
-  *launches = static_cast<int>(ctx->events_used);
+  *launches = n;
   *total_ms = sum;
   return ESM_GFX950_OK;
 }
@@ -573,7 +573,7 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
   ESM_HIP(ctx, launch_cast_f32(q, n, qb, 1, ctx->stream));
   ESM_HIP(ctx, launch_cast_f32(k, n, kb, 1, ctx->stream));
   ESM_HIP(ctx, launch_cast_f32(v, n, vb, 0, ctx->stream));
-  ESM_HIP(ctx, launch_attention_mfma(qb, kb, vb, 0, ld, d_cu, d_work, nwork, out, ld, nullptr, ctx->stream));
+  ESM_HIP(ctx, launch_attention_mfma(qb, kb, vb, 0, 0, ld, d_cu, d_work, nwork, out, ld, nullptr, ctx->stream));
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
 }
@@ -594,7 +594,7 @@ extern "C" int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint1
   const int ld = num_heads * kHeadDimMfma;
   int slot;
   ESM_TRY(ctx->time_begin("attention", &slot));
-  ESM_HIP(ctx, launch_attention_mfma(q, k, v, v_is_fp16 ? 0 : 1, ld, d_cu, d_work, nwork, out, ld, nullptr,
+  ESM_HIP(ctx, launch_attention_mfma(q, k, v, 0, v_is_fp16 ? 0 : 1, ld, d_cu, d_work, nwork, out, ld, nullptr,
                                      ctx->stream));
   ESM_TRY(ctx->time_end(slot));
   return ESM_GFX950_OK;
@@ -639,6 +639,8 @@ struct esm_gfx950_model {
   size_t meta_bytes = 0;
   hipEvent_t meta_done = nullptr;
   int rope_len = 0;  // rows currently in the device rope tables
+  // The staged batch (esm_gfx950_batch_upload).
+  int staged_T = 0, staged_B = 0, staged_work = 0;
 };
 
 namespace {
@@ -721,11 +723,13 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   ESM_REQUIRE(ctx, c.head_dim % 2 == 0 && c.head_dim <= 128, "model_create: head_dim must be even and <= 128");
   ESM_REQUIRE(ctx, c.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR || c.act_quant_mode == ESM_GFX950_ACT_PER_TOKEN,
               "model_create: unknown act_quant_mode");
+  ESM_REQUIRE(ctx, c.attention_mode >= ESM_GFX950_ATTN_MODE_FP16 && c.attention_mode <= ESM_GFX950_ATTN_MODE_FP32,
+              "model_create: unknown attention_mode");
   if (c.weights_int8) {
     ESM_REQUIRE(ctx, c.hidden_size % 16 == 0 && c.intermediate_size % 16 == 0,
                 "model_create: W8A8 needs hidden and intermediate sizes divisible by 16");
-    ESM_REQUIRE(ctx, c.attention_fp32 || c.head_dim == kHeadDimMfma,
-                "model_create: MFMA attention needs head_dim 64 (set attention_fp32)");
+    ESM_REQUIRE(ctx, (c.attention_mode == ESM_GFX950_ATTN_MODE_FP32) || c.head_dim == kHeadDimMfma,
+                "model_create: MFMA attention needs head_dim 64 (use ESM_GFX950_ATTN_MODE_FP32)");
     ESM_REQUIRE(ctx, c.hidden_size % 4 == 0 && c.hidden_size <= 2560,
                 "model_create: fused LayerNorm+quant supports hidden_size % 4 == 0 and <= 2560");
   }
@@ -835,7 +839,7 @@ Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
   a.qb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.kb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.vb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
-  const bool need_qkv_f32 = !c.weights_int8 || c.attention_fp32;
+  const bool need_qkv_f32 = !c.weights_int8 || (c.attention_mode == ESM_GFX950_ATTN_MODE_FP32);
   a.qkv = reinterpret_cast<float*>(take(need_qkv_f32 ? Ts * 3 * d * 4 : 0));
   a.attn = reinterpret_cast<float*>(take(Ts * d * 4));
   a.inter = reinterpret_cast<float*>(take(Ts * f * 4));
@@ -917,7 +921,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.w_scale = L.qkv.ws;
   g.bias = L.qkv.bias;
   ESM_TRY(ctx->time_begin("qkv", &slot));
-  if (c.attention_fp32) {
+  if ((c.attention_mode == ESM_GFX950_ATTN_MODE_FP32)) {
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
@@ -930,6 +934,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     g.rope_cos = md.cos_t;
     g.rope_sin = md.sin_t;
     g.q_scale = q_scale;
+    g.qk_fp16 = c.attention_mode == ESM_GFX950_ATTN_MODE_FP16 ? 1 : 0;
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvRope, s));
   }
   ESM_TRY(ctx->time_end(slot));
@@ -938,14 +943,15 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   float* amax_attn = tok ? nullptr : a.absmax + 1;
   if (!tok) ESM_HIP(ctx, launch_fill_f32(a.absmax + 1, 1, 0.0f, s));
   ESM_TRY(ctx->time_begin("attention", &slot));
-  if (c.attention_fp32) {
+  if ((c.attention_mode == ESM_GFX950_ATTN_MODE_FP32)) {
     ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
     ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
     ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d,
                                       s));
     if (!tok) ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
   } else {
-    ESM_HIP(ctx, launch_attention_mfma(a.qb, a.kb, a.vb, 0, d, md.cu, md.work, nwork, a.attn, d, amax_attn, s));
+    const int qk16 = c.attention_mode == ESM_GFX950_ATTN_MODE_FP16 ? 1 : 0;
+    ESM_HIP(ctx, launch_attention_mfma(a.qb, a.kb, a.vb, qk16, 0, d, md.cu, md.work, nwork, a.attn, d, amax_attn, s));
   }
   ESM_TRY(ctx->time_end(slot));
   if (tok) {
@@ -1066,14 +1072,15 @@ constexpr float kTokenDropoutMaskRatioTrain = 0.15f * 0.8f;
 
 }  // namespace
 
-extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
-                                         const int32_t* cu, int B, int T, float* logits, int logits_on_device) {
+extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                       const int32_t* cu, int B, int T) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_TRY(validate_batch(ctx, cu, B, T));
   const auto& c = m->cfg;
+  m->staged_T = 0;
   if (T == 0) return ESM_GFX950_OK;
-  ESM_REQUIRE(ctx, ids && logits, "forward_packed: null ids or logits");
-  const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
+  ESM_REQUIRE(ctx, ids, "batch_upload: null ids");
+  const int V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
   for (int t = 0; t < T; ++t)
     if (ids[t] < 0 || ids[t] >= V)
       return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_packed: token id out of range at " + std::to_string(t));
@@ -1102,9 +1109,7 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
     m->cap_L = nL;
     m->rope_len = 0;
   }
-  const Arena a = layout(c, m->cap_T, static_cast<char*>(m->arena));
   const Meta mh = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_host));
-  const Meta md = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_dev));
 
   // Host metadata: ids, per-token embedding scale (Embed, model.cpp:737-778),
   // positions, cu_seqlens, attention work list, rope tables.
@@ -1122,7 +1127,7 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   }
   build_pos(cu, B, mh.pos);
   std::memcpy(mh.cu, cu, static_cast<size_t>(B + 1) * 4);
-  const bool mfma_attn = c.weights_int8 && !c.attention_fp32;
+  const bool mfma_attn = c.weights_int8 && !(c.attention_mode == ESM_GFX950_ATTN_MODE_FP32);
   std::vector<AttnWork> work;
   build_work(cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
   std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));
@@ -1133,7 +1138,22 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
                               ctx->stream));
   ESM_HIP(ctx, hipEventRecord(m->meta_done, ctx->stream));
   if (new_tables) m->rope_len = m->cap_L;
-  const int nwork = static_cast<int>(work.size());
+  m->staged_T = T;
+  m->staged_B = B;
+  m->staged_work = static_cast<int>(work.size());
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* m, float* logits) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  const auto& c = m->cfg;
+  const int T = m->staged_T;
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, logits, "forward_device: null logits");
+  const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
+  const Arena a = layout(c, m->cap_T, static_cast<char*>(m->arena));
+  const Meta md = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_dev));
+  const int nwork = m->staged_work;
 
   hipStream_t s = ctx->stream;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
@@ -1162,11 +1182,21 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   dec.bias = m->dec_bias;
   dec.N = V;
   dec.K = d;
-  float* dst = logits_on_device ? logits : a.logits;
-  ESM_TRY(f32_linear(ctx, a.attn, dec, dst, T, kF32Store));
-  if (!logits_on_device) {
-    ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * V * 4, hipMemcpyDeviceToHost, s));
-    ESM_HIP(ctx, hipStreamSynchronize(s));
-  }
+  ESM_TRY(f32_linear(ctx, a.attn, dec, logits, T, kF32Store));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                         const int32_t* cu, int B, int T, float* logits, int logits_on_device) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(esm_gfx950_batch_upload(ctx, m, ids, cu, B, T));
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, logits, "forward_packed: null logits");
+  if (logits_on_device) return esm_gfx950_forward_device(ctx, m, logits);
+  const Arena a = layout(m->cfg, m->cap_T, static_cast<char*>(m->arena));
+  ESM_TRY(esm_gfx950_forward_device(ctx, m, a.logits));
+  ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * m->cfg.vocab_size * 4,
+                              hipMemcpyDeviceToHost, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
 }

@@ -10,25 +10,41 @@
 // a per-row activation scale, which equals the per-tensor scale when every
 // row carries the tensor's scale.
 //
-// Tiling: a 256-thread workgroup owns a 128x128 output tile; its four
-// waves (2x2) each own 64x64 = 4x4 MFMA blocks. K advances 128 bytes per
-// stage; A and W stages are staged through LDS (double-buffered) with a
-// 144-byte row pitch so the 16 rows read by one ds_read_b128 quarter-wave
-// land on disjoint banks. Tiles are ordered so each XCD (workgroup id mod
-// 8) walks a contiguous, M-grouped slice of the tile space, which keeps the
-// A rows and W columns it shares inside that XCD's L2.
+// Tiling (TileCfg): a 256-thread workgroup owns a 256x128 output tile; its
+// four waves (2x2) each own 128x64 = 8x4 MFMA blocks of 16x16, so a wave
+// reads 12 fragments (192 B per lane) from LDS per 32 MFMAs. K advances 64
+// bytes per stage; A and W stages go global -> registers -> LDS, double-
+// buffered, with an 80-byte row pitch so the 16 rows read by one
+// ds_read_b128 quarter-wave land on disjoint banks. 60 KB of LDS and <= 256
+// VGPRs per wave let two workgroups share a CU (two waves per SIMD), so one
+// wave's LDS reads and barrier overlap the other's MFMAs. Tiles are ordered
+// so each XCD (workgroup id mod 8) walks a contiguous, M-grouped slice of
+// the tile space, which keeps the A rows and W columns it shares inside
+// that XCD's L2.
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace esm_gfx950 {
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int BK = 128;            // bytes of K per stage
-constexpr int kPitch = BK + 16;    // LDS row pitch in bytes
-constexpr int kThreads = 256;
-constexpr int kStage = (BM + BN) * kPitch;
+template <int WAVES_M_, int WAVES_N_, int WM_, int WN_, int BK_>
+struct TileCfg {
+  static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+  static constexpr int WM = WM_, WN = WN_;  // 16x16 MFMA blocks per wave
+  static constexpr int BM = WAVES_M * WM * 16;
+  static constexpr int BN = WAVES_N * WN * 16;
+  static constexpr int BK = BK_;            // bytes of K per stage
+  static constexpr int THREADS = WAVES_M * WAVES_N * 64;
+  static constexpr int PITCH = BK + 16;     // LDS row pitch in bytes
+  static constexpr int STAGE = (BM + BN) * PITCH;
+  static constexpr int CHUNKS = BK / 16;    // 16-byte chunks per staged row
+  static constexpr int A_LOADS = BM * CHUNKS / THREADS;
+  static constexpr int B_LOADS = BN * CHUNKS / THREADS;
+  static_assert(BM * CHUNKS % THREADS == 0 && BN * CHUNKS % THREADS == 0, "tile/threads mismatch");
+  static_assert(BK % 64 == 0, "BK must be a multiple of the MFMA K (64)");
+};
+
+using Cfg = TileCfg<2, 2, 8, 4, 64>;  // 256 x 128 tile, waves of 128 x 64
 constexpr int kGroupM = 8;
 
 __device__ __forceinline__ int xcd_remap(int id, int num) {
@@ -38,18 +54,18 @@ __device__ __forceinline__ int xcd_remap(int id, int num) {
   return xcd * per + min(xcd, rem) + local;
 }
 
-// Global -> registers for one 128-row x 128-byte stage. Rows past the
-// matrix edge re-read the last valid row (results are discarded); K bytes
-// past the end read as zero.
-__device__ __forceinline__ void load_stage(const int8_t* __restrict__ base,
-                                           int ld, int rows, int row0, int k0,
-                                           int K, i32x4 (&r)[4]) {
+// Global -> registers for one stage of ROWS rows x C::BK bytes. Rows past
+// the matrix edge re-read the last valid row (results are discarded); K
+// bytes past the end read as zero.
+template <class C, int LOADS>
+__device__ __forceinline__ void load_stage(const int8_t* __restrict__ base, int ld, int rows, int row0,
+                                           int k0, int K, i32x4 (&r)[LOADS]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = t + kThreads * i;
-    const int row = idx >> 3;
-    const int c = (idx & 7) * 16;
+  for (int i = 0; i < LOADS; ++i) {
+    const int idx = t + C::THREADS * i;
+    const int row = idx / C::CHUNKS;
+    const int c = (idx % C::CHUNKS) * 16;
     int gr = row0 + row;
     gr = gr < rows ? gr : rows - 1;
     const int kk = k0 + c;
@@ -61,70 +77,71 @@ __device__ __forceinline__ void load_stage(const int8_t* __restrict__ base,
   }
 }
 
-__device__ __forceinline__ void store_stage(int8_t* s, const i32x4 (&r)[4]) {
+template <class C, int LOADS>
+__device__ __forceinline__ void store_stage(int8_t* s, const i32x4 (&r)[LOADS]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = t + kThreads * i;
-    const int row = idx >> 3;
-    const int c = (idx & 7) * 16;
-    *reinterpret_cast<i32x4*>(s + row * kPitch + c) = r[i];
+  for (int i = 0; i < LOADS; ++i) {
+    const int idx = t + C::THREADS * i;
+    *reinterpret_cast<i32x4*>(s + (idx / C::CHUNKS) * C::PITCH + (idx % C::CHUNKS) * 16) = r[i];
   }
 }
 
-template <int EPI>
+template <class C, int EPI>
 __device__ __forceinline__ void epilogue(const GemmI8Args& p,
-                                         const i32x4 (&acc)[4][4], int rb,
+                                         const i32x4 (&acc)[C::WM][C::WN], int rb,
                                          int cb, int lr, int lg) {
+  constexpr int WM = C::WM, WN = C::WN;
   if constexpr (EPI == kEpiI32) {
 #pragma unroll
-    for (int bm = 0; bm < 4; ++bm)
+    for (int bm = 0; bm < WM; ++bm)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = rb + bm * 16 + lg * 4 + r;
         if (row >= p.M) continue;
 #pragma unroll
-        for (int bn = 0; bn < 4; ++bn) {
+        for (int bn = 0; bn < WN; ++bn) {
           const int col = cb + bn * 16 + lr;
           if (col < p.N) p.C_i32[static_cast<size_t>(row) * p.ldc + col] = acc[bm][bn][r];
         }
       }
     return;
   } else {
-    float ws[4], bs[4];
+    float ws[WN], bs[WN];
 #pragma unroll
-    for (int bn = 0; bn < 4; ++bn) {
+    for (int bn = 0; bn < WN; ++bn) {
       const int col = cb + bn * 16 + lr;
       const bool ok = col < p.N;
       ws[bn] = ok ? p.w_scale[col] : 0.0f;
       bs[bn] = (ok && p.bias) ? p.bias[col] : 0.0f;
     }
     if constexpr (EPI == kEpiQkvRope) {
+      static_assert(WN == 4, "QKV epilogue needs 64-column (one head) waves");
       // The wave's 64 columns are exactly one head of Q, K or V. Lane
       // column lr of block bn holds head dim bn*16+lr, so the rotary pairs
       // (i, i+32) sit in blocks (0,2) and (1,3) of the same lane and row.
       const int which = cb / p.d_model;
       const int hcol = cb - which * p.d_model;
 #pragma unroll
-      for (int bm = 0; bm < 4; ++bm)
+      for (int bm = 0; bm < WM; ++bm)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = rb + bm * 16 + lg * 4 + r;
           if (row >= p.M) continue;
           const float as = p.a_scale[row];
-          float v[4];
+          float v[WN];
 #pragma unroll
-          for (int bn = 0; bn < 4; ++bn)
+          for (int bn = 0; bn < WN; ++bn)
             v[bn] = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
           const size_t o = static_cast<size_t>(row) * p.d_model + hcol + lr;
           if (which == 2) {
 #pragma unroll
-            for (int bn = 0; bn < 4; ++bn) p.v_out[o + bn * 16] = f32_to_f16_bits(v[bn]);
+            for (int bn = 0; bn < WN; ++bn) p.v_out[o + bn * 16] = f32_to_f16_bits(v[bn]);
             continue;
           }
           if (which == 0) {
 #pragma unroll
-            for (int bn = 0; bn < 4; ++bn) v[bn] *= p.q_scale;
+            for (int bn = 0; bn < WN; ++bn) v[bn] *= p.q_scale;
           }
           const int ps = p.pos[row];
           const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
@@ -137,14 +154,19 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
             v[h + 2] = x2 * ct[i + 32] + x1 * st[i + 32];
           }
           uint16_t* dst = which == 0 ? p.q_out : p.k_out;
+          if (p.qk_fp16) {
 #pragma unroll
-          for (int bn = 0; bn < 4; ++bn) dst[o + bn * 16] = f32_to_bf16_bits(v[bn]);
+            for (int bn = 0; bn < WN; ++bn) dst[o + bn * 16] = f32_to_f16_bits(v[bn]);
+          } else {
+#pragma unroll
+            for (int bn = 0; bn < WN; ++bn) dst[o + bn * 16] = f32_to_bf16_bits(v[bn]);
+          }
         }
       return;
     } else {
       float tmax = 0.0f;
 #pragma unroll
-      for (int bm = 0; bm < 4; ++bm)
+      for (int bm = 0; bm < WM; ++bm)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = rb + bm * 16 + lg * 4 + r;
@@ -152,7 +174,7 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
           const float as = rok ? p.a_scale[row] : 0.0f;
           float rmax = 0.0f;
 #pragma unroll
-          for (int bn = 0; bn < 4; ++bn) {
+          for (int bn = 0; bn < WN; ++bn) {
             const int col = cb + bn * 16 + lr;
             float v = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
             if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
@@ -190,87 +212,88 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads, 2) void gemm_i8_kernel(const GemmI8Args p) {
-  __shared__ __attribute__((aligned(16))) int8_t smem[2 * kStage];
+template <class C, int EPI>
+__global__ __launch_bounds__(C::THREADS, 2) void gemm_i8_kernel(const GemmI8Args p) {
+  __shared__ __attribute__((aligned(16))) int8_t smem[2 * C::STAGE];
 
-  const int tiles_m = (p.M + BM - 1) / BM;
-  const int tiles_n = (p.N + BN - 1) / BN;
+  const int tiles_m = (p.M + C::BM - 1) / C::BM;
+  const int tiles_n = (p.N + C::BN - 1) / C::BN;
   const int pid = xcd_remap(blockIdx.x, tiles_m * tiles_n);
   const int per_group = kGroupM * tiles_n;
   const int group = pid / per_group;
   const int first_m = group * kGroupM;
   const int gsize = min(tiles_m - first_m, kGroupM);
   const int in_group = pid - group * per_group;
-  const int m0 = (first_m + in_group % gsize) * BM;
-  const int n0 = (in_group / gsize) * BN;
+  const int m0 = (first_m + in_group % gsize) * C::BM;
+  const int n0 = (in_group / gsize) * C::BN;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
   const int lr = lane & 15, lg = lane >> 4;
 
-  i32x4 acc[4][4];
+  i32x4 acc[C::WM][C::WN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+    for (int j = 0; j < C::WN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
-  i32x4 ra[4], rb[4];
-  const int nk = (p.K + BK - 1) / BK;
-  load_stage(p.A, p.lda, p.M, m0, 0, p.K, ra);
-  load_stage(p.W, p.ldw, p.N, n0, 0, p.K, rb);
-  store_stage(smem, ra);
-  store_stage(smem + BM * kPitch, rb);
+  i32x4 ra[C::A_LOADS], rb[C::B_LOADS];
+  const int nk = (p.K + C::BK - 1) / C::BK;
+  load_stage<C>(p.A, p.lda, p.M, m0, 0, p.K, ra);
+  load_stage<C>(p.W, p.ldw, p.N, n0, 0, p.K, rb);
+  store_stage<C>(smem, ra);
+  store_stage<C>(smem + C::BM * C::PITCH, rb);
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
-    const int8_t* cur = smem + (kt & 1) * kStage;
+    const int8_t* cur = smem + (kt & 1) * C::STAGE;
     const bool more = kt + 1 < nk;
     if (more) {
-      load_stage(p.A, p.lda, p.M, m0, (kt + 1) * BK, p.K, ra);
-      load_stage(p.W, p.ldw, p.N, n0, (kt + 1) * BK, p.K, rb);
+      load_stage<C>(p.A, p.lda, p.M, m0, (kt + 1) * C::BK, p.K, ra);
+      load_stage<C>(p.W, p.ldw, p.N, n0, (kt + 1) * C::BK, p.K, rb);
     }
-    const int8_t* sa = cur + (wm * 64 + lr) * kPitch + lg * 16;
-    const int8_t* sb = cur + BM * kPitch + (wn * 64 + lr) * kPitch + lg * 16;
+    const int8_t* sa = cur + (wm * C::WM * 16 + lr) * C::PITCH + lg * 16;
+    const int8_t* sb = cur + C::BM * C::PITCH + (wn * C::WN * 16 + lr) * C::PITCH + lg * 16;
 #pragma unroll
-    for (int kk = 0; kk < BK / 64; ++kk) {
-      i32x4 fa[4], fb[4];
+    for (int kk = 0; kk < C::BK / 64; ++kk) {
+      i32x4 fa[C::WM], fb[C::WN];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i] = *reinterpret_cast<const i32x4*>(sa + i * 16 * kPitch + kk * 64);
-        fb[i] = *reinterpret_cast<const i32x4*>(sb + i * 16 * kPitch + kk * 64);
-      }
+      for (int j = 0; j < C::WN; ++j)
+        fb[j] = *reinterpret_cast<const i32x4*>(sb + j * 16 * C::PITCH + kk * 64);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < C::WM; ++i)
+        fa[i] = *reinterpret_cast<const i32x4*>(sa + i * 16 * C::PITCH + kk * 64);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+      for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      int8_t* nxt = smem + ((kt + 1) & 1) * kStage;
-      store_stage(nxt, ra);
-      store_stage(nxt + BM * kPitch, rb);
+      int8_t* nxt = smem + ((kt + 1) & 1) * C::STAGE;
+      store_stage<C>(nxt, ra);
+      store_stage<C>(nxt + C::BM * C::PITCH, rb);
     }
     __syncthreads();
   }
 
-  epilogue<EPI>(p, acc, m0 + wm * 64, n0 + wn * 64, lr, lg);
+  epilogue<C, EPI>(p, acc, m0 + wm * C::WM * 16, n0 + wn * C::WN * 16, lr, lg);
 }
 
 }  // namespace
 
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
-  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const dim3 grid(tiles), block(kThreads);
+  const int tiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
+  const dim3 grid(tiles), block(Cfg::THREADS);
   switch (epi) {
-    case kEpiI32: hipLaunchKernelGGL(gemm_i8_kernel<kEpiI32>, grid, block, 0, s, p); break;
-    case kEpiF32: hipLaunchKernelGGL(gemm_i8_kernel<kEpiF32>, grid, block, 0, s, p); break;
-    case kEpiF32Gelu: hipLaunchKernelGGL(gemm_i8_kernel<kEpiF32Gelu>, grid, block, 0, s, p); break;
-    case kEpiF32Resid: hipLaunchKernelGGL(gemm_i8_kernel<kEpiF32Resid>, grid, block, 0, s, p); break;
-    case kEpiQkvRope: hipLaunchKernelGGL(gemm_i8_kernel<kEpiQkvRope>, grid, block, 0, s, p); break;
-    case kEpiF32GeluQ: hipLaunchKernelGGL(gemm_i8_kernel<kEpiF32GeluQ>, grid, block, 0, s, p); break;
+    case kEpiI32: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiI32>), grid, block, 0, s, p); break;
+    case kEpiF32: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32>), grid, block, 0, s, p); break;
+    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32Gelu>), grid, block, 0, s, p); break;
+    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32Resid>), grid, block, 0, s, p); break;
+    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRope>), grid, block, 0, s, p); break;
+    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluQ>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

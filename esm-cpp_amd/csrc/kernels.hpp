@@ -37,9 +37,10 @@ struct GemmI8Args {
   float* row_absmax = nullptr;     // [M] (atomic max of |out|) or null
   float* tensor_absmax = nullptr;  // scalar (atomic max of |out|) or null
   // kEpiQkvRope
-  uint16_t* q_out = nullptr;  // bf16 [M, d_model]
-  uint16_t* k_out = nullptr;  // bf16 [M, d_model]
+  uint16_t* q_out = nullptr;  // bf16 or fp16 [M, d_model]
+  uint16_t* k_out = nullptr;  // bf16 or fp16 [M, d_model]
   uint16_t* v_out = nullptr;  // fp16 [M, d_model]
+  int qk_fp16 = 0;            // Q/K stored as fp16 (else bf16)
   int d_model = 0;
   const int* pos = nullptr;          // [M] position inside the sequence
   const float* rope_cos = nullptr;   // [max_len, 32]
@@ -76,14 +77,15 @@ struct AttnWork {
   int q0;
   int pad;
 };
-// bf16 Q/K (QK^T on bf16 MFMA), V as bf16 or fp16 (PV on fp16 MFMA with
-// fp16 probabilities), fp32 online softmax, head_dim 64.
+// Q/K bf16 or fp16 (QK^T on the matching MFMA), V bf16 or fp16 (PV on fp16
+// MFMA with fp16 probabilities), fp32 online softmax, head_dim 64.
 // q/k/v rows: token t, head h at base + t*ld + h*64.
 hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
-                                 const uint16_t* v, int v_is_bf16, int ld,
-                                 const int* cu_seqlens, const AttnWork* work,
-                                 int num_work, float* out, int ld_out,
-                                 float* tensor_absmax, hipStream_t s);
+                                 const uint16_t* v, int qk_is_fp16, int v_is_bf16,
+                                 int ld, const int* cu_seqlens,
+                                 const AttnWork* work, int num_work, float* out,
+                                 int ld_out, float* tensor_absmax,
+                                 hipStream_t s);
 // Exact fp32 path for any head_dim <= 128 (one thread per query).
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
                                 int ld, int head_dim, const int* cu_seqlens,

@@ -22,6 +22,9 @@ ACT_PER_TENSOR = 0
 ACT_PER_TOKEN = 1
 ATTN_FP32 = 0
 ATTN_BF16_MFMA = 1
+ATTN_MODE_FP16 = 0
+ATTN_MODE_BF16 = 1
+ATTN_MODE_FP32 = 2
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED = [
@@ -34,7 +37,8 @@ EXPORTED = [
     "esm_gfx950_residual_add", "esm_gfx950_scale", "esm_gfx950_rope_build_tables",
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
     "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
-    "esm_gfx950_forward_packed", "esm_gfx950_model_arena_bytes",
+    "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
+    "esm_gfx950_model_arena_bytes",
 ]
 
 
@@ -69,8 +73,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_memcpy_d2d": (i32, [vp, vp, vp, sz]),
         "esm_gfx950_timer_start": (i32, [vp]),
         "esm_gfx950_timer_stop": (i32, [vp, C.POINTER(f32)]),
-        "esm_gfx950_kernel_timing": (i32, [vp, C.c_char_p, i32]),
-        "esm_gfx950_kernel_timing_query": (i32, [vp, C.POINTER(i32), C.POINTER(C.c_double)]),
+        "esm_gfx950_kernel_timing": (i32, [vp, i32]),
+        "esm_gfx950_kernel_timing_query": (i32, [vp, C.c_char_p, C.POINTER(i32), C.POINTER(C.c_double)]),
         "esm_gfx950_weight_upload_i8": (i32, [vp, vp, vp, i32, i32, C.POINTER(vp)]),
         "esm_gfx950_weight_free": (i32, [vp, vp]),
         "esm_gfx950_gemm_i8_i32": (i32, [vp, vp, i32, vp, i32, vp]),
@@ -90,6 +94,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_model_free": (i32, [vp, vp]),
         "esm_gfx950_model_set_act_mode": (i32, [vp, vp, i32]),
         "esm_gfx950_forward_packed": (i32, [vp, vp, vp, vp, i32, i32, vp, i32]),
+        "esm_gfx950_batch_upload": (i32, [vp, vp, vp, vp, i32, i32]),
+        "esm_gfx950_forward_device": (i32, [vp, vp, vp]),
         "esm_gfx950_model_arena_bytes": (i32, [vp, C.POINTER(sz)]),
     }
     for name, (res, args) in sig.items():
@@ -208,12 +214,13 @@ class Device:
         self._check(self.lib.esm_gfx950_timer_stop(self.ctx, C.byref(ms)))
         return float(ms.value)
 
-    def kernel_timing(self, site: Optional[str], enable: bool = True):
-        self._check(self.lib.esm_gfx950_kernel_timing(self.ctx, site.encode() if site else None, int(enable)))
+    def kernel_timing(self, enable: bool = True):
+        self._check(self.lib.esm_gfx950_kernel_timing(self.ctx, int(enable)))
 
-    def kernel_timing_query(self):
+    def kernel_timing_query(self, site: str):
+        """(launches, total_ms) of the timed launches of `site` since enabling."""
         n, ms = C.c_int(), C.c_double()
-        self._check(self.lib.esm_gfx950_kernel_timing_query(self.ctx, C.byref(n), C.byref(ms)))
+        self._check(self.lib.esm_gfx950_kernel_timing_query(self.ctx, site.encode(), C.byref(n), C.byref(ms)))
         return int(n.value), float(ms.value)
 
     # ------------------------------------------------------------------ ops
@@ -273,7 +280,7 @@ class _ModelConfig(C.Structure):
     _fields_ = [("num_layers", C.c_int), ("hidden_size", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int),
                 ("intermediate_size", C.c_int), ("vocab_size", C.c_int), ("layer_norm_eps", C.c_float),
                 ("mask_token_id", C.c_int), ("weights_int8", C.c_int), ("act_quant_mode", C.c_int),
-                ("attention_fp32", C.c_int)]
+                ("attention_mode", C.c_int)]
 
 
 class _LinearDesc(C.Structure):
@@ -300,7 +307,8 @@ class Model:
     W8A8, the per-channel int8 packs).
     """
 
-    def __init__(self, dev: Device, weights, int8: bool, act_mode: int = ACT_PER_TOKEN, attention_fp32: bool = False):
+    def __init__(self, dev: Device, weights, int8: bool, act_mode: int = ACT_PER_TOKEN,
+                 attention_mode: int = ATTN_MODE_FP16):
         cfg = weights.cfg
         keep: List[np.ndarray] = []
 
@@ -332,7 +340,7 @@ class Model:
         desc = _ModelDesc()
         desc.cfg = _ModelConfig(cfg.num_layers, cfg.hidden_size, cfg.num_heads, cfg.head_dim, cfg.intermediate_size,
                                 cfg.vocab_size, cfg.layer_norm_eps, cfg.mask_token_id, int(int8), act_mode,
-                                int(attention_fp32))
+                                int(attention_mode))
         f = weights.f32
         desc.embed = p(f["embed"])
         desc.layers = layers
@@ -360,6 +368,17 @@ class Model:
         self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
                                                                len(cu) - 1, T, out.ptr, 1))
         return out
+
+    def upload_batch(self, ids: np.ndarray, cu: np.ndarray):
+        """Stages a packed batch in device memory (esm_gfx950_batch_upload)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        cu = np.ascontiguousarray(cu, np.int32)
+        self.dev._check(self.dev.lib.esm_gfx950_batch_upload(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
+                                                             len(cu) - 1, int(ids.shape[0])))
+
+    def forward_device(self, out: DeviceArray):
+        """Forward on the staged batch; logits stay on the device."""
+        self.dev._check(self.dev.lib.esm_gfx950_forward_device(self.dev.ctx, self.handle, out.ptr))
 
     def arena_bytes(self) -> int:
         n = C.c_size_t()

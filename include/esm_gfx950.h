@@ -55,6 +55,13 @@ enum { ESM_GFX950_ACT_PER_TENSOR = 0, ESM_GFX950_ACT_PER_TOKEN = 1 };
 /* Attention arithmetic for esm_gfx950_attention_varlen. */
 enum { ESM_GFX950_ATTN_FP32 = 0, ESM_GFX950_ATTN_BF16_MFMA = 1 };
 
+/* Attention inside the W8A8 forward. FP16 (default): the QKV epilogue
+ * writes Q/K/V as fp16 and QK^T runs on fp16 MFMA; BF16: Q/K as bf16 on
+ * bf16 MFMA; both keep fp16 P and V on fp16 MFMA and an fp32 softmax. FP32:
+ * Q/K/V stay fp32 and the exact fp32 kernel runs (the reference's
+ * arithmetic, for parity studies). */
+enum { ESM_GFX950_ATTN_MODE_FP16 = 0, ESM_GFX950_ATTN_MODE_BF16 = 1, ESM_GFX950_ATTN_MODE_FP32 = 2 };
+
 typedef struct esm_gfx950_ctx esm_gfx950_ctx;
 typedef struct esm_gfx950_weight esm_gfx950_weight;
 typedef struct esm_gfx950_model esm_gfx950_model;
@@ -83,13 +90,14 @@ int esm_gfx950_memcpy_d2d(esm_gfx950_ctx* ctx, void* dst, const void* src, size_
 int esm_gfx950_timer_start(esm_gfx950_ctx* ctx);
 int esm_gfx950_timer_stop(esm_gfx950_ctx* ctx, float* elapsed_ms);
 
-/* Per-kernel timing: while enabled, the launches of the named GEMM site
- * ("qkv", "out", "fc1", "fc2", "lm_dense", "attention" or "all_i8_gemm")
- * inside esm_gfx950_forward_packed are bracketed by HIP events on the
- * context stream. Query returns the number of launches and their summed
- * duration since the last reset. */
-int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, const char* site, int enable);
-int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, int* launches, double* total_ms);
+/* Per-kernel timing: while enabled, every launch of a timed site inside the
+ * forward -- "qkv", "attention", "out", "fc1", "fc2" (INT8 GEMMs and the
+ * attention kernel), "lm_dense" -- and of esm_gfx950_attention_varlen_bf16
+ * ("attention") is bracketed by HIP events on the context stream. Enabling
+ * (or disabling) resets the record; the query returns the number of timed
+ * launches of `site` and their summed duration. */
+int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, int enable);
+int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, const char* site, int* launches, double* total_ms);
 
 /* ------------------------------------------------------- weights (L2 pack)
  * Upload a per-channel symmetric INT8 weight: packed [N, K] int8 in
@@ -187,8 +195,7 @@ typedef struct {
   int mask_token_id;   /* 32 for ESM-2 (src/tokenizer.cpp:12-17) */
   int weights_int8;    /* 1: W8A8 layer linears; 0: fp32 layer linears */
   int act_quant_mode;  /* ESM_GFX950_ACT_PER_TENSOR / _PER_TOKEN */
-  int attention_fp32;  /* W8A8 models: 1 = fp32 Q/K/V + exact fp32 attention,
-                          0 = bf16 Q/K, fp16 V, MFMA attention (default) */
+  int attention_mode;  /* W8A8 models: ESM_GFX950_ATTN_MODE_* */
 } esm_gfx950_model_config;
 
 typedef struct {
@@ -230,10 +237,19 @@ int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, 
  * validated like BatchView (batch.cpp:8-46); masks are not supported (all
  * tokens real). logits fp32 [T, vocab] is written to DEVICE memory when
  * logits_on_device != 0, else to HOST memory (the call then synchronises).
+ * Equivalent to esm_gfx950_batch_upload + esm_gfx950_forward_device.
  * The device arena grows only when T exceeds every earlier batch. */
 int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                               const int32_t* cu_seqlens, int batch_size, int total_tokens,
                               float* logits, int logits_on_device);
+/* Stages a packed batch in the model's device buffers: ids, per-token
+ * embedding scale, in-sequence positions, cu_seqlens, the attention work
+ * list and the RoPE tables (one pinned host-to-device copy). */
+int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                            const int32_t* cu_seqlens, int batch_size, int total_tokens);
+/* Runs the forward on the staged batch with every input already in HBM;
+ * logits fp32 [T, vocab] go to DEVICE memory. Stream-ordered, no host sync. */
+int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, float* logits);
 /* Bytes currently held by the model's device arena (for zero-growth checks). */
 int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
 
