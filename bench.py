@@ -195,7 +195,7 @@ def main():
                                f"{len(batch.lengths)} sequences",
                    "tokens": T, "residues": residues, "sequences": int(len(batch.lengths)),
                    "act_quant": "per-token" if mode == eg.ACT_PER_TOKEN else "per-tensor",
-                   "attention": "bf16 QK^T / fp16 PV MFMA", "parallelism": "single GPU"},
+                   "attention": "split-fp16 (hi+lo, 3 MFMAs per product) fp32-accurate MFMA", "parallelism": "single GPU"},
         "tokens_per_s": round(T / (ms_plain * 1e-3), 1),
         "ms_per_step_with_kernel_events": round(ms_events, 3),
         "kernel_sites": sites,

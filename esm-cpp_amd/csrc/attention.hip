@@ -242,6 +242,240 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   }
 }
 
+// ---- Split-fp16 MFMA path (head_dim 64): fp32 accuracy on fp16 MFMA.
+//
+// Every fp32 operand x is carried as an unevaluated sum hi + lo of two fp16
+// values (hi = fp16(x), lo = fp16(x - hi), 22 significant bits together),
+// and each product uses three MFMAs: hi*hi + lo*hi + hi*lo (the dropped
+// lo*lo term is below 2^-22 relative). Q is multiplied by 8 before the
+// split (exact: a power of two) so the lo parts of the pre-scaled Q stay
+// normal fp16; the factor is folded back into the exp2 argument. Layout and
+// wave roles are those of the single-fp16 kernel above: S^T = K Q^T puts each
+// lane's probabilities in the B-operand layout of O^T = V^T P^T. The
+// running sum uses the fp32 probabilities, so the normalisation is that of
+// the reference's fp32/double softmax (attention.cpp:118-139).
+constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
+constexpr int kVPitchX = KC * 2 + 16;   // bytes per dim row of V^T hi / lo
+constexpr float kQPre = 8.0f;
+
+struct SplitH {
+  _Float16 hi, lo;
+};
+__device__ __forceinline__ SplitH split_f16(float x) {
+  const _Float16 h = static_cast<_Float16>(x);
+  return SplitH{h, static_cast<_Float16>(x - static_cast<float>(h))};
+}
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+__device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256, 2) void attn_x3_kernel(
+    const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int ld, const int* __restrict__ cu,
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
+  __shared__ __attribute__((aligned(16))) uint8_t sKh[KC * kKPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sKl[KC * kKPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sVh[64 * kVPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sVl[64 * kVPitchX];
+
+  const AttnWork w = work[blockIdx.x];
+  const int start = cu[w.seq];
+  const int L = cu[w.seq + 1] - start;
+  const int hoff = w.head * 64;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int qbase = w.q0 + wave * 32;
+  const bool active = qbase < L;  // wave-uniform
+
+  // Q fragments (B operand of S^T = K Q^T): lane (lr, lg) holds query lr of
+  // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8).
+  f16x8 qh[2][2], ql[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    int qi = qbase + qb * 16 + lr;
+    qi = qi < L ? qi : L - 1;
+    const float* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const float4 a = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8);
+      const float4 b = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8 + 4);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const SplitH sp = split_f16(x[j] * kQPre);
+        qh[qb][half][j] = sp.hi;
+        ql[qb][half][j] = sp.lo;
+      }
+    }
+  }
+
+  f32x4 o[2][4];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mrun[2] = {-INFINITY, -INFINITY};
+  float lrun[2] = {0.f, 0.f};
+  constexpr float kS2 = kLog2e / kQPre;
+
+  for (int kc0 = 0; kc0 < L; kc0 += KC) {
+    const int nkeys = min(KC, L - kc0);
+    __syncthreads();
+    // K chunk, split: KC keys x 16 float4 per key; rows past the sequence
+    // are zero.
+#pragma unroll
+    for (int i = 0; i < KC * 16 / 256; ++i) {
+      const int idx = tid + 256 * i;
+      const int key = idx >> 4, c4 = idx & 15;
+      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (key < nkeys)
+        x = *reinterpret_cast<const float4*>(k + static_cast<size_t>(start + kc0 + key) * ld + hoff + c4 * 4);
+      const SplitH a = split_f16(x.x), b = split_f16(x.y), c = split_f16(x.z), d = split_f16(x.w);
+      *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.hi, b.hi), pack_h2(c.hi, d.hi));
+      *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.lo, b.lo), pack_h2(c.lo, d.lo));
+    }
+    // V chunk, split and transposed to V^T[dim][key]: each item is a key
+    // pair x 4 dims.
+#pragma unroll
+    for (int i = 0; i < KC / 2 * 16 / 256; ++i) {
+      const int idx = tid + 256 * i;
+      const int dq = idx & 15, kp = idx >> 4;
+      const int key0 = 2 * kp;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+      const float* vp = v + static_cast<size_t>(start + kc0 + key0) * ld + hoff + dq * 4;
+      if (key0 < nkeys) a = *reinterpret_cast<const float4*>(vp);
+      if (key0 + 1 < nkeys) b = *reinterpret_cast<const float4*>(vp + ld);
+      const float xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const SplitH sa = split_f16(xa[j]), sb = split_f16(xb[j]);
+        const int off = (dq * 4 + j) * kVPitchX + key0 * 2;
+        *reinterpret_cast<uint32_t*>(sVh + off) = pack_h2(sa.hi, sb.hi);
+        *reinterpret_cast<uint32_t*>(sVl + off) = pack_h2(sa.lo, sb.lo);
+      }
+    }
+    __syncthreads();
+    if (!active) continue;
+
+    const int nkb = (nkeys + 15) >> 4;
+    f32x4 s[8][2];
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+      if (kb < nkb) {
+        const int off = (kb * 16 + lr) * kKPitchX + lg * 16;
+        const f16x8 kh0 = *reinterpret_cast<const f16x8*>(sKh + off);
+        const f16x8 kh1 = *reinterpret_cast<const f16x8*>(sKh + off + 64);
+        const f16x8 kl0 = *reinterpret_cast<const f16x8*>(sKl + off);
+        const f16x8 kl1 = *reinterpret_cast<const f16x8*>(sKl + off + 64);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          f32x4 acc = mma16(kh0, qh[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+          acc = mma16(kl0, qh[qb][0], acc);
+          acc = mma16(kh0, ql[qb][0], acc);
+          acc = mma16(kh1, qh[qb][1], acc);
+          acc = mma16(kl1, qh[qb][1], acc);
+          s[kb][qb] = mma16(kh1, ql[qb][1], acc);
+        }
+      }
+    }
+
+    // Online softmax in base 2; lane holds keys kb*16 + 4*lg + i. The
+    // running max and the rescale of O happen first; the probabilities are
+    // then formed, summed and split per key-block pair inside the PV loop, so
+    // only one pair's fp16 fragments are live at a time.
+    float mnew[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 8; ++kb) {
+        if (kb < nkb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb * 16 + lg * 4 + i;
+            const float sv = key < nkeys ? s[kb][qb][i] * kS2 : -INFINITY;
+            s[kb][qb][i] = sv;
+            cmax = fmaxf(cmax, sv);
+          }
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      mnew[qb] = fmaxf(mrun[qb], cmax);
+      const float alpha = exp2f(mrun[qb] - mnew[qb]);
+      mrun[qb] = mnew[qb];
+      lrun[qb] *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+    }
+
+    // O^T += V^T P^T over key-block pairs, three MFMAs per product.
+#pragma unroll
+    for (int kp = 0; kp < 4; ++kp) {
+      if (2 * kp < nkb) {
+        f16x8 pfh[2], pfl[2];
+        const bool two = 2 * kp + 1 < nkb;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          float psum = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int kb = 2 * kp + (j >> 2);
+            float p = 0.f;
+            if (j < 4 || two) p = exp2f(s[kb][qb][j & 3] - mnew[qb]);
+            psum += p;
+            const SplitH sp = split_f16(p);
+            pfh[qb][j] = sp.hi;
+            pfl[qb][j] = sp.lo;
+          }
+          lrun[qb] += psum;
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const int r = (db * 16 + lr) * kVPitchX;
+          const int ca = ((2 * kp) * 16 + lg * 4) * 2, cb = ((2 * kp + 1) * 16 + lg * 4) * 2;
+          const f16x4 vah = *reinterpret_cast<const f16x4*>(sVh + r + ca);
+          const f16x4 vbh = *reinterpret_cast<const f16x4*>(sVh + r + cb);
+          const f16x4 val = *reinterpret_cast<const f16x4*>(sVl + r + ca);
+          const f16x4 vbl = *reinterpret_cast<const f16x4*>(sVl + r + cb);
+          const f16x8 vfh = f16x8{vah[0], vah[1], vah[2], vah[3], vbh[0], vbh[1], vbh[2], vbh[3]};
+          const f16x8 vfl = f16x8{val[0], val[1], val[2], val[3], vbl[0], vbl[1], vbl[2], vbl[3]};
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            f32x4 acc = mma16(vfh, pfh[qb], o[qb][db]);
+            acc = mma16(vfl, pfh[qb], acc);
+            o[qb][db] = mma16(vfh, pfl[qb], acc);
+          }
+        }
+      }
+    }
+  }
+
+  if (!active) return;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float lt = lrun[qb];
+    lt += __shfl_xor(lt, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    const float inv = 1.0f / lt;
+    const int qi = qbase + qb * 16 + lr;
+    if (qi < L) {
+      float* orow = out + static_cast<size_t>(start + qi) * ld_out + hoff + lg * 4;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        *reinterpret_cast<float4*>(orow + db * 16) =
+            make_float4(o[qb][db][0] * inv, o[qb][db][1] * inv, o[qb][db][2] * inv, o[qb][db][3] * inv);
+    }
+  }
+}
+
 template <int DH_MAX>
 __global__ __launch_bounds__(64) void attn_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k,
@@ -313,6 +547,15 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
     if (v_is_bf16) ESM_ATTN_LAUNCH(false, true); else ESM_ATTN_LAUNCH(false, false);
   }
 #undef ESM_ATTN_LAUNCH
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_x3(const float* q, const float* k, const float* v, int ld,
+                               const int* cu_seqlens, const AttnWork* work, int num_work,
+                               float* out, int ld_out, hipStream_t s) {
+  if (num_work <= 0) return hipSuccess;
+  hipLaunchKernelGGL(attn_x3_kernel, dim3(num_work), dim3(256), 0, s, q, k, v, ld, cu_seqlens, work, out,
+                     ld_out);
   return hipGetLastError();
 }
 

@@ -556,9 +556,21 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
   }
-  if (precision != ESM_GFX950_ATTN_BF16_MFMA)
+  if (precision != ESM_GFX950_ATTN_BF16_MFMA && precision != ESM_GFX950_ATTN_F16X3_MFMA)
     return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "attention_varlen: unknown precision");
   ESM_REQUIRE(ctx, head_dim == kHeadDimMfma, "attention_varlen: the MFMA path needs head_dim == 64");
+  if (precision == ESM_GFX950_ATTN_F16X3_MFMA) {
+    int* d_cu;
+    AttnWork* d_work;
+    int nwork;
+    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork));
+    int slot;
+    ESM_TRY(ctx->time_begin("attention", &slot));
+    ESM_HIP(ctx, launch_attention_x3(q, k, v, ld, d_cu, d_work, nwork, out, ld, ctx->stream));
+    ESM_TRY(ctx->time_end(slot));
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ESM_GFX950_OK;
+  }
   const size_t n = static_cast<size_t>(T) * ld;
   const size_t cbytes = align_up(n * 2, 256);
   int* d_cu;
@@ -723,7 +735,7 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   ESM_REQUIRE(ctx, c.head_dim % 2 == 0 && c.head_dim <= 128, "model_create: head_dim must be even and <= 128");
   ESM_REQUIRE(ctx, c.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR || c.act_quant_mode == ESM_GFX950_ACT_PER_TOKEN,
               "model_create: unknown act_quant_mode");
-  ESM_REQUIRE(ctx, c.attention_mode >= ESM_GFX950_ATTN_MODE_FP16 && c.attention_mode <= ESM_GFX950_ATTN_MODE_FP32,
+  ESM_REQUIRE(ctx, c.attention_mode >= ESM_GFX950_ATTN_MODE_FP16 && c.attention_mode <= ESM_GFX950_ATTN_MODE_F16X3,
               "model_create: unknown attention_mode");
   if (c.weights_int8) {
     ESM_REQUIRE(ctx, c.hidden_size % 16 == 0 && c.intermediate_size % 16 == 0,
@@ -821,6 +833,11 @@ struct Arena {
   size_t bytes;
 };
 
+// Attention modes whose Q/K/V live in the fp32 [T, 3d] buffer.
+bool qkv_is_f32(const esm_gfx950_model_config& c) {
+  return c.attention_mode == ESM_GFX950_ATTN_MODE_FP32 || c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3;
+}
+
 Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
   const size_t d = c.hidden_size, f = c.intermediate_size, V = c.vocab_size;
   const size_t Ts = static_cast<size_t>(T);
@@ -839,7 +856,7 @@ Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
   a.qb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.kb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.vb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
-  const bool need_qkv_f32 = !c.weights_int8 || (c.attention_mode == ESM_GFX950_ATTN_MODE_FP32);
+  const bool need_qkv_f32 = !c.weights_int8 || qkv_is_f32(c);
   a.qkv = reinterpret_cast<float*>(take(need_qkv_f32 ? Ts * 3 * d * 4 : 0));
   a.attn = reinterpret_cast<float*>(take(Ts * d * 4));
   a.inter = reinterpret_cast<float*>(take(Ts * f * 4));
@@ -920,20 +937,28 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.a_scale = a.xs;
   g.w_scale = L.qkv.ws;
   g.bias = L.qkv.bias;
+  g.d_model = d;
+  g.pos = md.pos;
+  g.rope_cos = md.cos_t;
+  g.rope_sin = md.sin_t;
+  g.q_scale = q_scale;
+  const bool f32qkv = qkv_is_f32(c);
   ESM_TRY(ctx->time_begin("qkv", &slot));
-  if ((c.attention_mode == ESM_GFX950_ATTN_MODE_FP32)) {
+  if (f32qkv && dh == kHeadDimMfma) {
+    // Dequant + bias, Q scale and RoPE fused; fp32 Q|K|V rows.
+    g.C_f32 = a.qkv;
+    g.ldc = 3 * d;
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvRopeF32, s));
+  } else if (f32qkv) {
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+    ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   } else {
     g.q_out = a.qb;
     g.k_out = a.kb;
     g.v_out = a.vb;
-    g.d_model = d;
-    g.pos = md.pos;
-    g.rope_cos = md.cos_t;
-    g.rope_sin = md.sin_t;
-    g.q_scale = q_scale;
     g.qk_fp16 = c.attention_mode == ESM_GFX950_ATTN_MODE_FP16 ? 1 : 0;
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvRope, s));
   }
@@ -943,11 +968,13 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   float* amax_attn = tok ? nullptr : a.absmax + 1;
   if (!tok) ESM_HIP(ctx, launch_fill_f32(a.absmax + 1, 1, 0.0f, s));
   ESM_TRY(ctx->time_begin("attention", &slot));
-  if ((c.attention_mode == ESM_GFX950_ATTN_MODE_FP32)) {
-    ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
-    ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
-    ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d,
-                                      s));
+  if (f32qkv) {
+    if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
+      ESM_HIP(ctx, launch_attention_x3(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, md.cu, md.work, nwork, a.attn, d, s));
+    } else {
+      ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
+                                        d, s));
+    }
     if (!tok) ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
   } else {
     const int qk16 = c.attention_mode == ESM_GFX950_ATTN_MODE_FP16 ? 1 : 0;
@@ -1127,7 +1154,7 @@ extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m,
   }
   build_pos(cu, B, mh.pos);
   std::memcpy(mh.cu, cu, static_cast<size_t>(B + 1) * 4);
-  const bool mfma_attn = c.weights_int8 && !(c.attention_mode == ESM_GFX950_ATTN_MODE_FP32);
+  const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
   std::vector<AttnWork> work;
   build_work(cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
   std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));

@@ -115,8 +115,48 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
       ws[bn] = ok ? p.w_scale[col] : 0.0f;
       bs[bn] = (ok && p.bias) ? p.bias[col] : 0.0f;
     }
-    if constexpr (EPI == kEpiQkvRope) {
+    if constexpr (EPI == kEpiQkvRopeF32) {
       static_assert(WN == 4, "QKV epilogue needs 64-column (one head) waves");
+      if (cb >= p.N) return;
+      // fp32 Q|K|V row of width 3*d_model: the wave's 64 columns are one
+      // head of Q, K or V; rotary pairs (i, i+32) are blocks (0,2), (1,3).
+      const int which = cb / p.d_model;
+#pragma unroll
+      for (int bm = 0; bm < WM; ++bm)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rb + bm * 16 + lg * 4 + r;
+          if (row >= p.M) continue;
+          const float as = p.a_scale[row];
+          float v[WN];
+#pragma unroll
+          for (int bn = 0; bn < WN; ++bn)
+            v[bn] = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
+          if (which < 2) {
+            if (which == 0) {
+#pragma unroll
+              for (int bn = 0; bn < WN; ++bn) v[bn] *= p.q_scale;
+            }
+            const int ps = p.pos[row];
+            const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
+            const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int i = h * 16 + lr;
+              const float x1 = v[h], x2 = v[h + 2];
+              v[h] = x1 * ct[i] - x2 * st[i];
+              v[h + 2] = x2 * ct[i + 32] + x1 * st[i + 32];
+            }
+          }
+          float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + cb + lr;
+#pragma unroll
+          for (int bn = 0; bn < WN; ++bn) dst[bn * 16] = v[bn];
+        }
+      return;
+    } else if constexpr (EPI == kEpiQkvRope) {
+      static_assert(WN == 4, "QKV epilogue needs 64-column (one head) waves");
+      // With an odd head count the last tile's second wave lies past N.
+      if (cb >= p.N) return;
       // The wave's 64 columns are exactly one head of Q, K or V. Lane
       // column lr of block bn holds head dim bn*16+lr, so the rotary pairs
       // (i, i+32) sit in blocks (0,2) and (1,3) of the same lane and row.
@@ -294,6 +334,7 @@ hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32Resid>), grid, block, 0, s, p); break;
     case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRope>), grid, block, 0, s, p); break;
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRopeF32>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

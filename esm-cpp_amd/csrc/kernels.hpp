@@ -19,6 +19,7 @@ enum GemmEpilogue : int {
   kEpiF32Resid = 3,   // C_f32 += fma(...)   (residual add into hidden)
   kEpiQkvRope = 4,    // split Q|K|V, Q*q_scale, RoPE on Q and K, bf16/fp16 out
   kEpiF32GeluQ = 5,   // gelu(...) -> fp16 store + per-row absmax (atomic)
+  kEpiQkvRopeF32 = 6, // fp32 [M, 3*d_model] (ldc): Q*q_scale and RoPE on Q, K
 };
 
 struct GemmI8Args {
@@ -86,6 +87,13 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
                                  const AttnWork* work, int num_work, float* out,
                                  int ld_out, float* tensor_absmax,
                                  hipStream_t s);
+// Split-fp16 MFMA path, head_dim 64: fp32 q/k/v (row stride ld), each
+// operand carried as fp16 hi + lo with three MFMAs per product (fp32-level
+// accuracy on the fp16 matrix cores). Same work list as the MFMA path.
+hipError_t launch_attention_x3(const float* q, const float* k, const float* v,
+                               int ld, const int* cu_seqlens,
+                               const AttnWork* work, int num_work, float* out,
+                               int ld_out, hipStream_t s);
 // Exact fp32 path for any head_dim <= 128 (one thread per query).
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
                                 int ld, int head_dim, const int* cu_seqlens,

@@ -22,9 +22,11 @@ ACT_PER_TENSOR = 0
 ACT_PER_TOKEN = 1
 ATTN_FP32 = 0
 ATTN_BF16_MFMA = 1
+ATTN_F16X3_MFMA = 2
 ATTN_MODE_FP16 = 0
 ATTN_MODE_BF16 = 1
 ATTN_MODE_FP32 = 2
+ATTN_MODE_F16X3 = 3
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED = [
@@ -308,7 +310,7 @@ class Model:
     """
 
     def __init__(self, dev: Device, weights, int8: bool, act_mode: int = ACT_PER_TOKEN,
-                 attention_mode: int = ATTN_MODE_FP16):
+                 attention_mode: int = ATTN_MODE_F16X3):
         cfg = weights.cfg
         keep: List[np.ndarray] = []
 

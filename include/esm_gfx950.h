@@ -52,15 +52,27 @@ enum {
  * [M,K] input, 1 when all zero); PER_TOKEN uses one such scale per row. */
 enum { ESM_GFX950_ACT_PER_TENSOR = 0, ESM_GFX950_ACT_PER_TOKEN = 1 };
 
-/* Attention arithmetic for esm_gfx950_attention_varlen. */
-enum { ESM_GFX950_ATTN_FP32 = 0, ESM_GFX950_ATTN_BF16_MFMA = 1 };
+/* Attention arithmetic for esm_gfx950_attention_varlen. FP32: scalar fp32
+ * kernel in the reference's operation order. BF16_MFMA: q/k rounded to bf16,
+ * v and the probabilities to fp16, on MFMA. F16X3_MFMA: fp32 inputs, every
+ * operand split into fp16 hi + lo and each product formed by three fp16
+ * MFMAs (hi*hi + lo*hi + hi*lo), i.e. fp32-level results at MFMA speed;
+ * needs |8*q|, |k|, |v| < 65504 (fp16 range). */
+enum { ESM_GFX950_ATTN_FP32 = 0, ESM_GFX950_ATTN_BF16_MFMA = 1, ESM_GFX950_ATTN_F16X3_MFMA = 2 };
 
-/* Attention inside the W8A8 forward. FP16 (default): the QKV epilogue
- * writes Q/K/V as fp16 and QK^T runs on fp16 MFMA; BF16: Q/K as bf16 on
- * bf16 MFMA; both keep fp16 P and V on fp16 MFMA and an fp32 softmax. FP32:
- * Q/K/V stay fp32 and the exact fp32 kernel runs (the reference's
- * arithmetic, for parity studies). */
-enum { ESM_GFX950_ATTN_MODE_FP16 = 0, ESM_GFX950_ATTN_MODE_BF16 = 1, ESM_GFX950_ATTN_MODE_FP32 = 2 };
+/* Attention inside the W8A8 forward. F16X3 (default): the QKV epilogue
+ * writes fp32 Q/K/V (Q scaled, RoPE applied) and the split-fp16 MFMA kernel
+ * runs -- logits track the reference's fp32 attention. FP16: Q/K/V stored as
+ * fp16, single fp16 MFMAs; BF16: Q/K as bf16. Those two halve the Q/K/V
+ * traffic but round every attention operand once (about 3e-4 off the logit
+ * correlation of a W8A8 network, whose int8 rounding amplifies any
+ * perturbation). FP32: fp32 Q/K/V and the scalar fp32 kernel. */
+enum {
+  ESM_GFX950_ATTN_MODE_FP16 = 0,
+  ESM_GFX950_ATTN_MODE_BF16 = 1,
+  ESM_GFX950_ATTN_MODE_FP32 = 2,
+  ESM_GFX950_ATTN_MODE_F16X3 = 3
+};
 
 typedef struct esm_gfx950_ctx esm_gfx950_ctx;
 typedef struct esm_gfx950_weight esm_gfx950_weight;
@@ -169,7 +181,9 @@ int esm_gfx950_rope_apply_varlen(esm_gfx950_ctx* ctx, float* x, const float* cos
  * attention.cpp:99-144): q, k, v fp32 [T, H, head_dim] (Q pre-scaled),
  * out fp32 [T, H*head_dim]. precision FP32 is the exact path (any
  * head_dim <= 128); BF16_MFMA rounds q/k to bf16 and v to fp16 on device
- * and runs the MFMA kernel (head_dim == 64). cu_seqlens is a HOST array. */
+ * and runs the MFMA kernel (head_dim == 64); F16X3_MFMA runs the split-fp16
+ * MFMA kernel on the fp32 inputs directly (head_dim == 64). cu_seqlens is a
+ * HOST array. */
 int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
                                 const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
                                 float* out, int precision);

@@ -2,8 +2,11 @@
 
 Bars: fp32 path within 1e-4 * (1 + |ref|) (the reference's own SIMD-vs-Ref
 tolerance, tests/cpp/test_attention_varlen.cpp:370-375) and in practice
-~1e-6; MFMA path (bf16 Q/K, fp16 V and P, fp32 softmax) on bf16-rounded
-inputs within rtol = atol = 1e-3 of the fp32 kernel on the same values.
+~1e-6; split-fp16 MFMA path (fp32 inputs, hi+lo fp16 operands, three MFMAs
+per product) within rtol = atol = 1e-5 of the fp32 oracle on the same fp32
+inputs; single-fp16 MFMA path (bf16 Q/K, fp16 V and P, fp32 softmax) on
+bf16-rounded inputs within rtol = atol = 1e-3 of the fp32 kernel on the same
+values.
 """
 import numpy as np
 import pytest
@@ -93,6 +96,46 @@ def test_mfma_unscaled_q_stress(dev, oracle):
     _mfma_vs_oracle(dev, oracle, [200, 90, 64], H=8, seed=11, scale_q=False)
 
 
+def _x3_vs_oracle(dev, oracle, lengths, H, seed, scale_q=True, check_seqs=None, tol=1e-5):
+    r = rng(seed)
+    cu = cu_from_lengths(lengths)
+    T = int(cu[-1])
+    q, k, v = _qkv(r, T, H, 64, scale_q=scale_q)
+    out = dev.empty((T, H * 64), np.float32)
+    dev.attention_varlen(dev.array(q), dev.array(k), dev.array(v), cu, H, 64, out, eg.ATTN_F16X3_MFMA)
+    got = out.numpy()
+    assert np.all(np.isfinite(got))
+    seqs = range(len(lengths)) if check_seqs is None else check_seqs
+    for b in seqs:
+        s0, s1 = int(cu[b]), int(cu[b + 1])
+        if s1 == s0:
+            continue
+        sub = np.array([0, s1 - s0], np.int32)
+        want = oracle.attention_varlen(q[s0:s1], k[s0:s1], v[s0:s1], sub, H, 64)
+        np.testing.assert_allclose(got[s0:s1], want, rtol=tol, atol=tol, err_msg=f"seq {b} L={s1 - s0}")
+
+
+@pytest.mark.parametrize("lengths", [[1], [7, 1, 16], [33, 129, 64], [250, 60, 128, 127], [1024], [300, 0, 5]])
+def test_x3_ragged(dev, oracle, lengths):
+    _x3_vs_oracle(dev, oracle, lengths, H=20, seed=100 + sum(lengths))
+
+
+def test_x3_config2_full(dev, oracle):
+    """Config 2 on fp32 inputs: the whole batch on the GPU, 24 sequences plus
+    the longest checked against the fp32 oracle at 1e-5."""
+    lengths = syn.varlen_lengths(256, 20261201 + 2)
+    r = rng(1)
+    _x3_vs_oracle(dev, oracle, list(lengths), H=20, seed=3,
+                  check_seqs=sorted(r.choice(256, 24, replace=False).tolist() + [int(np.argmax(lengths))]))
+
+
+def test_x3_unscaled_q_stress(dev, oracle):
+    """Q not pre-scaled (8x larger logits, peaked rows): the fp32 oracle's own
+    rounding grows with |q.k|, so the bar here is the reference's SIMD-vs-Ref
+    tolerance, 1e-4 * (1 + |ref|) (tests/cpp/test_attention_varlen.cpp:370-375)."""
+    _x3_vs_oracle(dev, oracle, [200, 90, 64], H=8, seed=12, scale_q=False, tol=1e-4)
+
+
 def test_fp32_mfma_input_equivalence(dev, oracle):
     """The fp32-input MFMA entry (device bf16/fp16 cast) matches the bf16 entry."""
     r = rng(12)
@@ -106,7 +149,7 @@ def test_fp32_mfma_input_equivalence(dev, oracle):
     np.testing.assert_allclose(out.numpy(), want, rtol=2e-2, atol=2e-2)
 
 
-@pytest.mark.parametrize("precision", [eg.ATTN_FP32, eg.ATTN_BF16_MFMA])
+@pytest.mark.parametrize("precision", [eg.ATTN_FP32, eg.ATTN_BF16_MFMA, eg.ATTN_F16X3_MFMA])
 def test_isolation(dev, precision):
     """A poisoned second sequence leaves the first bit-identical
     (reference tests/cpp/test_attention_varlen.cpp:185-225)."""
@@ -125,7 +168,7 @@ def test_isolation(dev, precision):
     assert np.array_equal(packed.numpy()[:L1], solo.numpy())
 
 
-@pytest.mark.parametrize("precision", [eg.ATTN_FP32, eg.ATTN_BF16_MFMA])
+@pytest.mark.parametrize("precision", [eg.ATTN_FP32, eg.ATTN_BF16_MFMA, eg.ATTN_F16X3_MFMA])
 def test_single_token_is_v(dev, precision):
     """L = 1: softmax is 1, out = V (reference tests/cpp/test_kernels.cpp:355-365)."""
     H, dh = 20, 64
