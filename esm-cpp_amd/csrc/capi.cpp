@@ -465,7 +465,8 @@ extern "C" int esm_gfx950_layernorm(esm_gfx950_ctx* ctx, const float* x, const f
                                     const float* beta, float eps, float* out, int num_rows, int d) {
   if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_REQUIRE(ctx, (x && gamma && beta && out) || num_rows <= 0, "layernorm: null pointer");
-  ESM_HIP(ctx, launch_layernorm(x, gamma, beta, eps, out, num_rows, d, nullptr, ctx->stream));
+  ESM_HIP(ctx, launch_layernorm(const_cast<float*>(x), nullptr, gamma, beta, eps, out, num_rows, d, nullptr,
+                                ctx->stream));
   return ESM_GFX950_OK;
 }
 
@@ -826,6 +827,7 @@ struct Arena {
   uint16_t* vb;      // [T, d] fp16 V
   float* qkv;        // [T, 3d] fp32 (fp32 paths)
   float* attn;       // [T, d]
+  float* ybuf;       // [T, d] out-proj / fc2 output awaiting its residual add
   float* inter;      // [T, ffn]
   float* lm_a;       // [T, d]
   float* logits;     // [T, V]
@@ -859,6 +861,7 @@ Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
   const bool need_qkv_f32 = !c.weights_int8 || qkv_is_f32(c);
   a.qkv = reinterpret_cast<float*>(take(need_qkv_f32 ? Ts * 3 * d * 4 : 0));
   a.attn = reinterpret_cast<float*>(take(Ts * d * 4));
+  a.ybuf = reinterpret_cast<float*>(take(c.weights_int8 ? Ts * d * 4 : 0));
   a.inter = reinterpret_cast<float*>(take(Ts * f * 4));
   a.lm_a = reinterpret_cast<float*>(take(Ts * d * 4));
   a.logits = reinterpret_cast<float*>(take(Ts * V * 4));
@@ -906,8 +909,13 @@ P shift(P p, const char* from, const char* to) {
 // One pre-LN encoder layer on the device (reference TransformerBlock,
 // src/model.cpp:932-1066): LN -> QKV -> Q-scale -> RoPE -> attention ->
 // out-proj -> residual -> LN -> fc1 -> GELU -> fc2 -> residual.
+// The out-proj and fc2 GEMMs store their outputs to a.ybuf; each residual add
+// (hidden += ybuf) is performed by the LayerNorm kernel that reads hidden
+// next -- this layer's ffn LN, the next layer's attn LN, or the final LN --
+// so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
+// fc2 output of the previous layer (null for the first layer).
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, const Arena& a, const Meta& md,
-               int T, int nwork) {
+               int T, int nwork, const float* resid_in) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
   const int ldq_d = pad16(d), ldq_f = pad16(f);
@@ -916,12 +924,13 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
   int slot;
 
-  // attn LN + activation quant
+  // (residual) + attn LN + activation quant
   if (tok) {
-    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d, a.xs, s));
+    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
+                                        a.xs, s));
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax, 1, 0.0f, s));
-    ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
+    ESM_HIP(ctx, launch_layernorm(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
     ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax, a.xq, ldq_d, a.xs, s));
   }
 
@@ -987,7 +996,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_quant_tensor(a.attn, d, T, d, amax_attn, a.xq, ldq_d, a.xs, s));
   }
 
-  // out-proj + residual
+  // out-proj (its residual add happens in the ffn LN below)
   g = GemmI8Args();
   g.A = a.xq;
   g.lda = ldq_d;
@@ -999,18 +1008,20 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.a_scale = a.xs;
   g.w_scale = L.out.ws;
   g.bias = L.out.bias;
-  g.C_f32 = a.hidden;
+  g.C_f32 = a.ybuf;
   g.ldc = d;
   ESM_TRY(ctx->time_begin("out", &slot));
-  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
   ESM_TRY(ctx->time_end(slot));
 
-  // ffn LN + quant
+  // residual + ffn LN + quant
   if (tok) {
-    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d, a.xs, s));
+    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
+                                        a.xs, s));
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
-    ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2, s));
+    ESM_HIP(ctx, launch_layernorm(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
+                                  s));
     ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax + 2, a.xq, ldq_d, a.xs, s));
   }
 
@@ -1028,20 +1039,23 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.bias = L.fc1.bias;
   g.C_f32 = a.inter;
   g.ldc = f;
-  if (!tok) {
+  if (tok) {
+    // Dequant + bias only; GELU runs in the per-token quantisation pass that
+    // reads these rows anyway.
+    ESM_TRY(ctx->time_begin("fc1", &slot));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    ESM_TRY(ctx->time_end(slot));
+    ESM_HIP(ctx, launch_gelu_quant_rows(a.inter, f, T, f, a.xq, ldq_f, a.xs, s));
+  } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 3, 1, 0.0f, s));
     g.tensor_absmax = a.absmax + 3;
-  }
-  ESM_TRY(ctx->time_begin("fc1", &slot));
-  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Gelu, s));
-  ESM_TRY(ctx->time_end(slot));
-  if (tok) {
-    ESM_HIP(ctx, launch_quant_rows(a.inter, 0, f, T, f, a.xq, ldq_f, a.xs, s));
-  } else {
+    ESM_TRY(ctx->time_begin("fc1", &slot));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Gelu, s));
+    ESM_TRY(ctx->time_end(slot));
     ESM_HIP(ctx, launch_quant_tensor(a.inter, f, T, f, a.absmax + 3, a.xq, ldq_f, a.xs, s));
   }
 
-  // fc2 + residual
+  // fc2 (its residual add happens in the next LN that reads hidden)
   g = GemmI8Args();
   g.A = a.xq;
   g.lda = ldq_f;
@@ -1053,10 +1067,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.a_scale = a.xs;
   g.w_scale = L.fc2.ws;
   g.bias = L.fc2.bias;
-  g.C_f32 = a.hidden;
+  g.C_f32 = a.ybuf;
   g.ldc = d;
   ESM_TRY(ctx->time_begin("fc2", &slot));
-  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
   ESM_TRY(ctx->time_end(slot));
   return ESM_GFX950_OK;
 }
@@ -1083,13 +1097,13 @@ int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L,
   const int d = c.hidden_size, H = c.num_heads, dh = c.head_dim;
   hipStream_t s = ctx->stream;
   const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
-  ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
   ESM_TRY(f32_linear(ctx, a.ln, L.qkv, a.qkv, T, kF32Store));
   ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
   ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d, s));
   ESM_TRY(f32_linear(ctx, a.attn, L.out, a.hidden, T, kF32Resid));
-  ESM_HIP(ctx, launch_layernorm(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
   ESM_TRY(f32_linear(ctx, a.ln, L.fc1, a.inter, T, kF32Gelu));
   ESM_TRY(f32_linear(ctx, a.inter, L.fc2, a.hidden, T, kF32Resid));
   return ESM_GFX950_OK;
@@ -1184,16 +1198,19 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
 
   hipStream_t s = ctx->stream;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
+  const float* pending = nullptr;  // fc2 output awaiting its residual add
   for (const DevLayer& L : m->layers) {
     if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, a, md, T, nwork));
+      ESM_TRY(layer_int8(ctx, m, L, a, md, T, nwork, pending));
+      pending = a.ybuf;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, a, md, T, nwork));
     }
   }
-  // Final LN and lm head: dense -> GELU -> LN -> tied decoder + bias
-  // (reference src/model.cpp:1181-1239).
-  ESM_HIP(ctx, launch_layernorm(a.hidden, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  // (Last residual +) final LN and lm head: dense -> GELU -> LN -> tied
+  // decoder + bias (reference src/model.cpp:1181-1239).
+  ESM_HIP(ctx, launch_layernorm(a.hidden, pending, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d,
+                                nullptr, s));
   DevLinear dense;
   dense.w32 = m->lm_dense_w;
   dense.bias = m->lm_dense_b;
@@ -1203,7 +1220,7 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   ESM_TRY(ctx->time_begin("lm_dense", &slot));
   ESM_TRY(f32_linear(ctx, a.ln, dense, a.lm_a, T, kF32Gelu));
   ESM_TRY(ctx->time_end(slot));
-  ESM_HIP(ctx, launch_layernorm(a.lm_a, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr, s));
+  ESM_HIP(ctx, launch_layernorm(a.lm_a, nullptr, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr, s));
   DevLinear dec;
   dec.w32 = m->embed;
   dec.bias = m->dec_bias;

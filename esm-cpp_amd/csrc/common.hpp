@@ -10,6 +10,7 @@
 namespace esm_gfx950 {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -64,6 +65,27 @@ __device__ __forceinline__ void atomic_max_nonneg(float* addr, float v) {
 // device library's erf.
 __device__ __forceinline__ float gelu_erf(float x) {
   return x * 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// GELU with erf from Abramowitz & Stegun, Handbook of Mathematical
+// Functions, eq. 7.1.26 (|error of erf| <= 1.5e-7 for every x): erf(u) =
+// 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-u^2), t = 1/(1 + p|u|),
+// odd in u. The reference's AVX-512 GELU uses the same approximation
+// (reference src/kernels/gelu.cpp:69-94); exp(-u^2) here is the hardware
+// base-2 exponential, which returns 0 (not NaN) for large |u|.
+__device__ __forceinline__ float gelu_as(float x) {
+  const float u = x * 0.70710678118654752440f;
+  const float au = fabsf(u);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, au, 1.0f));
+  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  poly = __builtin_fmaf(poly, t, 1.421413741f);
+  poly = __builtin_fmaf(poly, t, -0.284496736f);
+  poly = __builtin_fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float e = __builtin_amdgcn_exp2f(-au * au * 1.44269504088896340736f);
+  const float erf_abs = __builtin_fmaf(-poly, e, 1.0f);
+  const float erf_u = u < 0.0f ? -erf_abs : erf_abs;
+  return x * 0.5f * (1.0f + erf_u);
 }
 
 // Symmetric int8 quantisation of one value with a precomputed reciprocal

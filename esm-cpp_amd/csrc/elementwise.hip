@@ -23,16 +23,20 @@ __device__ __forceinline__ float act_scale_from_absmax(float amax) {
 }
 
 // ---- LayerNorm with the row cached in registers (d % 4 == 0, d <= NV*256).
+// With resid != null the row is first updated in place, x += resid (the
+// residual add that precedes the next LayerNorm, reference src/model.cpp:1013
+// and :1063), and the LayerNorm runs on the sum.
 template <int NV, bool QUANT>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(
-    const float* __restrict__ x, const float* __restrict__ gamma,
+    float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ out,
     int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
     float* __restrict__ scales) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* xr = x + static_cast<size_t>(row) * d;
+  float* xr = x + static_cast<size_t>(row) * d;
+  const float* rr = resid ? resid + static_cast<size_t>(row) * d : nullptr;
   float4 v[NV];
   float sum = 0.f;
 #pragma unroll
@@ -40,6 +44,14 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     const int c = (j * 64 + lane) * 4;
     if (c < d) {
       v[j] = *reinterpret_cast<const float4*>(xr + c);
+      if (rr) {
+        const float4 a = *reinterpret_cast<const float4*>(rr + c);
+        v[j].x += a.x;
+        v[j].y += a.y;
+        v[j].z += a.z;
+        v[j].w += a.w;
+        *reinterpret_cast<float4*>(xr + c) = v[j];
+      }
       sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     } else {
       v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -99,13 +111,17 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
 
 // ---- Generic LayerNorm for any d (three passes over the row in cache).
 __global__ __launch_bounds__(256) void layernorm_any_kernel(
-    const float* __restrict__ x, const float* __restrict__ gamma,
+    float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ out,
     int rows, int d, float* tensor_absmax) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const float* xr = x + static_cast<size_t>(row) * d;
+  float* xr = x + static_cast<size_t>(row) * d;
+  if (resid) {
+    const float* rr = resid + static_cast<size_t>(row) * d;
+    for (int c = lane; c < d; c += 64) xr[c] += rr[c];
+  }
   float sum = 0.f;
   for (int c = lane; c < d; c += 64) sum += xr[c];
   const float mean = wave_sum(sum) / static_cast<float>(d);
@@ -172,6 +188,50 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
     if (c < cols) {
       v[j] = *reinterpret_cast<const float4*>(xr + c);
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    }
+  }
+  const float scale = act_scale_from_absmax(wave_max(amax));
+  const float inv = 1.0f / scale;
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
+      const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
+      const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
+      const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
+      *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+  }
+  for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
+  if (lane == 0) scales[row] = scale;
+}
+
+// GELU fused with per-row quantisation (cols % 4 == 0, cols <= NV*256): the
+// fc1 output row is read once, GELU'd in registers, its absmax taken, and it
+// is written as int8 with the row's scale.
+template <int NV>
+__global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
+    const float* __restrict__ x, int ldx, int rows, int cols,
+    int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * ldx;
+  float4 v[NV];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    if (c < cols) {
+      float4 a = *reinterpret_cast<const float4*>(xr + c);
+      a.x = gelu_as(a.x);
+      a.y = gelu_as(a.y);
+      a.z = gelu_as(a.z);
+      a.w = gelu_as(a.w);
+      v[j] = a;
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
     }
   }
   const float scale = act_scale_from_absmax(wave_max(amax));
@@ -297,33 +357,48 @@ inline dim3 rows_grid(int rows) { return dim3((rows + kRowsPerBlock - 1) / kRows
 
 }  // namespace
 
-hipError_t launch_layernorm(const float* x, const float* gamma, const float* beta, float eps,
+hipError_t launch_layernorm(float* x, const float* resid, const float* gamma, const float* beta, float eps,
                             float* out, int rows, int d, float* tensor_absmax, hipStream_t s) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   const dim3 g = rows_grid(rows), b(256);
   if (d % 4 == 0 && d <= 1280) {
-    hipLaunchKernelGGL((layernorm_vec_kernel<5, false>), g, b, 0, s, x, gamma, beta, eps, out, rows, d,
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, false>), g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d,
                        tensor_absmax, nullptr, 0, nullptr);
   } else if (d % 4 == 0 && d <= 2560) {
-    hipLaunchKernelGGL((layernorm_vec_kernel<10, false>), g, b, 0, s, x, gamma, beta, eps, out, rows, d,
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, false>), g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d,
                        tensor_absmax, nullptr, 0, nullptr);
   } else {
-    hipLaunchKernelGGL(layernorm_any_kernel, g, b, 0, s, x, gamma, beta, eps, out, rows, d, tensor_absmax);
+    hipLaunchKernelGGL(layernorm_any_kernel, g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d, tensor_absmax);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_layernorm_quant(const float* x, const float* gamma, const float* beta, float eps,
+hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gamma, const float* beta, float eps,
                                   int rows, int d, int8_t* q, int ldq, float* scales, hipStream_t s) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   if (d % 4 != 0 || d > 2560) return hipErrorInvalidValue;
   const dim3 g = rows_grid(rows), b(256);
   if (d <= 1280) {
-    hipLaunchKernelGGL((layernorm_vec_kernel<5, true>), g, b, 0, s, x, gamma, beta, eps, nullptr, rows, d,
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
                        nullptr, q, ldq, scales);
   } else {
-    hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, gamma, beta, eps, nullptr, rows, d,
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
                        nullptr, q, ldq, scales);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols, int8_t* q, int ldq, float* scales,
+                                  hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (cols % 4 != 0 || ldx % 4 != 0 || cols > 10240) return hipErrorInvalidValue;
+  const dim3 g = rows_grid(rows), b(256);
+  if (cols <= 1280) {
+    hipLaunchKernelGGL(gelu_quant_rows_kernel<5>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  } else if (cols <= 5120) {
+    hipLaunchKernelGGL(gelu_quant_rows_kernel<20>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  } else {
+    hipLaunchKernelGGL(gelu_quant_rows_kernel<40>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   }
   return hipGetLastError();
 }

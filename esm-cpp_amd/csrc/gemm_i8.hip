@@ -54,6 +54,23 @@ __device__ __forceinline__ int xcd_remap(int id, int num) {
   return xcd * per + min(xcd, rem) + local;
 }
 
+// Output tile of this workgroup: ids are first spread so that each XCD
+// (workgroup id mod 8) owns a contiguous range, then walked in groups of
+// kGroupM row tiles so consecutive tiles on one XCD share W columns and A rows
+// in that XCD's L2.
+__device__ __forceinline__ void tile_origin(int M, int N, int BM, int BN, int* m0, int* n0) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  const int pid = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int per_group = kGroupM * tiles_n;
+  const int group = pid / per_group;
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int in_group = pid - group * per_group;
+  *m0 = (first_m + in_group % gsize) * BM;
+  *n0 = (in_group / gsize) * BN;
+}
+
 // Global -> registers for one stage of ROWS rows x C::BK bytes. Rows past
 // the matrix edge re-read the last valid row (results are discarded); K
 // bytes past the end read as zero.
@@ -87,11 +104,12 @@ __device__ __forceinline__ void store_stage(int8_t* s, const i32x4 (&r)[LOADS]) 
   }
 }
 
-template <class C, int EPI>
-__device__ __forceinline__ void epilogue(const GemmI8Args& p,
-                                         const i32x4 (&acc)[C::WM][C::WN], int rb,
+// Epilogue of one wave's WM x WN blocks of 16x16 int32 accumulators; the
+// block (bm, bn) element r of lane (lr, lg) is row rb + bm*16 + lg*4 + r,
+// column cb + bn*16 + lr.
+template <int WM, int WN, int EPI>
+__device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)[WM][WN], int rb,
                                          int cb, int lr, int lg) {
-  constexpr int WM = C::WM, WN = C::WN;
   if constexpr (EPI == kEpiI32) {
 #pragma unroll
     for (int bm = 0; bm < WM; ++bm)
@@ -116,26 +134,78 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
       bs[bn] = (ok && p.bias) ? p.bias[col] : 0.0f;
     }
     if constexpr (EPI == kEpiQkvRopeF32) {
-      static_assert(WN == 4, "QKV epilogue needs 64-column (one head) waves");
-      if (cb >= p.N) return;
-      // fp32 Q|K|V row of width 3*d_model: the wave's 64 columns are one
-      // head of Q, K or V; rotary pairs (i, i+32) are blocks (0,2), (1,3).
-      const int which = cb / p.d_model;
+      static_assert(WN % 4 == 0, "QKV epilogue needs whole 64-column heads per wave");
+      // fp32 Q|K|V row of width 3*d_model. Each group of four blocks is one
+      // head of Q, K or V; lane column lr of block g*4+j holds head dim
+      // j*16+lr, so the rotary pairs (i, i+32) are blocks (0,2) and (1,3).
 #pragma unroll
-      for (int bm = 0; bm < WM; ++bm)
+      for (int g = 0; g < WN / 4; ++g) {
+        const int hc = cb + g * 64;
+        if (hc >= p.N) break;
+        const int which = hc / p.d_model;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = rb + bm * 16 + lg * 4 + r;
-          if (row >= p.M) continue;
-          const float as = p.a_scale[row];
-          float v[WN];
+        for (int bm = 0; bm < WM; ++bm)
 #pragma unroll
-          for (int bn = 0; bn < WN; ++bn)
-            v[bn] = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
-          if (which < 2) {
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + bm * 16 + lg * 4 + r;
+            if (row >= p.M) continue;
+            const float as = p.a_scale[row];
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              v[j] = __builtin_fmaf(static_cast<float>(acc[bm][g * 4 + j][r]), as * ws[g * 4 + j], bs[g * 4 + j]);
+            if (which < 2) {
+              if (which == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] *= p.q_scale;
+              }
+              const int ps = p.pos[row];
+              const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
+              const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const int i = h * 16 + lr;
+                const float x1 = v[h], x2 = v[h + 2];
+                v[h] = x1 * ct[i] - x2 * st[i];
+                v[h + 2] = x2 * ct[i + 32] + x1 * st[i + 32];
+              }
+            }
+            float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + hc + lr;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j * 16] = v[j];
+          }
+      }
+      return;
+    } else if constexpr (EPI == kEpiQkvRope) {
+      static_assert(WN % 4 == 0, "QKV epilogue needs whole 64-column heads per wave");
+      // Same head-group layout as above; Q/K stored bf16 or fp16, V fp16,
+      // each as [M, d_model].
+#pragma unroll
+      for (int g = 0; g < WN / 4; ++g) {
+        const int hc = cb + g * 64;
+        if (hc >= p.N) break;
+        const int which = hc / p.d_model;
+        const int hcol = hc - which * p.d_model;
+#pragma unroll
+        for (int bm = 0; bm < WM; ++bm)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = rb + bm * 16 + lg * 4 + r;
+            if (row >= p.M) continue;
+            const float as = p.a_scale[row];
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              v[j] = __builtin_fmaf(static_cast<float>(acc[bm][g * 4 + j][r]), as * ws[g * 4 + j], bs[g * 4 + j]);
+            const size_t o = static_cast<size_t>(row) * p.d_model + hcol + lr;
+            if (which == 2) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) p.v_out[o + j * 16] = f32_to_f16_bits(v[j]);
+              continue;
+            }
             if (which == 0) {
 #pragma unroll
-              for (int bn = 0; bn < WN; ++bn) v[bn] *= p.q_scale;
+              for (int j = 0; j < 4; ++j) v[j] *= p.q_scale;
             }
             const int ps = p.pos[row];
             const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
@@ -147,61 +217,16 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p,
               v[h] = x1 * ct[i] - x2 * st[i];
               v[h + 2] = x2 * ct[i + 32] + x1 * st[i + 32];
             }
+            uint16_t* dst = which == 0 ? p.q_out : p.k_out;
+            if (p.qk_fp16) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) dst[o + j * 16] = f32_to_f16_bits(v[j]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) dst[o + j * 16] = f32_to_bf16_bits(v[j]);
+            }
           }
-          float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + cb + lr;
-#pragma unroll
-          for (int bn = 0; bn < WN; ++bn) dst[bn * 16] = v[bn];
-        }
-      return;
-    } else if constexpr (EPI == kEpiQkvRope) {
-      static_assert(WN == 4, "QKV epilogue needs 64-column (one head) waves");
-      // With an odd head count the last tile's second wave lies past N.
-      if (cb >= p.N) return;
-      // The wave's 64 columns are exactly one head of Q, K or V. Lane
-      // column lr of block bn holds head dim bn*16+lr, so the rotary pairs
-      // (i, i+32) sit in blocks (0,2) and (1,3) of the same lane and row.
-      const int which = cb / p.d_model;
-      const int hcol = cb - which * p.d_model;
-#pragma unroll
-      for (int bm = 0; bm < WM; ++bm)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = rb + bm * 16 + lg * 4 + r;
-          if (row >= p.M) continue;
-          const float as = p.a_scale[row];
-          float v[WN];
-#pragma unroll
-          for (int bn = 0; bn < WN; ++bn)
-            v[bn] = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
-          const size_t o = static_cast<size_t>(row) * p.d_model + hcol + lr;
-          if (which == 2) {
-#pragma unroll
-            for (int bn = 0; bn < WN; ++bn) p.v_out[o + bn * 16] = f32_to_f16_bits(v[bn]);
-            continue;
-          }
-          if (which == 0) {
-#pragma unroll
-            for (int bn = 0; bn < WN; ++bn) v[bn] *= p.q_scale;
-          }
-          const int ps = p.pos[row];
-          const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
-          const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int i = h * 16 + lr;
-            const float x1 = v[h], x2 = v[h + 2];
-            v[h] = x1 * ct[i] - x2 * st[i];
-            v[h + 2] = x2 * ct[i + 32] + x1 * st[i + 32];
-          }
-          uint16_t* dst = which == 0 ? p.q_out : p.k_out;
-          if (p.qk_fp16) {
-#pragma unroll
-            for (int bn = 0; bn < WN; ++bn) dst[o + bn * 16] = f32_to_f16_bits(v[bn]);
-          } else {
-#pragma unroll
-            for (int bn = 0; bn < WN; ++bn) dst[o + bn * 16] = f32_to_bf16_bits(v[bn]);
-          }
-        }
+      }
       return;
     } else {
       float tmax = 0.0f;
@@ -256,16 +281,8 @@ template <class C, int EPI>
 __global__ __launch_bounds__(C::THREADS, 2) void gemm_i8_kernel(const GemmI8Args p) {
   __shared__ __attribute__((aligned(16))) int8_t smem[2 * C::STAGE];
 
-  const int tiles_m = (p.M + C::BM - 1) / C::BM;
-  const int tiles_n = (p.N + C::BN - 1) / C::BN;
-  const int pid = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  const int per_group = kGroupM * tiles_n;
-  const int group = pid / per_group;
-  const int first_m = group * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
-  const int in_group = pid - group * per_group;
-  const int m0 = (first_m + in_group % gsize) * C::BM;
-  const int n0 = (in_group / gsize) * C::BN;
+  int m0, n0;
+  tile_origin(p.M, p.N, C::BM, C::BN, &m0, &n0);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -318,13 +335,257 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_i8_kernel(const GemmI8Args
     __syncthreads();
   }
 
-  epilogue<C, EPI>(p, acc, m0 + wm * C::WM * 16, n0 + wn * C::WN * 16, lr, lg);
+  epilogue<C::WM, C::WN, EPI>(p, acc, m0 + wm * C::WM * 16, n0 + wn * C::WN * 16, lr, lg);
 }
 
+
+// ---------------------------------------------------------------------------
+// Pipelined kernel for K % 128 == 0 (every ESM-2 linear): 256x256 workgroup
+// tile, eight waves (2 x 4) of 128x64, two waves per SIMD, on
+// v_mfma_i32_32x32x32_i8 (4 x 2 blocks of 32x32 per wave).
+//
+// Staging: K advances 128 bytes per stage; each stage moves global -> LDS
+// with global_load_lds_dwordx4, one instruction per 8 rows x 128 bytes, so
+// every request is a whole 128-byte cache line (L2 -> CU throughput on this
+// part measured 2.3x that of 64-byte row pieces). Lane l of the instruction
+// writes LDS bytes [16l, 16l+16) of its 1 KB block; it loads row l/8 of the
+// block and 16-byte chunk (l%8) ^ (l/8) ^ (block & 1), so the LDS copy holds
+// chunk c of row r at position c ^ r ^ (block & 1). That XOR keeps the
+// 32x32x32 fragment reads (32 rows x one chunk per half-wave) on distinct
+// banks. Two 64 KB stages ping-pong with one barrier per stage: the barrier
+// publishes stage kt (each wave waited for its own loads) and retires the
+// reads of stage kt-1, whose buffer then receives stage kt+1 while stage
+// kt's 64 MFMAs per wave run.
+namespace v3 {
+
+constexpr int WAVES_M = 2, WAVES_N = 4;
+constexpr int BLK_M = 4, BLK_N = 2;               // 32x32 blocks per wave
+constexpr int BM = WAVES_M * BLK_M * 32;          // 256
+constexpr int BN = WAVES_N * BLK_N * 32;          // 256
+constexpr int BK = 128;
+constexpr int kThreads = WAVES_M * WAVES_N * 64;  // 512
+constexpr int kBlocks = (BM + BN) / 8;            // 1 KB blocks per stage
+constexpr int kPer = kBlocks / (WAVES_M * WAVES_N);
+constexpr int kStage = kBlocks * 1024;            // 64 KB
+static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+#endif
+}
+
+__device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// Byte offset of (row R, 16-byte chunk c) in a stage.
+__device__ __forceinline__ int soff(int R, int c) {
+  const int b = R >> 3, r = R & 7;
+  return b * 1024 + ((r << 3) + (c ^ r ^ (b & 1))) * 16;
+}
+
+// Epilogue of one wave's BLK_M x BLK_N blocks of 32x32 int32 accumulators.
+// Element r of block (i, j) in lane l is row rb + i*32 + (r/4)*8 + (l/32)*4 +
+// r%4, column cb + j*32 + l%32: each store instruction writes 128 contiguous
+// bytes of two rows.
+template <int EPI>
+__device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int rb, int cb,
+                                           int l32, int hi) {
+  if constexpr (EPI == kEpiI32) {
+#pragma unroll
+    for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) {
+        const int col = cb + j * 32 + l32;
+        if (col >= p.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+          if (row < p.M) p.C_i32[static_cast<size_t>(row) * p.ldc + col] = acc[i][j][r];
+        }
+      }
+    return;
+  } else {
+    float ws[BLK_N], bs[BLK_N];
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j) {
+      const int col = cb + j * 32 + l32;
+      const bool ok = col < p.N;
+      ws[j] = ok ? p.w_scale[col] : 0.0f;
+      bs[j] = (ok && p.bias) ? p.bias[col] : 0.0f;
+    }
+    if constexpr (EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope) {
+      static_assert(BLK_N % 2 == 0, "QKV epilogue needs whole 64-column heads per wave");
+      // Blocks (2g, 2g+1) are one head of Q, K or V: lane column l32 holds
+      // head dims l32 and 32 + l32 -- exactly a rotary pair.
+#pragma unroll
+      for (int g = 0; g < BLK_N / 2; ++g) {
+        const int hc = cb + g * 64;
+        if (hc >= p.N) break;
+        const int which = hc / p.d_model;
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+            if (row >= p.M) continue;
+            const float as = p.a_scale[row];
+            float x1 = __builtin_fmaf(static_cast<float>(acc[i][2 * g][r]), as * ws[2 * g], bs[2 * g]);
+            float x2 = __builtin_fmaf(static_cast<float>(acc[i][2 * g + 1][r]), as * ws[2 * g + 1], bs[2 * g + 1]);
+            if (which < 2) {
+              if (which == 0) {
+                x1 *= p.q_scale;
+                x2 *= p.q_scale;
+              }
+              const int ps = p.pos[row];
+              const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
+              const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
+              const float y1 = x1 * ct[l32] - x2 * st[l32];
+              const float y2 = x2 * ct[l32 + 32] + x1 * st[l32 + 32];
+              x1 = y1;
+              x2 = y2;
+            }
+            if constexpr (EPI == kEpiQkvRopeF32) {
+              float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + hc + l32;
+              dst[0] = x1;
+              dst[32] = x2;
+            } else {
+              const size_t o = static_cast<size_t>(row) * p.d_model + (hc - which * p.d_model) + l32;
+              if (which == 2) {
+                p.v_out[o] = f32_to_f16_bits(x1);
+                p.v_out[o + 32] = f32_to_f16_bits(x2);
+              } else {
+                uint16_t* dst = which == 0 ? p.q_out : p.k_out;
+                dst[o] = p.qk_fp16 ? f32_to_f16_bits(x1) : f32_to_bf16_bits(x1);
+                dst[o + 32] = p.qk_fp16 ? f32_to_f16_bits(x2) : f32_to_bf16_bits(x2);
+              }
+            }
+          }
+      }
+      return;
+    } else {
+      constexpr bool kMax = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
+      float tmax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+          const bool rok = row < p.M;
+          const float as = rok ? p.a_scale[row] : 0.0f;
+          float rmax = 0.0f;
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j) {
+            const int col = cb + j * 32 + l32;
+            float v = __builtin_fmaf(static_cast<float>(acc[i][j][r]), as * ws[j], bs[j]);
+            if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
+            if (rok && col < p.N) {
+              const size_t o = static_cast<size_t>(row) * p.ldc + col;
+              if constexpr (EPI == kEpiF32Resid) {
+                p.C_f32[o] += v;
+              } else if constexpr (EPI == kEpiF32GeluQ) {
+                p.C_f16[o] = f32_to_f16_bits(v);
+                rmax = fmaxf(rmax, fabsf(v));
+              } else {
+                p.C_f32[o] = v;
+                rmax = fmaxf(rmax, fabsf(v));
+              }
+            }
+          }
+          if constexpr (kMax) {
+            if (p.row_absmax) {
+              // The 32 lanes of a half-wave hold the same row.
+#pragma unroll
+              for (int off = 16; off >= 1; off >>= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, off, kWave));
+              if (l32 == 0 && rok) atomic_max_nonneg(p.row_absmax + row, rmax);
+            }
+            tmax = fmaxf(tmax, rmax);
+          }
+        }
+      if constexpr (kMax) {
+        if (p.tensor_absmax) {
+          tmax = wave_max(tmax);
+          if ((threadIdx.x & 63) == 0) atomic_max_nonneg(p.tensor_absmax, tmax);
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
+  __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
+
+  int m0, n0;
+  tile_origin(p.M, p.N, BM, BN, &m0, &n0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int l32 = lane & 31, hi = lane >> 5;
+
+  // Load blocks wave*kPer .. +kPer of each stage: blocks [0, BM/8) are A row
+  // groups, the rest W row groups. Rows past the edge re-read the last valid
+  // row (their products are never stored).
+  const int8_t* gp[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int b = wave * kPer + i;
+    const int r = lane >> 3;
+    const int c = (lane & 7) ^ r ^ (b & 1);
+    const bool is_a = b < BM / 8;
+    const int row = is_a ? min(m0 + b * 8 + r, p.M - 1) : min(n0 + (b - BM / 8) * 8 + r, p.N - 1);
+    gp[i] = (is_a ? p.A + static_cast<size_t>(row) * p.lda : p.W + static_cast<size_t>(row) * p.ldw) + c * 16;
+  }
+  int8_t* ldst = smem + wave * kPer * 1024;
+  const int nk = p.K / BK;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) dma16(gp[i], ldst + i * 1024);
+
+  i32x16 acc[BLK_M][BLK_N];
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int arow = wm * BLK_M * 32 + l32;       // A fragment rows (+ i*32)
+  const int brow = BM + wn * BLK_N * 32 + l32;  // W fragment rows (+ j*32)
+  for (int kt = 0; kt < nk; ++kt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (kt + 1 < nk) {
+      int8_t* dst = ldst + ((kt + 1) & 1) * kStage;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) dma16(gp[i] + (kt + 1) * BK, dst + i * 1024);
+    }
+    const int8_t* cur = smem + (kt & 1) * kStage;
+#pragma unroll
+    for (int q = 0; q < BK / 32; ++q) {
+      const int c = 2 * q + hi;
+      i32x4 fa[BLK_M], fb[BLK_N];
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i) fa[i] = *reinterpret_cast<const i32x4*>(cur + soff(arow + i * 32, c));
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) fb[j] = *reinterpret_cast<const i32x4*>(cur + soff(brow + j * 32, c));
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+    }
+  }
+
+  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi);
+}
+
+}  // namespace v3
 }  // namespace
 
-hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
-  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+namespace {
+
+hipError_t launch_v1(const GemmI8Args& p, int epi, hipStream_t s) {
   const int tiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
   const dim3 grid(tiles), block(Cfg::THREADS);
   switch (epi) {
@@ -338,6 +599,43 @@ hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
+  using namespace v3;
+  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const dim3 grid(tiles), block(kThreads);
+  switch (epi) {
+    case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiI32>), grid, block, 0, s, p); break;
+    case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32>), grid, block, 0, s, p); break;
+    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32Gelu>), grid, block, 0, s, p); break;
+    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32Resid>), grid, block, 0, s, p); break;
+    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRope>), grid, block, 0, s, p); break;
+    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRopeF32>), grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_i8_pipelined_ok(const GemmI8Args& p) {
+  return p.K > 0 && p.K % v3::BK == 0 && p.lda % 16 == 0 && p.ldw % 16 == 0 && p.lda >= p.K && p.ldw >= p.K &&
+         reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && reinterpret_cast<uintptr_t>(p.W) % 16 == 0;
+}
+
+hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epi, int variant, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (variant == 2) {
+    if (!gemm_i8_pipelined_ok(p)) return hipErrorInvalidValue;
+    return launch_v3(p, epi, s);
+  }
+  return launch_v1(p, epi, s);
+}
+
+hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
+  return launch_gemm_i8_variant(p, epi, gemm_i8_pipelined_ok(p) ? 2 : 1, s);
 }
 
 }  // namespace esm_gfx950

@@ -49,7 +49,12 @@ struct GemmI8Args {
   float q_scale = 1.0f;
 };
 
+// Picks the pipelined 256x256 kernel when gemm_i8_pipelined_ok(p) (K a
+// multiple of 128, 16-byte aligned rows), else the general 256x128 kernel.
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epilogue, hipStream_t s);
+bool gemm_i8_pipelined_ok(const GemmI8Args& p);
+// variant 1: general kernel; 2: pipelined kernel (fails on shapes it cannot take).
+hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epilogue, int variant, hipStream_t s);
 
 // ---------------------------------------------------------------- FP32 GEMM
 enum GemmF32Epilogue : int {
@@ -103,14 +108,22 @@ constexpr int kAttnMfmaQTile = 128;
 constexpr int kAttnF32QTile = 64;
 
 // ------------------------------------------------------------ elementwise
-hipError_t launch_layernorm(const float* x, const float* gamma,
+// LayerNorm of x [rows, d]; with resid != null x is first updated in place
+// (x += resid) and normalised after the add.
+hipError_t launch_layernorm(float* x, const float* resid, const float* gamma,
                             const float* beta, float eps, float* out,
                             int rows, int d, float* tensor_absmax,
                             hipStream_t s);
-// LayerNorm fused with per-token symmetric int8 quantisation.
-hipError_t launch_layernorm_quant(const float* x, const float* gamma,
+// LayerNorm (with the same optional residual add) fused with per-token
+// symmetric int8 quantisation.
+hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gamma,
                                   const float* beta, float eps, int rows,
                                   int d, int8_t* q, int ldq, float* scales,
+                                  hipStream_t s);
+// GELU (erf of Abramowitz & Stegun 7.1.26) fused with per-token int8
+// quantisation of fp32 rows (cols % 4 == 0, cols <= 10240).
+hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols,
+                                  int8_t* q, int ldq, float* scales,
                                   hipStream_t s);
 // Per-row (per-token) quantisation. src_kind: 0 fp32, 1 fp16, 2 bf16.
 hipError_t launch_quant_rows(const void* x, int src_kind, int ldx, int rows,
