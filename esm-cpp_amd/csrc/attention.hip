@@ -274,10 +274,17 @@ __device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// With rope_cos/rope_sin non-null, Q and K arrive un-rotated and the kernel
+// applies RoPE (reference RopeApplyVarlenRef, src/kernels/rope.cpp:47-70) at
+// each token's position inside its sequence -- the query / key index -- in
+// the reference's fp32 expression: for i < 32, lo = x[i], hi = x[i+32],
+// x[i] = lo*cos[i] - hi*sin[i], x[i+32] = hi*cos[i+32] + lo*sin[i+32]. The
+// tables are [max_len, 64], half-then-half (RopeBuildTables layout).
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, int ld, const int* __restrict__ cu,
-    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out,
+    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
   __shared__ __attribute__((aligned(16))) uint8_t sKh[KC * kKPitchX];
   __shared__ __attribute__((aligned(16))) uint8_t sKl[KC * kKPitchX];
   __shared__ __attribute__((aligned(16))) uint8_t sVh[64 * kVPitchX];
@@ -296,24 +303,40 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 
   // Q fragments (B operand of S^T = K Q^T): lane (lr, lg) holds query lr of
   // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8).
+  // The lane's dims lg*8+j (first half) and 32+lg*8+j (second half) are
+  // rotary partners, so RoPE on Q is lane-local.
   f16x8 qh[2][2], ql[2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     int qi = qbase + qb * 16 + lr;
     qi = qi < L ? qi : L - 1;
     const float* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
+    float x[2][8];
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const float4 a = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8);
       const float4 b = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8 + 4);
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      x[half][0] = a.x; x[half][1] = a.y; x[half][2] = a.z; x[half][3] = a.w;
+      x[half][4] = b.x; x[half][5] = b.y; x[half][6] = b.z; x[half][7] = b.w;
+    }
+    if (rope_cos) {
+      const float* ct = rope_cos + static_cast<size_t>(qi) * 64 + lg * 8;
+      const float* st = rope_sin + static_cast<size_t>(qi) * 64 + lg * 8;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const SplitH sp = split_f16(x[j] * kQPre);
+        const float lo = x[0][j], hi = x[1][j];
+        x[0][j] = lo * ct[j] - hi * st[j];
+        x[1][j] = hi * ct[j + 32] + lo * st[j + 32];
+      }
+    }
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const SplitH sp = split_f16(x[half][j] * kQPre);
         qh[qb][half][j] = sp.hi;
         ql[qb][half][j] = sp.lo;
       }
-    }
   }
 
   f32x4 o[2][4];
@@ -328,8 +351,9 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   for (int kc0 = 0; kc0 < L; kc0 += KC) {
     const int nkeys = min(KC, L - kc0);
     __syncthreads();
-    // K chunk, split: KC keys x 16 float4 per key; rows past the sequence
-    // are zero.
+    // K chunk, split: KC keys x 16 float4 per key (lane bits 0-3 = chunk,
+    // so a chunk's rotary partner, chunk ^ 8, is lane ^ 8); rows past the
+    // sequence are zero.
 #pragma unroll
     for (int i = 0; i < KC * 16 / 256; ++i) {
       const int idx = tid + 256 * i;
@@ -337,6 +361,25 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
       if (key < nkeys)
         x = *reinterpret_cast<const float4*>(k + static_cast<size_t>(start + kc0 + key) * ld + hoff + c4 * 4);
+      if (rope_cos) {
+        float4 y;
+        y.x = __shfl_xor(x.x, 8, kWave);
+        y.y = __shfl_xor(x.y, 8, kWave);
+        y.z = __shfl_xor(x.z, 8, kWave);
+        y.w = __shfl_xor(x.w, 8, kWave);
+        if (key < nkeys) {
+          const int pos = kc0 + key;
+          const float4 cs = *reinterpret_cast<const float4*>(rope_cos + static_cast<size_t>(pos) * 64 + c4 * 4);
+          const float4 sn = *reinterpret_cast<const float4*>(rope_sin + static_cast<size_t>(pos) * 64 + c4 * 4);
+          if (c4 < 8) {  // x is the low half, y its partner
+            x = make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y, x.z * cs.z - y.z * sn.z,
+                            x.w * cs.w - y.w * sn.w);
+          } else {       // x is the high half
+            x = make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y, x.z * cs.z + y.z * sn.z,
+                            x.w * cs.w + y.w * sn.w);
+          }
+        }
+      }
       const SplitH a = split_f16(x.x), b = split_f16(x.y), c = split_f16(x.z), d = split_f16(x.w);
       *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.hi, b.hi), pack_h2(c.hi, d.hi));
       *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.lo, b.lo), pack_h2(c.lo, d.lo));
@@ -552,10 +595,11 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 
 hipError_t launch_attention_x3(const float* q, const float* k, const float* v, int ld,
                                const int* cu_seqlens, const AttnWork* work, int num_work,
-                               float* out, int ld_out, hipStream_t s) {
+                               float* out, int ld_out, const float* rope_cos, const float* rope_sin,
+                               hipStream_t s) {
   if (num_work <= 0) return hipSuccess;
   hipLaunchKernelGGL(attn_x3_kernel, dim3(num_work), dim3(256), 0, s, q, k, v, ld, cu_seqlens, work, out,
-                     ld_out);
+                     ld_out, rope_cos, rope_sin);
   return hipGetLastError();
 }
 

@@ -567,7 +567,7 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork));
     int slot;
     ESM_TRY(ctx->time_begin("attention", &slot));
-    ESM_HIP(ctx, launch_attention_x3(q, k, v, ld, d_cu, d_work, nwork, out, ld, ctx->stream));
+    ESM_HIP(ctx, launch_attention_x3(q, k, v, ld, d_cu, d_work, nwork, out, ld, nullptr, nullptr, ctx->stream));
     ESM_TRY(ctx->time_end(slot));
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
@@ -652,6 +652,9 @@ struct esm_gfx950_model {
   size_t meta_bytes = 0;
   hipEvent_t meta_done = nullptr;
   int rope_len = 0;  // rows currently in the device rope tables
+  // W8A8 models: Q's 1/sqrt(head_dim) multiplied into the Q weight scales and
+  // bias at upload (exact when it is a power of two).
+  bool q_scale_folded = false;
   // The staged batch (esm_gfx950_batch_upload).
   int staged_T = 0, staged_B = 0, staged_work = 0;
 };
@@ -677,8 +680,9 @@ int upload_f(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const T* src, size_t n, T
 }
 
 // Concatenates the given linears along N into one device weight.
+// part0_scale multiplies part 0's per-channel scales and bias (int8 only).
 int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_linear_desc* const* parts,
-                  int nparts, int N_each, int K, bool int8, DevLinear* out) {
+                  int nparts, int N_each, int K, bool int8, DevLinear* out, float part0_scale = 1.0f) {
   const int N = N_each * nparts;
   out->N = N;
   out->K = K;
@@ -688,6 +692,8 @@ int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_lin
     if (!parts[p]->bias) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "model_create: null bias");
     std::memcpy(bias.data() + static_cast<size_t>(p) * N_each, parts[p]->bias, N_each * sizeof(float));
   }
+  if (int8 && part0_scale != 1.0f)
+    for (int n = 0; n < N_each; ++n) bias[n] *= part0_scale;
   ESM_TRY(upload_f(ctx, m, bias.data(), bias.size(), &out->bias));
   if (int8) {
     std::vector<int8_t> w(static_cast<size_t>(N) * out->ldk, 0);
@@ -700,6 +706,8 @@ int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_lin
                     parts[p]->w_i8 + static_cast<size_t>(n) * K, K);
       std::memcpy(s.data() + static_cast<size_t>(p) * N_each, parts[p]->w_scale, N_each * sizeof(float));
     }
+    if (part0_scale != 1.0f)
+      for (int n = 0; n < N_each; ++n) s[n] *= part0_scale;
     ESM_TRY(upload_f(ctx, m, w.data(), w.size(), &out->w8));
     ESM_TRY(upload_f(ctx, m, s.data(), s.size(), &out->ws));
   } else {
@@ -751,6 +759,14 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   m->cfg = c;
   const int d = c.hidden_size, f = c.intermediate_size, V = c.vocab_size;
   const bool i8 = c.weights_int8 != 0;
+  // ScaleInplace(q, 1/sqrt(dh)) after the Q projection (reference
+  // src/model.cpp:975-979) commutes exactly with the dequant fma when the
+  // factor is a power of two: fma(acc, a*(w*f), b*f) == fma(acc, a*w, b)*f.
+  const float q_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+  int q_exp = 0;
+  const bool pow2 = std::frexp(q_scale, &q_exp) == 0.5f;
+  const float q_fold = (i8 && pow2) ? q_scale : 1.0f;
+  m->q_scale_folded = i8 && pow2;
   int rc = ESM_GFX950_OK;
   auto step = [&](int r) {
     if (rc == ESM_GFX950_OK) rc = r;
@@ -769,7 +785,7 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
     const esm_gfx950_linear_desc* o1[1] = {&L.out};
     const esm_gfx950_linear_desc* f1[1] = {&L.fc1};
     const esm_gfx950_linear_desc* f2[1] = {&L.fc2};
-    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, qkv, 3, d, d, i8, &D.qkv));
+    if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, qkv, 3, d, d, i8, &D.qkv, q_fold));
     if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, o1, 1, d, d, i8, &D.out));
     if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, f1, 1, f, d, i8, &D.fc1));
     if (rc == ESM_GFX950_OK) step(upload_linear(ctx, m, f2, 1, d, f, i8, &D.fc2));
@@ -950,10 +966,18 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.pos = md.pos;
   g.rope_cos = md.cos_t;
   g.rope_sin = md.sin_t;
-  g.q_scale = q_scale;
+  // Q's 1/sqrt(dh) is already in the Q weight scales and bias when it is a
+  // power of two (see model_create); otherwise the epilogues apply it.
+  g.q_scale = m->q_scale_folded ? 1.0f : q_scale;
   const bool f32qkv = qkv_is_f32(c);
   ESM_TRY(ctx->time_begin("qkv", &slot));
-  if (f32qkv && dh == kHeadDimMfma) {
+  if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
+    // Plain dequant + bias; RoPE is applied inside the attention kernel.
+    if (!m->q_scale_folded) return ctx->fail(ESM_GFX950_INTERNAL, "F16X3 attention needs a folded Q scale");
+    g.C_f32 = a.qkv;
+    g.ldc = 3 * d;
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+  } else if (f32qkv && dh == kHeadDimMfma) {
     // Dequant + bias, Q scale and RoPE fused; fp32 Q|K|V rows.
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
@@ -962,7 +986,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
-    ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+    ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, g.q_scale, s));
     ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   } else {
     g.q_out = a.qb;
@@ -979,7 +1003,8 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   ESM_TRY(ctx->time_begin("attention", &slot));
   if (f32qkv) {
     if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
-      ESM_HIP(ctx, launch_attention_x3(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, md.cu, md.work, nwork, a.attn, d, s));
+      ESM_HIP(ctx, launch_attention_x3(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, md.cu, md.work, nwork, a.attn, d,
+                                       md.cos_t, md.sin_t, s));
     } else {
       ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
                                         d, s));

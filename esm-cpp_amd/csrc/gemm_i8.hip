@@ -391,9 +391,12 @@ __device__ __forceinline__ int soff(int R, int c) {
 // Element r of block (i, j) in lane l is row rb + i*32 + (r/4)*8 + (l/32)*4 +
 // r%4, column cb + j*32 + l%32: each store instruction writes 128 contiguous
 // bytes of two rows.
+// s_as / s_ws / s_bs: the tile's activation scales (by row - m0), weight
+// scales and bias (by column - n0), staged in LDS at kernel start.
 template <int EPI>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int rb, int cb,
-                                           int l32, int hi) {
+                                           int l32, int hi, const float* s_as, const float* s_ws,
+                                           const float* s_bs, int m0, int n0) {
   if constexpr (EPI == kEpiI32) {
 #pragma unroll
     for (int i = 0; i < BLK_M; ++i)
@@ -412,10 +415,9 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
     float ws[BLK_N], bs[BLK_N];
 #pragma unroll
     for (int j = 0; j < BLK_N; ++j) {
-      const int col = cb + j * 32 + l32;
-      const bool ok = col < p.N;
-      ws[j] = ok ? p.w_scale[col] : 0.0f;
-      bs[j] = (ok && p.bias) ? p.bias[col] : 0.0f;
+      const int c = cb + j * 32 + l32 - n0;
+      ws[j] = s_ws[c];
+      bs[j] = s_bs[c];
     }
     if constexpr (EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope) {
       static_assert(BLK_N % 2 == 0, "QKV epilogue needs whole 64-column heads per wave");
@@ -432,7 +434,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
           for (int r = 0; r < 16; ++r) {
             const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
             if (row >= p.M) continue;
-            const float as = p.a_scale[row];
+            const float as = s_as[row - m0];
             float x1 = __builtin_fmaf(static_cast<float>(acc[i][2 * g][r]), as * ws[2 * g], bs[2 * g]);
             float x2 = __builtin_fmaf(static_cast<float>(acc[i][2 * g + 1][r]), as * ws[2 * g + 1], bs[2 * g + 1]);
             if (which < 2) {
@@ -475,7 +477,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
         for (int r = 0; r < 16; ++r) {
           const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
           const bool rok = row < p.M;
-          const float as = rok ? p.a_scale[row] : 0.0f;
+          const float as = s_as[row - m0];
           float rmax = 0.0f;
 #pragma unroll
           for (int j = 0; j < BLK_N; ++j) {
@@ -518,9 +520,26 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
   __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
+  __shared__ float s_as[BM], s_ws[BN], s_bs[BN];
+  static_assert(kThreads == BM + BN, "one thread per staged row / column scale");
 
   int m0, n0;
   tile_origin(p.M, p.N, BM, BN, &m0, &n0);
+  if constexpr (EPI != kEpiI32) {
+    // Per-row activation scales and per-column weight scales / bias of the
+    // tile, read once here instead of per element in the epilogue.
+    const int t = threadIdx.x;
+    if (t < BM) {
+      const int row = m0 + t;
+      s_as[t] = row < p.M ? p.a_scale[row] : 0.0f;
+    } else {
+      const int c = t - BM, col = n0 + c;
+      const bool ok = col < p.N;
+      s_ws[c] = ok ? p.w_scale[col] : 0.0f;
+      s_bs[c] = (ok && p.bias) ? p.bias[col] : 0.0f;
+    }
+    __syncthreads();
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -577,7 +596,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     }
   }
 
-  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi);
+  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi, s_as, s_ws, s_bs, m0, n0);
 }
 
 }  // namespace v3

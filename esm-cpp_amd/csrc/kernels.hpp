@@ -95,10 +95,13 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 // Split-fp16 MFMA path, head_dim 64: fp32 q/k/v (row stride ld), each
 // operand carried as fp16 hi + lo with three MFMAs per product (fp32-level
 // accuracy on the fp16 matrix cores). Same work list as the MFMA path.
+// With rope_cos/rope_sin ([max_len, 64] tables) non-null, q and k are
+// rotated inside the kernel at each token's in-sequence position.
 hipError_t launch_attention_x3(const float* q, const float* k, const float* v,
                                int ld, const int* cu_seqlens,
                                const AttnWork* work, int num_work, float* out,
-                               int ld_out, hipStream_t s);
+                               int ld_out, const float* rope_cos,
+                               const float* rope_sin, hipStream_t s);
 // Exact fp32 path for any head_dim <= 128 (one thread per query).
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
                                 int ld, int head_dim, const int* cu_seqlens,
