@@ -244,49 +244,50 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 
 // ---- Split-fp16 MFMA path (head_dim 64): fp32 accuracy on fp16 MFMA.
 //
-// Every fp32 operand x is carried as an unevaluated sum hi + lo of two fp16
-// values (hi = fp16(x), lo = fp16(x - hi), 22 significant bits together),
+// Every operand arrives as split-fp16 words (low half fp16(x), high half
+// fp16(x - fp16(x)): 22 significant bits together), written by the QKV
+// GEMM epilogue after RoPE (or by launch_pack_split for the op-level entry),
 // and each product uses three MFMAs: hi*hi + lo*hi + hi*lo (the dropped
-// lo*lo term is below 2^-22 relative). Q is multiplied by 8 before the
-// split (exact: a power of two) so the lo parts of the pre-scaled Q stay
-// normal fp16; the factor is folded back into the exp2 argument. Layout and
-// wave roles are those of the single-fp16 kernel above: S^T = K Q^T puts each
-// lane's probabilities in the B-operand layout of O^T = V^T P^T. The
-// running sum uses the fp32 probabilities, so the normalisation is that of
-// the reference's fp32/double softmax (attention.cpp:118-139).
+// lo*lo term is below 2^-22 relative). Q comes multiplied by a power of two
+// (q_prescale) so the lo parts of the small pre-scaled Q stay normal fp16;
+// the factor is divided back out in the exp2 argument. Layout and wave roles
+// are those of the single-fp16 kernel above: S^T = K Q^T puts each lane's
+// probabilities in the B-operand layout of O^T = V^T P^T. The running sum
+// uses the fp32 probabilities, so the normalisation is that of the
+// reference's fp32/double softmax (attention.cpp:118-139). Staging is
+// branch-free: rows past the sequence are loaded clamped and zeroed by
+// select, then the words are unpacked into hi/lo planes with v_perm.
+constexpr int KCX = 64;                 // keys per LDS chunk
 constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
-constexpr int kVPitchX = KC * 2 + 16;   // bytes per dim row of V^T hi / lo
-constexpr float kQPre = 8.0f;
+constexpr int kVPitchX = KCX * 2 + 16;  // bytes per dim row of V^T hi / lo
 
-struct SplitH {
-  _Float16 hi, lo;
-};
-__device__ __forceinline__ SplitH split_f16(float x) {
-  const _Float16 h = static_cast<_Float16>(x);
-  return SplitH{h, static_cast<_Float16>(x - static_cast<float>(h))};
-}
-__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+// Low (sel_lo) or high (sel_hi) 16-bit halves of two words, packed: the hi
+// or lo fp16 parts of two consecutive values.
+constexpr uint32_t kSelLo = 0x05040100u, kSelHi = 0x07060302u;
+__device__ __forceinline__ uint32_t halves(uint32_t first, uint32_t second, uint32_t sel) {
+  return __builtin_amdgcn_perm(second, first, sel);
 }
 
 __device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// With rope_cos/rope_sin non-null, Q and K arrive un-rotated and the kernel
-// applies RoPE (reference RopeApplyVarlenRef, src/kernels/rope.cpp:47-70) at
-// each token's position inside its sequence -- the query / key index -- in
-// the reference's fp32 expression: for i < 32, lo = x[i], hi = x[i+32],
-// x[i] = lo*cos[i] - hi*sin[i], x[i+32] = hi*cos[i+32] + lo*sin[i+32]. The
-// tables are [max_len, 64], half-then-half (RopeBuildTables layout).
+// 8 split words -> f16x8 hi and lo parts.
+__device__ __forceinline__ void unpack8(const uint4& a, const uint4& b, f16x8* hi, f16x8* lo) {
+  const uint32_t h[4] = {halves(a.x, a.y, kSelLo), halves(a.z, a.w, kSelLo), halves(b.x, b.y, kSelLo),
+                         halves(b.z, b.w, kSelLo)};
+  const uint32_t l[4] = {halves(a.x, a.y, kSelHi), halves(a.z, a.w, kSelHi), halves(b.x, b.y, kSelHi),
+                         halves(b.z, b.w, kSelHi)};
+  *hi = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(h));
+  *lo = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(l));
+}
+
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
-    const float* __restrict__ q, const float* __restrict__ k,
-    const float* __restrict__ v, int ld, const int* __restrict__ cu,
-    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out,
-    const float* __restrict__ rope_cos, const float* __restrict__ rope_sin) {
-  __shared__ __attribute__((aligned(16))) uint8_t sKh[KC * kKPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sKl[KC * kKPitchX];
+    const uint32_t* __restrict__ q, const uint32_t* __restrict__ k,
+    const uint32_t* __restrict__ v, int ld, float s2, const int* __restrict__ cu,
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
+  __shared__ __attribute__((aligned(16))) uint8_t sKh[KCX * kKPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sKl[KCX * kKPitchX];
   __shared__ __attribute__((aligned(16))) uint8_t sVh[64 * kVPitchX];
   __shared__ __attribute__((aligned(16))) uint8_t sVl[64 * kVPitchX];
 
@@ -303,40 +304,17 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 
   // Q fragments (B operand of S^T = K Q^T): lane (lr, lg) holds query lr of
   // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8).
-  // The lane's dims lg*8+j (first half) and 32+lg*8+j (second half) are
-  // rotary partners, so RoPE on Q is lane-local.
   f16x8 qh[2][2], ql[2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    int qi = qbase + qb * 16 + lr;
-    qi = qi < L ? qi : L - 1;
-    const float* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
-    float x[2][8];
+    const int qi = min(qbase + qb * 16 + lr, L - 1);
+    const uint32_t* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const float4 a = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8);
-      const float4 b = *reinterpret_cast<const float4*>(qp + half * 32 + lg * 8 + 4);
-      x[half][0] = a.x; x[half][1] = a.y; x[half][2] = a.z; x[half][3] = a.w;
-      x[half][4] = b.x; x[half][5] = b.y; x[half][6] = b.z; x[half][7] = b.w;
+      const uint4 a = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8);
+      const uint4 b = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8 + 4);
+      unpack8(a, b, &qh[qb][half], &ql[qb][half]);
     }
-    if (rope_cos) {
-      const float* ct = rope_cos + static_cast<size_t>(qi) * 64 + lg * 8;
-      const float* st = rope_sin + static_cast<size_t>(qi) * 64 + lg * 8;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float lo = x[0][j], hi = x[1][j];
-        x[0][j] = lo * ct[j] - hi * st[j];
-        x[1][j] = hi * ct[j + 32] + lo * st[j + 32];
-      }
-    }
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const SplitH sp = split_f16(x[half][j] * kQPre);
-        qh[qb][half][j] = sp.hi;
-        ql[qb][half][j] = sp.lo;
-      }
   }
 
   f32x4 o[2][4];
@@ -346,71 +324,60 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     for (int db = 0; db < 4; ++db) o[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mrun[2] = {-INFINITY, -INFINITY};
   float lrun[2] = {0.f, 0.f};
-  constexpr float kS2 = kLog2e / kQPre;
 
-  for (int kc0 = 0; kc0 < L; kc0 += KC) {
-    const int nkeys = min(KC, L - kc0);
-    __syncthreads();
-    // K chunk, split: KC keys x 16 float4 per key (lane bits 0-3 = chunk,
-    // so a chunk's rotary partner, chunk ^ 8, is lane ^ 8); rows past the
-    // sequence are zero.
+  for (int kc0 = 0; kc0 < L; kc0 += KCX) {
+    const int nkeys = min(KCX, L - kc0);
+    const uint32_t* kbase = k + static_cast<size_t>(start + kc0) * ld + hoff;
+    const uint32_t* vbase = v + static_cast<size_t>(start + kc0) * ld + hoff;
+    // Global loads for the whole chunk first (K: KCX keys x 16 uint4; V: KCX/2
+    // key pairs x 16 dim quads), clamped to the last key and zeroed past it.
+    uint4 kr[KCX * 16 / 256], va[KCX / 2 * 16 / 256], vb[KCX / 2 * 16 / 256];
 #pragma unroll
-    for (int i = 0; i < KC * 16 / 256; ++i) {
+    for (int i = 0; i < KCX * 16 / 256; ++i) {
       const int idx = tid + 256 * i;
       const int key = idx >> 4, c4 = idx & 15;
-      float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (key < nkeys)
-        x = *reinterpret_cast<const float4*>(k + static_cast<size_t>(start + kc0 + key) * ld + hoff + c4 * 4);
-      if (rope_cos) {
-        float4 y;
-        y.x = __shfl_xor(x.x, 8, kWave);
-        y.y = __shfl_xor(x.y, 8, kWave);
-        y.z = __shfl_xor(x.z, 8, kWave);
-        y.w = __shfl_xor(x.w, 8, kWave);
-        if (key < nkeys) {
-          const int pos = kc0 + key;
-          const float4 cs = *reinterpret_cast<const float4*>(rope_cos + static_cast<size_t>(pos) * 64 + c4 * 4);
-          const float4 sn = *reinterpret_cast<const float4*>(rope_sin + static_cast<size_t>(pos) * 64 + c4 * 4);
-          if (c4 < 8) {  // x is the low half, y its partner
-            x = make_float4(x.x * cs.x - y.x * sn.x, x.y * cs.y - y.y * sn.y, x.z * cs.z - y.z * sn.z,
-                            x.w * cs.w - y.w * sn.w);
-          } else {       // x is the high half
-            x = make_float4(x.x * cs.x + y.x * sn.x, x.y * cs.y + y.y * sn.y, x.z * cs.z + y.z * sn.z,
-                            x.w * cs.w + y.w * sn.w);
-          }
-        }
-      }
-      const SplitH a = split_f16(x.x), b = split_f16(x.y), c = split_f16(x.z), d = split_f16(x.w);
-      *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.hi, b.hi), pack_h2(c.hi, d.hi));
-      *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) = make_uint2(pack_h2(a.lo, b.lo), pack_h2(c.lo, d.lo));
+      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(min(key, nkeys - 1)) * ld + c4 * 4);
     }
-    // V chunk, split and transposed to V^T[dim][key]: each item is a key
-    // pair x 4 dims.
 #pragma unroll
-    for (int i = 0; i < KC / 2 * 16 / 256; ++i) {
+    for (int i = 0; i < KCX / 2 * 16 / 256; ++i) {
       const int idx = tid + 256 * i;
-      const int dq = idx & 15, kp = idx >> 4;
-      const int key0 = 2 * kp;
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-      const float* vp = v + static_cast<size_t>(start + kc0 + key0) * ld + hoff + dq * 4;
-      if (key0 < nkeys) a = *reinterpret_cast<const float4*>(vp);
-      if (key0 + 1 < nkeys) b = *reinterpret_cast<const float4*>(vp + ld);
-      const float xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
+      const int dq = idx & 15, key0 = 2 * (idx >> 4);
+      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0, nkeys - 1)) * ld + dq * 4);
+      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0 + 1, nkeys - 1)) * ld + dq * 4);
+    }
+    __syncthreads();  // the previous chunk's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < KCX * 16 / 256; ++i) {
+      const int idx = tid + 256 * i;
+      const int key = idx >> 4, c4 = idx & 15;
+      const uint4 x = key < nkeys ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) =
+          make_uint2(halves(x.x, x.y, kSelLo), halves(x.z, x.w, kSelLo));
+      *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) =
+          make_uint2(halves(x.x, x.y, kSelHi), halves(x.z, x.w, kSelHi));
+    }
+    // V^T[dim][key]: each item is a key pair x 4 dims.
+#pragma unroll
+    for (int i = 0; i < KCX / 2 * 16 / 256; ++i) {
+      const int idx = tid + 256 * i;
+      const int dq = idx & 15, key0 = 2 * (idx >> 4);
+      const uint4 a = key0 < nkeys ? va[i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 b = key0 + 1 < nkeys ? vb[i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const SplitH sa = split_f16(xa[j]), sb = split_f16(xb[j]);
         const int off = (dq * 4 + j) * kVPitchX + key0 * 2;
-        *reinterpret_cast<uint32_t*>(sVh + off) = pack_h2(sa.hi, sb.hi);
-        *reinterpret_cast<uint32_t*>(sVl + off) = pack_h2(sa.lo, sb.lo);
+        *reinterpret_cast<uint32_t*>(sVh + off) = halves(xa[j], xb[j], kSelLo);
+        *reinterpret_cast<uint32_t*>(sVl + off) = halves(xa[j], xb[j], kSelHi);
       }
     }
     __syncthreads();
     if (!active) continue;
 
     const int nkb = (nkeys + 15) >> 4;
-    f32x4 s[8][2];
+    f32x4 s[KCX / 16][2];
 #pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
+    for (int kb = 0; kb < KCX / 16; ++kb) {
       if (kb < nkb) {
         const int off = (kb * 16 + lr) * kKPitchX + lg * 16;
         const f16x8 kh0 = *reinterpret_cast<const f16x8*>(sKh + off);
@@ -438,12 +405,12 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     for (int qb = 0; qb < 2; ++qb) {
       float cmax = -INFINITY;
 #pragma unroll
-      for (int kb = 0; kb < 8; ++kb) {
+      for (int kb = 0; kb < KCX / 16; ++kb) {
         if (kb < nkb) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kb * 16 + lg * 4 + i;
-            const float sv = key < nkeys ? s[kb][qb][i] * kS2 : -INFINITY;
+            const float sv = key < nkeys ? s[kb][qb][i] * s2 : -INFINITY;
             s[kb][qb][i] = sv;
             cmax = fmaxf(cmax, sv);
           }
@@ -461,23 +428,24 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 
     // O^T += V^T P^T over key-block pairs, three MFMAs per product.
 #pragma unroll
-    for (int kp = 0; kp < 4; ++kp) {
+    for (int kp = 0; kp < KCX / 32; ++kp) {
       if (2 * kp < nkb) {
         f16x8 pfh[2], pfl[2];
         const bool two = 2 * kp + 1 < nkb;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           float psum = 0.f;
+          uint32_t wd[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int kb = 2 * kp + (j >> 2);
             float p = 0.f;
             if (j < 4 || two) p = exp2f(s[kb][qb][j & 3] - mnew[qb]);
             psum += p;
-            const SplitH sp = split_f16(p);
-            pfh[qb][j] = sp.hi;
-            pfl[qb][j] = sp.lo;
+            wd[j] = split_f16_word(p);
           }
+          const uint4 a = make_uint4(wd[0], wd[1], wd[2], wd[3]), b = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+          unpack8(a, b, &pfh[qb], &pfl[qb]);
           lrun[qb] += psum;
         }
 #pragma unroll
@@ -516,6 +484,16 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         *reinterpret_cast<float4*>(orow + db * 16) =
             make_float4(o[qb][db][0] * inv, o[qb][db][1] * inv, o[qb][db][2] * inv, o[qb][db][3] * inv);
     }
+  }
+}
+
+__global__ void pack_split_kernel(const float* __restrict__ x, int ld_x, int rows, int cols, float scale,
+                                  uint32_t* __restrict__ out, int ld_out) {
+  const size_t total = static_cast<size_t>(rows) * cols;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t r = i / cols, c = i % cols;
+    out[r * ld_out + c] = split_f16_word(x[r * ld_x + c] * scale);
   }
 }
 
@@ -593,13 +571,24 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
   return hipGetLastError();
 }
 
-hipError_t launch_attention_x3(const float* q, const float* k, const float* v, int ld,
-                               const int* cu_seqlens, const AttnWork* work, int num_work,
-                               float* out, int ld_out, const float* rope_cos, const float* rope_sin,
+hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v, int ld, float q_prescale,
+                               const int* cu_seqlens, const AttnWork* work, int num_work, float* out, int ld_out,
                                hipStream_t s) {
   if (num_work <= 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_x3_kernel, dim3(num_work), dim3(256), 0, s, q, k, v, ld, cu_seqlens, work, out,
-                     ld_out, rope_cos, rope_sin);
+  const float s2 = kLog2e / q_prescale;
+  hipLaunchKernelGGL(attn_x3_kernel, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work, out,
+                     ld_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_split(const float* x, int ld_x, int rows, int cols, float scale, uint32_t* out, int ld_out,
+                             hipStream_t s) {
+  const size_t n = static_cast<size_t>(rows) * cols;
+  if (n == 0) return hipSuccess;
+  size_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL(pack_split_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, ld_x, rows, cols, scale,
+                     out, ld_out);
   return hipGetLastError();
 }
 

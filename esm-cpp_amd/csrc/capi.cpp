@@ -20,6 +20,9 @@ using namespace esm_gfx950;
 namespace {
 
 constexpr int kHeadDimMfma = 64;
+// Power of two applied to Q before its split-fp16 split: keeps the lo parts
+// of the pre-scaled (|q| ~ 0.1) values out of the fp16 subnormal range.
+constexpr float kQPrescale = 8.0f;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int pad16(int k) { return (k + 15) & ~15; }
@@ -561,13 +564,25 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "attention_varlen: unknown precision");
   ESM_REQUIRE(ctx, head_dim == kHeadDimMfma, "attention_varlen: the MFMA path needs head_dim == 64");
   if (precision == ESM_GFX950_ATTN_F16X3_MFMA) {
+    // Pack the fp32 operands into split-fp16 words (Q times kQPrescale), then
+    // run the split-fp16 kernel.
+    const size_t n = static_cast<size_t>(T) * ld;
+    const size_t wbytes = align_up(n * 4, 256);
     int* d_cu;
     AttnWork* d_work;
     int nwork;
-    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork));
+    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 3 * wbytes, &d_cu, &d_work,
+                                 &nwork));
+    char* base = static_cast<char*>(ctx->scratch);
+    auto* qw = reinterpret_cast<uint32_t*>(base);
+    auto* kw = reinterpret_cast<uint32_t*>(base + wbytes);
+    auto* vw = reinterpret_cast<uint32_t*>(base + 2 * wbytes);
+    ESM_HIP(ctx, launch_pack_split(q, ld, T, ld, kQPrescale, qw, ld, ctx->stream));
+    ESM_HIP(ctx, launch_pack_split(k, ld, T, ld, 1.0f, kw, ld, ctx->stream));
+    ESM_HIP(ctx, launch_pack_split(v, ld, T, ld, 1.0f, vw, ld, ctx->stream));
     int slot;
     ESM_TRY(ctx->time_begin("attention", &slot));
-    ESM_HIP(ctx, launch_attention_x3(q, k, v, ld, d_cu, d_work, nwork, out, ld, nullptr, nullptr, ctx->stream));
+    ESM_HIP(ctx, launch_attention_x3(qw, kw, vw, ld, kQPrescale, d_cu, d_work, nwork, out, ld, ctx->stream));
     ESM_TRY(ctx->time_end(slot));
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
@@ -972,11 +987,12 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   const bool f32qkv = qkv_is_f32(c);
   ESM_TRY(ctx->time_begin("qkv", &slot));
   if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
-    // Plain dequant + bias; RoPE is applied inside the attention kernel.
-    if (!m->q_scale_folded) return ctx->fail(ESM_GFX950_INTERNAL, "F16X3 attention needs a folded Q scale");
+    // Dequant + bias, Q scale, RoPE, then every value stored as a split-fp16
+    // word (Q times kQPrescale) for the split-fp16 attention kernel.
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
-    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    g.q_prescale = kQPrescale;
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvSplit, s));
   } else if (f32qkv && dh == kHeadDimMfma) {
     // Dequant + bias, Q scale and RoPE fused; fp32 Q|K|V rows.
     g.C_f32 = a.qkv;
@@ -1003,8 +1019,8 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   ESM_TRY(ctx->time_begin("attention", &slot));
   if (f32qkv) {
     if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
-      ESM_HIP(ctx, launch_attention_x3(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, md.cu, md.work, nwork, a.attn, d,
-                                       md.cos_t, md.sin_t, s));
+      const auto* w = reinterpret_cast<const uint32_t*>(a.qkv);
+      ESM_HIP(ctx, launch_attention_x3(w, w + d, w + 2 * d, 3 * d, kQPrescale, md.cu, md.work, nwork, a.attn, d, s));
     } else {
       ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
                                         d, s));

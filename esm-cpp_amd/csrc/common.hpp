@@ -55,6 +55,16 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Split-fp16 word: fp16(x) in the low half, fp16(x - fp16(x)) in the high
+// half. x - fp16(x) is exact in fp32, so hi + lo keeps 22 significant bits of
+// x (lo is subnormal when |x| < 2^-3, i.e. absolute error <= 2^-25 there).
+__device__ __forceinline__ uint32_t split_f16_word(float x) {
+  const _Float16 h = static_cast<_Float16>(x);
+  const _Float16 l = static_cast<_Float16>(x - static_cast<float>(h));
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l)) << 16);
+}
+
 // Non-negative IEEE floats order like their bit patterns, so an unsigned
 // atomic max on the bits is a float max (used for absmax reductions).
 __device__ __forceinline__ void atomic_max_nonneg(float* addr, float v) {

@@ -396,7 +396,7 @@ __device__ __forceinline__ int soff(int R, int c) {
 template <int EPI>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int rb, int cb,
                                            int l32, int hi, const float* s_as, const float* s_ws,
-                                           const float* s_bs, int m0, int n0) {
+                                           const float* s_bs, const int* s_pos, int m0, int n0) {
   if constexpr (EPI == kEpiI32) {
 #pragma unroll
     for (int i = 0; i < BLK_M; ++i)
@@ -419,7 +419,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       ws[j] = s_ws[c];
       bs[j] = s_bs[c];
     }
-    if constexpr (EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope) {
+    if constexpr (EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit) {
       static_assert(BLK_N % 2 == 0, "QKV epilogue needs whole 64-column heads per wave");
       // Blocks (2g, 2g+1) are one head of Q, K or V: lane column l32 holds
       // head dims l32 and 32 + l32 -- exactly a rotary pair.
@@ -442,7 +442,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
                 x1 *= p.q_scale;
                 x2 *= p.q_scale;
               }
-              const int ps = p.pos[row];
+              const int ps = s_pos[row - m0];
               const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
               const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
               const float y1 = x1 * ct[l32] - x2 * st[l32];
@@ -454,6 +454,14 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
               float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + hc + l32;
               dst[0] = x1;
               dst[32] = x2;
+            } else if constexpr (EPI == kEpiQkvSplit) {
+              if (which == 0) {
+                x1 *= p.q_prescale;
+                x2 *= p.q_prescale;
+              }
+              uint32_t* dst = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(row) * p.ldc + hc + l32;
+              dst[0] = split_f16_word(x1);
+              dst[32] = split_f16_word(x2);
             } else {
               const size_t o = static_cast<size_t>(row) * p.d_model + (hc - which * p.d_model) + l32;
               if (which == 2) {
@@ -521,7 +529,9 @@ template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
   __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
   __shared__ float s_as[BM], s_ws[BN], s_bs[BN];
+  __shared__ int s_pos[BM];
   static_assert(kThreads == BM + BN, "one thread per staged row / column scale");
+  constexpr bool kRope = EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit;
 
   int m0, n0;
   tile_origin(p.M, p.N, BM, BN, &m0, &n0);
@@ -532,6 +542,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     if (t < BM) {
       const int row = m0 + t;
       s_as[t] = row < p.M ? p.a_scale[row] : 0.0f;
+      if constexpr (kRope) s_pos[t] = row < p.M ? p.pos[row] : 0;
     } else {
       const int c = t - BM, col = n0 + c;
       const bool ok = col < p.N;
@@ -596,7 +607,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     }
   }
 
-  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi, s_as, s_ws, s_bs, m0, n0);
+  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi, s_as, s_ws, s_bs, s_pos, m0, n0);
 }
 
 }  // namespace v3
@@ -632,6 +643,7 @@ hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRope>), grid, block, 0, s, p); break;
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32GeluQ>), grid, block, 0, s, p); break;
     case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRopeF32>), grid, block, 0, s, p); break;
+    case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvSplit>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -20,7 +20,12 @@ enum GemmEpilogue : int {
   kEpiQkvRope = 4,    // split Q|K|V, Q*q_scale, RoPE on Q and K, bf16/fp16 out
   kEpiF32GeluQ = 5,   // gelu(...) -> fp16 store + per-row absmax (atomic)
   kEpiQkvRopeF32 = 6, // fp32 [M, 3*d_model] (ldc): Q*q_scale and RoPE on Q, K
+  kEpiQkvSplit = 7,   // as kEpiQkvRopeF32, then Q *= q_prescale and every value
+                      // stored as a split-fp16 word (C_f32 reinterpreted)
 };
+
+// Split-fp16 word of an fp32 value x: low half fp16(x), high half
+// fp16(x - fp16(x)); hi + lo carries 22 significant bits.
 
 struct GemmI8Args {
   const int8_t* A = nullptr;
@@ -44,9 +49,10 @@ struct GemmI8Args {
   int qk_fp16 = 0;            // Q/K stored as fp16 (else bf16)
   int d_model = 0;
   const int* pos = nullptr;          // [M] position inside the sequence
-  const float* rope_cos = nullptr;   // [max_len, 32]
+  const float* rope_cos = nullptr;   // [max_len, 64]
   const float* rope_sin = nullptr;   // [max_len, 32]
   float q_scale = 1.0f;
+  float q_prescale = 1.0f;  // kEpiQkvSplit: power of two applied to Q before the split
 };
 
 // Picks the pipelined 256x256 kernel when gemm_i8_pipelined_ok(p) (K a
@@ -92,16 +98,17 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
                                  const AttnWork* work, int num_work, float* out,
                                  int ld_out, float* tensor_absmax,
                                  hipStream_t s);
-// Split-fp16 MFMA path, head_dim 64: fp32 q/k/v (row stride ld), each
-// operand carried as fp16 hi + lo with three MFMAs per product (fp32-level
-// accuracy on the fp16 matrix cores). Same work list as the MFMA path.
-// With rope_cos/rope_sin ([max_len, 64] tables) non-null, q and k are
-// rotated inside the kernel at each token's in-sequence position.
-hipError_t launch_attention_x3(const float* q, const float* k, const float* v,
-                               int ld, const int* cu_seqlens,
+// Split-fp16 MFMA path, head_dim 64: q/k/v as split-fp16 words (row stride
+// ld words; q already multiplied by q_prescale), three MFMAs per product
+// (fp32-level accuracy on the fp16 matrix cores). Same work list as the
+// MFMA path; softmax logits are (q.k) / q_prescale.
+hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v,
+                               int ld, float q_prescale, const int* cu_seqlens,
                                const AttnWork* work, int num_work, float* out,
-                               int ld_out, const float* rope_cos,
-                               const float* rope_sin, hipStream_t s);
+                               int ld_out, hipStream_t s);
+// fp32 [rows, cols] (row stride ld_x) -> split-fp16 words of x * scale.
+hipError_t launch_pack_split(const float* x, int ld_x, int rows, int cols, float scale,
+                             uint32_t* out, int ld_out, hipStream_t s);
 // Exact fp32 path for any head_dim <= 128 (one thread per query).
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
                                 int ld, int head_dim, const int* cu_seqlens,
