@@ -407,7 +407,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          if (row < p.M) p.C_i32[static_cast<size_t>(row) * p.ldc + col] = acc[i][j][r];
+          if (row < p.M) __builtin_nontemporal_store(acc[i][j][r], p.C_i32 + static_cast<size_t>(row) * p.ldc + col);
         }
       }
     return;
@@ -460,8 +460,8 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
                 x2 *= p.q_prescale;
               }
               uint32_t* dst = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(row) * p.ldc + hc + l32;
-              dst[0] = split_f16_word(x1);
-              dst[32] = split_f16_word(x2);
+              __builtin_nontemporal_store(split_f16_word(x1), dst);
+              __builtin_nontemporal_store(split_f16_word(x2), dst + 32);
             } else {
               const size_t o = static_cast<size_t>(row) * p.d_model + (hc - which * p.d_model) + l32;
               if (which == 2) {
@@ -500,7 +500,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
                 p.C_f16[o] = f32_to_f16_bits(v);
                 rmax = fmaxf(rmax, fabsf(v));
               } else {
-                p.C_f32[o] = v;
+                __builtin_nontemporal_store(v, p.C_f32 + o);
                 rmax = fmaxf(rmax, fabsf(v));
               }
             }
