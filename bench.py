@@ -106,6 +106,8 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=64)
     ap.add_argument("--cpu-iters", type=int, default=3)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--parts", type=int, default=2,
+                    help="concurrent sequence groups (streams) in the throughput pass")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the packed forward "
@@ -124,19 +126,24 @@ def main():
     model = eg.Model(dev, weights, int8=True, act_mode=mode)
     T = batch.total_tokens
     logits = dev.empty((T, cfg.vocab_size), np.float32)
+    model.set_parts(args.parts)
     model.upload_batch(batch.ids, batch.cu)
     for _ in range(args.warmup):
         model.forward_device(logits)
     dev.sync()
     log("warmup done")
 
-    # Timed region without per-kernel events (throughput), then with them
-    # (per-site kernel durations for the roofline).
+    # Timed region without per-kernel events (throughput), then with them on
+    # one stream (per-site kernel durations for the roofline).
     dev.sync()
     dev.timer_start()
     for _ in range(args.steps):
         model.forward_device(logits)
     ms_plain = dev.timer_stop() / args.steps
+    if args.parts != 1:
+        model.set_parts(1)
+        model.upload_batch(batch.ids, batch.cu)
+        model.forward_device(logits)
     dev.kernel_timing(True)
     dev.sync()
     dev.timer_start()
@@ -213,7 +220,8 @@ def main():
                                f"{len(batch.lengths)} sequences",
                    "tokens": T, "residues": residues, "sequences": int(len(batch.lengths)),
                    "act_quant": "per-token" if mode == eg.ACT_PER_TOKEN else "per-tensor",
-                   "attention": "split-fp16 (hi+lo, 3 MFMAs per product) fp32-accurate MFMA", "parallelism": "single GPU"},
+                   "attention": "split-fp16 (hi+lo, 3 MFMAs per product) fp32-accurate MFMA", "parallelism": "single GPU",
+                   "streams": args.parts},
         "tokens_per_s": round(T / (ms_plain * 1e-3), 1),
         "ms_per_step_with_kernel_events": round(ms_events, 3),
         "kernel_sites": sites,

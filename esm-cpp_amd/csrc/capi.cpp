@@ -657,21 +657,28 @@ struct esm_gfx950_model {
   float *lm_dense_w = nullptr, *lm_dense_b = nullptr;
   float *lm_ln_w = nullptr, *lm_ln_b = nullptr;
   float* dec_bias = nullptr;
-  // Arena (grown when T exceeds every earlier batch).
-  void* arena = nullptr;
-  size_t arena_bytes = 0;
-  int cap_T = 0, cap_B = 0, cap_L = 0;
-  // Pinned host staging for per-batch metadata.
-  void* meta_host = nullptr;
-  void* meta_dev = nullptr;
-  size_t meta_bytes = 0;
-  hipEvent_t meta_done = nullptr;
-  int rope_len = 0;  // rows currently in the device rope tables
   // W8A8 models: Q's 1/sqrt(head_dim) multiplied into the Q weight scales and
   // bias at upload (exact when it is a power of two).
   bool q_scale_folded = false;
-  // The staged batch (esm_gfx950_batch_upload).
-  int staged_T = 0, staged_B = 0, staged_work = 0;
+  // A staged batch is split into `parts` contiguous sequence groups; each
+  // part has its own arena, metadata and (with more than one part) its own
+  // HIP stream, so the parts' kernels can occupy different CUs at the same
+  // time. Part p's tokens are rows [t0, t0 + T) of the packed batch.
+  struct Part {
+    void* arena = nullptr;  // grown when the part exceeds every earlier batch
+    size_t arena_bytes = 0;
+    int cap_T = 0, cap_B = 0, cap_L = 0;
+    void* meta_host = nullptr;  // pinned staging of the per-batch metadata
+    void* meta_dev = nullptr;
+    size_t meta_bytes = 0;
+    hipEvent_t meta_done = nullptr;  // the part's metadata copy has consumed meta_host
+    hipEvent_t done = nullptr;       // the part's forward has finished (join)
+    hipStream_t stream = nullptr;    // null: the context stream
+    int rope_len = 0;                // rows currently in the device rope tables
+    int T = 0, B = 0, nwork = 0, t0 = 0;
+  };
+  std::vector<Part> parts = std::vector<Part>(1);
+  int staged_T = 0;  // tokens of the staged batch (all parts)
 };
 
 namespace {
@@ -737,13 +744,28 @@ int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_lin
   return ESM_GFX950_OK;
 }
 
+void free_part(esm_gfx950_model::Part& p) {
+  if (p.arena) hipFree(p.arena);
+  if (p.meta_dev) hipFree(p.meta_dev);
+  if (p.meta_host) hipHostFree(p.meta_host);
+  if (p.meta_done) hipEventDestroy(p.meta_done);
+  if (p.done) hipEventDestroy(p.done);
+  if (p.stream) hipStreamDestroy(p.stream);
+  p = esm_gfx950_model::Part();
+}
+
 void free_model(esm_gfx950_model* m) {
   for (void* p : m->allocations) hipFree(p);
-  if (m->arena) hipFree(m->arena);
-  if (m->meta_dev) hipFree(m->meta_dev);
-  if (m->meta_host) hipHostFree(m->meta_host);
-  if (m->meta_done) hipEventDestroy(m->meta_done);
+  for (auto& p : m->parts) free_part(p);
   delete m;
+}
+
+// Events (and, for multi-part models, a stream) of one part.
+int init_part(esm_gfx950_ctx* ctx, esm_gfx950_model::Part& p, bool own_stream) {
+  ESM_HIP(ctx, hipEventCreateWithFlags(&p.meta_done, hipEventDisableTiming));
+  ESM_HIP(ctx, hipEventCreateWithFlags(&p.done, hipEventDisableTiming));
+  if (own_stream) ESM_HIP(ctx, hipStreamCreate(&p.stream));
+  return ESM_GFX950_OK;
 }
 
 }  // namespace
@@ -812,8 +834,7 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   step(upload_f(ctx, m, desc->lm_ln_w, d, &m->lm_ln_w));
   step(upload_f(ctx, m, desc->lm_ln_b, d, &m->lm_ln_b));
   step(upload_f(ctx, m, desc->lm_decoder_bias, V, &m->dec_bias));
-  if (rc == ESM_GFX950_OK && hipEventCreateWithFlags(&m->meta_done, hipEventDisableTiming) != hipSuccess)
-    rc = ctx->fail(ESM_GFX950_HIP_ERROR, "hipEventCreate failed");
+  if (rc == ESM_GFX950_OK) step(init_part(ctx, m->parts[0], false));
   if (rc != ESM_GFX950_OK) {
     hipStreamSynchronize(ctx->stream);
     free_model(m);
@@ -841,7 +862,9 @@ extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_mod
 
 extern "C" int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes) {
   if (!model || !bytes) return ESM_GFX950_INVALID_ARGUMENT;
-  *bytes = model->arena_bytes + model->meta_bytes;
+  size_t b = 0;
+  for (const auto& p : model->parts) b += p.arena_bytes + p.meta_bytes;
+  *bytes = b;
   return ESM_GFX950_OK;
 }
 
@@ -1154,88 +1177,97 @@ constexpr float kTokenDropoutMaskRatioTrain = 0.15f * 0.8f;
 
 }  // namespace
 
-extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
-                                       const int32_t* cu, int B, int T) {
-  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
-  ESM_TRY(validate_batch(ctx, cu, B, T));
-  const auto& c = m->cfg;
-  m->staged_T = 0;
-  if (T == 0) return ESM_GFX950_OK;
-  ESM_REQUIRE(ctx, ids, "batch_upload: null ids");
-  const int V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
-  for (int t = 0; t < T; ++t)
-    if (ids[t] < 0 || ids[t] >= V)
-      return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_packed: token id out of range at " + std::to_string(t));
-  int maxL = 0;
-  for (int b = 0; b < B; ++b) maxL = std::max(maxL, cu[b + 1] - cu[b]);
+namespace {
 
-  // Grow the arena and metadata buffers only when this batch exceeds them.
-  if (T > m->cap_T || B > m->cap_B || maxL > m->cap_L) {
+// Makes ctx->stream refer to a part's stream for the launches of that part.
+struct StreamScope {
+  esm_gfx950_ctx* ctx;
+  hipStream_t saved;
+  StreamScope(esm_gfx950_ctx* c, hipStream_t s) : ctx(c), saved(c->stream) {
+    if (s) ctx->stream = s;
+  }
+  ~StreamScope() { ctx->stream = saved; }
+};
+
+// Stages one part: sequences [b0, b0 + B) of the packed batch, tokens
+// [cu[b0], cu[b0 + B]).
+int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part& P, const int32_t* ids,
+               const int32_t* cu, int b0, int B) {
+  const auto& c = m->cfg;
+  const int H = c.num_heads, dh = c.head_dim;
+  const int t0 = cu[b0];
+  const int T = cu[b0 + B] - t0;
+  int maxL = 0;
+  for (int b = b0; b < b0 + B; ++b) maxL = std::max(maxL, cu[b + 1] - cu[b]);
+  StreamScope scope(ctx, P.stream);
+
+  // Grow the arena and metadata buffers only when this part exceeds them.
+  if (T > P.cap_T || B > P.cap_B || maxL > P.cap_L) {
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    const int nT = std::max(T, m->cap_T), nB = std::max(B, m->cap_B), nL = std::max(maxL, m->cap_L);
-    if (m->arena) hipFree(m->arena);
-    if (m->meta_dev) hipFree(m->meta_dev);
-    if (m->meta_host) hipHostFree(m->meta_host);
-    m->arena = m->meta_dev = m->meta_host = nullptr;
-    m->arena_bytes = m->meta_bytes = 0;
-    m->cap_T = m->cap_B = m->cap_L = 0;
+    const int nT = std::max(T, P.cap_T), nB = std::max(B, P.cap_B), nL = std::max(maxL, P.cap_L);
+    if (P.arena) hipFree(P.arena);
+    if (P.meta_dev) hipFree(P.meta_dev);
+    if (P.meta_host) hipHostFree(P.meta_host);
+    P.arena = P.meta_dev = P.meta_host = nullptr;
+    P.arena_bytes = P.meta_bytes = 0;
+    P.cap_T = P.cap_B = P.cap_L = 0;
     const Arena probe = layout(c, nT, nullptr);
     const Meta mprobe = meta_layout(nT, nB, nL, H, dh, nullptr);
-    ESM_HIP(ctx, hipMalloc(&m->arena, probe.bytes));
-    m->arena_bytes = probe.bytes;
-    ESM_HIP(ctx, hipMalloc(&m->meta_dev, mprobe.bytes));
-    ESM_HIP(ctx, hipHostMalloc(&m->meta_host, mprobe.bytes, hipHostMallocDefault));
-    m->meta_bytes = mprobe.bytes;
-    m->cap_T = nT;
-    m->cap_B = nB;
-    m->cap_L = nL;
-    m->rope_len = 0;
+    ESM_HIP(ctx, hipMalloc(&P.arena, probe.bytes));
+    P.arena_bytes = probe.bytes;
+    ESM_HIP(ctx, hipMalloc(&P.meta_dev, mprobe.bytes));
+    ESM_HIP(ctx, hipHostMalloc(&P.meta_host, mprobe.bytes, hipHostMallocDefault));
+    P.meta_bytes = mprobe.bytes;
+    P.cap_T = nT;
+    P.cap_B = nB;
+    P.cap_L = nL;
+    P.rope_len = 0;
   }
-  const Meta mh = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_host));
+  const Meta mh = meta_layout(P.cap_T, P.cap_B, P.cap_L, H, dh, static_cast<char*>(P.meta_host));
 
   // Host metadata: ids, per-token embedding scale (Embed, model.cpp:737-778),
-  // positions, cu_seqlens, attention work list, rope tables.
-  ESM_HIP(ctx, hipEventSynchronize(m->meta_done));
-  std::memcpy(mh.ids, ids, static_cast<size_t>(T) * 4);
+  // positions, cu_seqlens (rebased to the part), attention work list, rope
+  // tables.
+  ESM_HIP(ctx, hipEventSynchronize(P.meta_done));
+  std::memcpy(mh.ids, ids + t0, static_cast<size_t>(T) * 4);
+  for (int b = 0; b <= B; ++b) mh.cu[b] = cu[b0 + b] - t0;
   for (int b = 0; b < B; ++b) {
     int src_len = 0, masks = 0;
-    for (int t = cu[b]; t < cu[b + 1]; ++t) {
+    for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) {
       ++src_len;
-      if (ids[t] == c.mask_token_id) ++masks;
+      if (mh.ids[t] == c.mask_token_id) ++masks;
     }
     const float ratio = src_len > 0 ? static_cast<float>(masks) / static_cast<float>(src_len) : 0.0f;
     const float scale = (1.0f - kTokenDropoutMaskRatioTrain) / std::max(1.0f - ratio, 1e-12f);
-    for (int t = cu[b]; t < cu[b + 1]; ++t) mh.tok_scale[t] = scale;
+    for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) mh.tok_scale[t] = scale;
   }
-  build_pos(cu, B, mh.pos);
-  std::memcpy(mh.cu, cu, static_cast<size_t>(B + 1) * 4);
+  build_pos(mh.cu, B, mh.pos);
   const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
   std::vector<AttnWork> work;
-  build_work(cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
+  build_work(mh.cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
   std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));
-  const bool new_tables = m->rope_len < maxL;
-  if (new_tables) rope_tables(m->cap_L, dh, mh.cos_t, mh.sin_t);
-  const size_t upto = reinterpret_cast<const char*>(mh.cos_t) - static_cast<const char*>(m->meta_host);
-  ESM_HIP(ctx, hipMemcpyAsync(m->meta_dev, m->meta_host, new_tables ? m->meta_bytes : upto, hipMemcpyHostToDevice,
+  const bool new_tables = P.rope_len < maxL;
+  if (new_tables) rope_tables(P.cap_L, dh, mh.cos_t, mh.sin_t);
+  const size_t upto = reinterpret_cast<const char*>(mh.cos_t) - static_cast<const char*>(P.meta_host);
+  ESM_HIP(ctx, hipMemcpyAsync(P.meta_dev, P.meta_host, new_tables ? P.meta_bytes : upto, hipMemcpyHostToDevice,
                               ctx->stream));
-  ESM_HIP(ctx, hipEventRecord(m->meta_done, ctx->stream));
-  if (new_tables) m->rope_len = m->cap_L;
-  m->staged_T = T;
-  m->staged_B = B;
-  m->staged_work = static_cast<int>(work.size());
+  ESM_HIP(ctx, hipEventRecord(P.meta_done, ctx->stream));
+  if (new_tables) P.rope_len = P.cap_L;
+  P.T = T;
+  P.B = B;
+  P.t0 = t0;
+  P.nwork = static_cast<int>(work.size());
   return ESM_GFX950_OK;
 }
 
-extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* m, float* logits) {
-  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+// The whole forward of one part on ctx->stream; logits rows [0, T).
+int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx950_model::Part& P, float* logits) {
   const auto& c = m->cfg;
-  const int T = m->staged_T;
-  if (T == 0) return ESM_GFX950_OK;
-  ESM_REQUIRE(ctx, logits, "forward_device: null logits");
+  const int T = P.T;
   const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
-  const Arena a = layout(c, m->cap_T, static_cast<char*>(m->arena));
-  const Meta md = meta_layout(m->cap_T, m->cap_B, m->cap_L, H, dh, static_cast<char*>(m->meta_dev));
-  const int nwork = m->staged_work;
+  const Arena a = layout(c, P.cap_T, static_cast<char*>(P.arena));
+  const Meta md = meta_layout(P.cap_T, P.cap_B, P.cap_L, H, dh, static_cast<char*>(P.meta_dev));
+  const int nwork = P.nwork;
 
   hipStream_t s = ctx->stream;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
@@ -1271,6 +1303,79 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   return ESM_GFX950_OK;
 }
 
+}  // namespace
+
+extern "C" int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* m, int parts) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, parts >= 1 && parts <= 4, "model_set_parts: parts must be 1..4");
+  if (static_cast<int>(m->parts.size()) == parts) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (auto& p : m->parts) {
+    if (p.stream) ESM_HIP(ctx, hipStreamSynchronize(p.stream));
+    free_part(p);
+  }
+  m->parts.assign(parts, esm_gfx950_model::Part());
+  for (int i = 0; i < parts; ++i) ESM_TRY(init_part(ctx, m->parts[i], parts > 1));
+  m->staged_T = 0;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                       const int32_t* cu, int B, int T) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu, B, T));
+  m->staged_T = 0;
+  for (auto& p : m->parts) p.T = p.B = 0;
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, ids, "batch_upload: null ids");
+  const int V = m->cfg.vocab_size;
+  for (int t = 0; t < T; ++t)
+    if (ids[t] < 0 || ids[t] >= V)
+      return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_packed: token id out of range at " + std::to_string(t));
+  // Contiguous sequence groups of about T / parts tokens each (never empty).
+  // A per-tensor activation scale spans the whole batch, so that mode keeps
+  // the batch in one part.
+  const bool whole = m->cfg.weights_int8 && m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR;
+  const int np = whole ? 1 : std::min<int>(static_cast<int>(m->parts.size()), B);
+  int b0 = 0;
+  for (int p = 0; p < np; ++p) {
+    int b1 = b0 + 1;
+    const long target = static_cast<long>(T) * (p + 1) / np;
+    while (b1 < B - (np - 1 - p) && cu[b1] < target) ++b1;
+    if (p == np - 1) b1 = B;
+    ESM_TRY(stage_part(ctx, m, m->parts[p], ids, cu, b0, b1 - b0));
+    b0 = b1;
+  }
+  m->staged_T = T;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* m, float* logits) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  if (m->staged_T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, logits, "forward_device: null logits");
+  const int V = m->cfg.vocab_size;
+  if (m->parts.size() == 1) return forward_part(ctx, m, m->parts[0], logits);
+  ESM_REQUIRE(ctx,
+              !(m->cfg.weights_int8 && m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR) || m->parts[1].T == 0,
+              "forward_device: batch staged in several parts before the switch to per-tensor scales; upload it again");
+  // Fork: every part's stream waits for the work queued so far on the
+  // context stream, runs its forward, and the context stream joins them.
+  esm_gfx950_model::Part& P0 = m->parts[0];
+  ESM_HIP(ctx, hipEventRecord(P0.done, ctx->stream));
+  for (auto& P : m->parts)
+    if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(P.stream, P0.done, 0));
+  for (auto& P : m->parts) {
+    if (P.T == 0) continue;
+    StreamScope scope(ctx, P.stream);
+    ESM_TRY(forward_part(ctx, m, P, logits + static_cast<size_t>(P.t0) * V));
+    ESM_HIP(ctx, hipEventRecord(P.done, P.stream));
+  }
+  for (auto& P : m->parts)
+    if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
                                          const int32_t* cu, int B, int T, float* logits, int logits_on_device) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
@@ -1278,10 +1383,31 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   if (T == 0) return ESM_GFX950_OK;
   ESM_REQUIRE(ctx, logits, "forward_packed: null logits");
   if (logits_on_device) return esm_gfx950_forward_device(ctx, m, logits);
-  const Arena a = layout(m->cfg, m->cap_T, static_cast<char*>(m->arena));
-  ESM_TRY(esm_gfx950_forward_device(ctx, m, a.logits));
-  ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * m->cfg.vocab_size * 4,
-                              hipMemcpyDeviceToHost, ctx->stream));
+  // Host logits: each part writes its rows into its own arena, then one
+  // device-to-host copy per part after the join.
+  const int V = m->cfg.vocab_size;
+  if (m->parts.size() == 1) {
+    const esm_gfx950_model::Part& P = m->parts[0];
+    const Arena a = layout(m->cfg, P.cap_T, static_cast<char*>(P.arena));
+    ESM_TRY(forward_part(ctx, m, P, a.logits));
+    ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * V * 4, hipMemcpyDeviceToHost, ctx->stream));
+  } else {
+    esm_gfx950_model::Part& P0 = m->parts[0];
+    ESM_HIP(ctx, hipEventRecord(P0.done, ctx->stream));
+    for (auto& P : m->parts)
+      if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(P.stream, P0.done, 0));
+    for (auto& P : m->parts) {
+      if (P.T == 0) continue;
+      StreamScope scope(ctx, P.stream);
+      const Arena a = layout(m->cfg, P.cap_T, static_cast<char*>(P.arena));
+      ESM_TRY(forward_part(ctx, m, P, a.logits));
+      ESM_HIP(ctx, hipMemcpyAsync(logits + static_cast<size_t>(P.t0) * V, a.logits, static_cast<size_t>(P.T) * V * 4,
+                                  hipMemcpyDeviceToHost, P.stream));
+      ESM_HIP(ctx, hipEventRecord(P.done, P.stream));
+    }
+    for (auto& P : m->parts)
+      if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
+  }
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
 }

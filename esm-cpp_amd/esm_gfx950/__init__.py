@@ -40,7 +40,7 @@ EXPORTED = [
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
     "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
-    "esm_gfx950_model_arena_bytes",
+    "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts",
 ]
 
 
@@ -99,6 +99,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_batch_upload": (i32, [vp, vp, vp, vp, i32, i32]),
         "esm_gfx950_forward_device": (i32, [vp, vp, vp]),
         "esm_gfx950_model_arena_bytes": (i32, [vp, C.POINTER(sz)]),
+        "esm_gfx950_model_set_parts": (i32, [vp, vp, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -356,6 +357,10 @@ class Model:
 
     def set_act_mode(self, mode: int):
         self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))
+
+    def set_parts(self, parts: int):
+        """Concurrent sequence groups per batch (esm_gfx950_model_set_parts)."""
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_parts(self.dev.ctx, self.handle, int(parts)))
 
     def forward_packed(self, ids: np.ndarray, cu: np.ndarray, out: Optional[DeviceArray] = None):
         """Packed forward; returns host logits [T, vocab] or fills `out` on device."""

@@ -264,6 +264,14 @@ int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const 
 /* Runs the forward on the staged batch with every input already in HBM;
  * logits fp32 [T, vocab] go to DEVICE memory. Stream-ordered, no host sync. */
 int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, float* logits);
+/* Splits every later staged batch into `parts` (1..4) contiguous groups of
+ * whole sequences with about equal token counts; with parts > 1 each group
+ * gets its own arena and HIP stream (default priority), and forward_device
+ * forks from / joins back to the context stream, so the groups' kernels run
+ * concurrently on different CUs. Results are identical to parts = 1 (every
+ * row depends only on its own sequence). No reference counterpart: the
+ * reference's ForwardPacked (model.cpp:1093-1255) runs one thread pool. */
+int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int parts);
 /* Bytes currently held by the model's device arena (for zero-growth checks). */
 int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
 

@@ -142,3 +142,49 @@ def test_config4_varlen_full_forward_properties(dev):
         solo = m.forward_packed(batch.ids[s0:s1], np.array([0, s1 - s0], np.int32))
         np.testing.assert_allclose(logits[s0:s1], solo, rtol=1e-4, atol=1e-4)
     m.free()
+
+
+@pytest.mark.parametrize("parts", [2, 3, 4])
+def test_parts_match_single_stream(dev, w650_small, small_batch, parts):
+    """Concurrent sequence groups on separate streams: every row depends only
+    on its own sequence in per-token mode, so logits are bit-identical to the
+    one-stream forward, on the host-logits and the device-logits paths."""
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    want = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.set_parts(parts)
+    got = m.forward_packed(small_batch.ids, small_batch.cu)
+    np.testing.assert_array_equal(got, want)
+    out = dev.empty((small_batch.total_tokens, 33), np.float32)
+    m.upload_batch(small_batch.ids, small_batch.cu)
+    for _ in range(2):
+        m.forward_device(out)
+    dev.sync()
+    np.testing.assert_array_equal(out.numpy(), want)
+    # A different, smaller batch regroups the sequences (same packed-vs-serial
+    # bar as test_packed_equals_serial).
+    idx = [4, 1, 5]
+    sub = small_batch.subset(idx)
+    rows = np.concatenate([np.arange(small_batch.cu[b], small_batch.cu[b + 1]) for b in idx])
+    np.testing.assert_allclose(m.forward_packed(sub.ids, sub.cu), want[rows], rtol=1e-4, atol=1e-4)
+    m.free()
+
+
+def test_parts_per_tensor_stays_whole(dev, w650_small, small_batch):
+    """A per-tensor activation scale spans the batch: set_parts leaves such a
+    batch in one group (same logits), and a batch staged in several groups
+    before a switch to per-tensor scales is refused until uploaded again."""
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TENSOR)
+    want = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.set_parts(3)
+    np.testing.assert_array_equal(m.forward_packed(small_batch.ids, small_batch.cu), want)
+    m.set_act_mode(eg.ACT_PER_TOKEN)
+    m.upload_batch(small_batch.ids, small_batch.cu)
+    m.set_act_mode(eg.ACT_PER_TENSOR)
+    out = dev.empty((small_batch.total_tokens, 33), np.float32)
+    with pytest.raises(eg.Gfx950Error, match="upload it again"):
+        m.forward_device(out)
+    m.upload_batch(small_batch.ids, small_batch.cu)
+    m.forward_device(out)
+    dev.sync()
+    np.testing.assert_array_equal(out.numpy(), want)
+    m.free()
