@@ -22,6 +22,27 @@ __device__ __forceinline__ float act_scale_from_absmax(float amax) {
   return amax > 0.0f ? amax / 127.0f : 1.0f;
 }
 
+// Lane's NV float4 chunks of a row (chunk j at column (j*64 + lane)*4). Every
+// load is issued before any value is used: a chunk past `cols` re-reads
+// column 0 (in bounds) and is then zeroed, so no load sits in a branch that
+// would make the wave wait for it before issuing the next.
+template <int NV>
+__device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int cols, int lane, float4 (&v)[NV]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    v[j] = *reinterpret_cast<const float4*>(xr + (c < cols ? c : 0));
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool ok = (j * 64 + lane) * 4 < cols;
+    v[j].x = ok ? v[j].x : 0.0f;
+    v[j].y = ok ? v[j].y : 0.0f;
+    v[j].z = ok ? v[j].z : 0.0f;
+    v[j].w = ok ? v[j].w : 0.0f;
+  }
+}
+
 // ---- LayerNorm with the row cached in registers (d % 4 == 0, d <= NV*256).
 // With resid != null the row is first updated in place, x += resid (the
 // residual add that precedes the next LayerNorm, reference src/model.cpp:1013
@@ -36,52 +57,49 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   float* xr = x + static_cast<size_t>(row) * d;
-  const float* rr = resid ? resid + static_cast<size_t>(row) * d : nullptr;
   float4 v[NV];
-  float sum = 0.f;
+  load_row_vec<NV>(xr, d, lane, v);
+  if (resid) {
+    float4 r[NV];
+    load_row_vec<NV>(resid + static_cast<size_t>(row) * d, d, lane, r);
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (j * 64 + lane) * 4;
-    if (c < d) {
-      v[j] = *reinterpret_cast<const float4*>(xr + c);
-      if (rr) {
-        const float4 a = *reinterpret_cast<const float4*>(rr + c);
-        v[j].x += a.x;
-        v[j].y += a.y;
-        v[j].z += a.z;
-        v[j].w += a.w;
-        *reinterpret_cast<float4*>(xr + c) = v[j];
-      }
-      sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    } else {
-      v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < NV; ++j) {
+      v[j].x += r[j].x;
+      v[j].y += r[j].y;
+      v[j].z += r[j].z;
+      v[j].w += r[j].w;
+      const int c = (j * 64 + lane) * 4;
+      if (c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
     }
   }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   const float mean = wave_sum(sum) / static_cast<float>(d);
   float sq = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
-    if (c < d) {
-      const float a = v[j].x - mean, b = v[j].y - mean, e = v[j].z - mean, f = v[j].w - mean;
-      sq += (a * a + b * b) + (e * e + f * f);
-    }
+    const float a = v[j].x - mean, b = v[j].y - mean, e = v[j].z - mean, f = v[j].w - mean;
+    const float t = (a * a + b * b) + (e * e + f * f);
+    sq += c < d ? t : 0.0f;
   }
   const float var = wave_sum(sq) / static_cast<float>(d);
   const float inv_std = 1.0f / sqrtf(var + eps);
+  float4 g[NV], bt[NV];
+  load_row_vec<NV>(gamma, d, lane, g);
+  load_row_vec<NV>(beta, d, lane, bt);
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
+    float4 y;
+    y.x = (v[j].x - mean) * inv_std * g[j].x + bt[j].x;
+    y.y = (v[j].y - mean) * inv_std * g[j].y + bt[j].y;
+    y.z = (v[j].z - mean) * inv_std * g[j].z + bt[j].z;
+    y.w = (v[j].w - mean) * inv_std * g[j].w + bt[j].w;
+    v[j] = y;
     if (c < d) {
-      const float4 g = *reinterpret_cast<const float4*>(gamma + c);
-      const float4 b = *reinterpret_cast<const float4*>(beta + c);
-      float4 y;
-      y.x = (v[j].x - mean) * inv_std * g.x + b.x;
-      y.y = (v[j].y - mean) * inv_std * g.y + b.y;
-      y.z = (v[j].z - mean) * inv_std * g.z + b.z;
-      y.w = (v[j].w - mean) * inv_std * g.w + b.w;
-      v[j] = y;
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
       if constexpr (!QUANT) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = y;
     }
@@ -181,15 +199,11 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
   if (row >= rows) return;
   const float* xr = x + static_cast<size_t>(row) * ldx;
   float4 v[NV];
+  load_row_vec<NV>(xr, cols, lane, v);
   float amax = 0.f;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (j * 64 + lane) * 4;
-    if (c < cols) {
-      v[j] = *reinterpret_cast<const float4*>(xr + c);
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-    }
-  }
+  for (int j = 0; j < NV; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   const float scale = act_scale_from_absmax(wave_max(amax));
   const float inv = 1.0f / scale;
   int8_t* qr = q + static_cast<size_t>(row) * ldq;
@@ -220,19 +234,16 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
   if (row >= rows) return;
   const float* xr = x + static_cast<size_t>(row) * ldx;
   float4 v[NV];
+  load_row_vec<NV>(xr, cols, lane, v);
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int c = (j * 64 + lane) * 4;
-    if (c < cols) {
-      float4 a = *reinterpret_cast<const float4*>(xr + c);
-      a.x = gelu_as(a.x);
-      a.y = gelu_as(a.y);
-      a.z = gelu_as(a.z);
-      a.w = gelu_as(a.w);
-      v[j] = a;
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
-    }
+    // gelu(0) == 0, so zeroed chunks past `cols` stay zero.
+    v[j].x = gelu_as(v[j].x);
+    v[j].y = gelu_as(v[j].y);
+    v[j].z = gelu_as(v[j].z);
+    v[j].w = gelu_as(v[j].w);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   }
   const float scale = act_scale_from_absmax(wave_max(amax));
   const float inv = 1.0f / scale;
