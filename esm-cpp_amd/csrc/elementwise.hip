@@ -331,8 +331,9 @@ __global__ void rope_f32_kernel(float* __restrict__ x, int ld, const int* __rest
     const float* cr = cos_tab + static_cast<size_t>(p) * tab_ld;
     const float* sr = sin_tab + static_cast<size_t>(p) * tab_ld;
     const float x1 = xr[c] * pre_scale, x2 = xr[c + half] * pre_scale;
-    xr[c] = x1 * cr[c] - x2 * sr[c];
-    xr[c + half] = x2 * cr[c + half] + x1 * sr[c + half];
+    // Same fused forms as the QKV GEMM epilogue's rotation.
+    xr[c] = __builtin_fmaf(x1, cr[c], -(x2 * sr[c]));
+    xr[c + half] = __builtin_fmaf(x2, cr[c + half], x1 * sr[c + half]);
   }
 }
 

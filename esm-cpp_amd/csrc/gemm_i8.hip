@@ -387,135 +387,199 @@ __device__ __forceinline__ int soff(int R, int c) {
   return b * 1024 + ((r << 3) + (c ^ r ^ (b & 1))) * 16;
 }
 
+// RoPE cos / sin rows of a tile staged in LDS, transposed: [32 dims][BM rows
+// + pad], so that a lane reads four consecutive rows of one dim at once.
+constexpr int kRopeTPitch = BM + 4;
+
 // Epilogue of one wave's BLK_M x BLK_N blocks of 32x32 int32 accumulators.
-// Element r of block (i, j) in lane l is row rb + i*32 + (r/4)*8 + (l/32)*4 +
-// r%4, column cb + j*32 + l%32: each store instruction writes 128 contiguous
-// bytes of two rows.
-// s_as / s_ws / s_bs: the tile's activation scales (by row - m0), weight
-// scales and bias (by column - n0), staged in LDS at kernel start.
-template <int EPI>
-__device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int rb, int cb,
+// Element r of block (i, j) in lane l is tile row lr0 + i*32 + (r/4)*8 + r%4
+// (lr0 = wm*BLK_M*32 + (l/32)*4) and tile column lc0 + j*32 (lc0 =
+// wn*BLK_N*32 + l%32): each store instruction writes 128 contiguous bytes of
+// two rows. Addresses are 32-bit offsets from the tile's origin (uniform), so
+// no per-element 64-bit arithmetic is needed. FULL: the tile lies inside M x N
+// and no element needs a bounds check.
+// s_as / s_ws / s_bs: the tile's activation scales (by tile row), weight
+// scales and bias (by tile column), staged in LDS at kernel start. s_cosT /
+// s_sinT: the tile rows' RoPE tables (first half of each row; the model's
+// tables repeat it in the second half), staged after the main loop.
+// base + off elements, with the byte offset formed in 32 bits so that the
+// store adds one 32-bit lane offset to a uniform 64-bit base.
+template <class T>
+__device__ __forceinline__ T* at(T* base, uint32_t off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + off * static_cast<uint32_t>(sizeof(T)));
+}
+
+// One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
+// wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
+// rotary pair. hc: the head's first column relative to the tile origin.
+template <int EPI, bool FULL, int WHICH>
+__device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int g, int hc,
+                                         int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
+                                         const float (&bs)[BLK_N], const float* s_cosT, const float* s_sinT, int m0,
+                                         int n0) {
+  const uint32_t ldc = p.ldc;
+  const uint32_t dm = p.d_model;
+  // Row offsets: the lane's first row (lr0) times the stride once; the rest
+  // of each row index is a compile-time constant times a uniform stride.
+  const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(hc + l32);
+  const uint32_t lane_d = static_cast<uint32_t>(lr0) * dm + static_cast<uint32_t>(n0 + hc - WHICH * p.d_model + l32);
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int lr = lr0 + i * 32 + q * 8;  // rows lr .. lr+3 hold elements r = 4q .. 4q+3
+      const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
+      float4 c4, s4;
+      if constexpr (WHICH < 2) {
+        c4 = *reinterpret_cast<const float4*>(s_cosT + l32 * kRopeTPitch + lr);
+        s4 = *reinterpret_cast<const float4*>(s_sinT + l32 * kRopeTPitch + lr);
+      }
+      const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = 4 * q + u;
+        if (!FULL && m0 + lr + u >= p.M) continue;
+        float x1 = __builtin_fmaf(static_cast<float>(acc[i][2 * g][r]), asv[u] * ws[2 * g], bs[2 * g]);
+        float x2 = __builtin_fmaf(static_cast<float>(acc[i][2 * g + 1][r]), asv[u] * ws[2 * g + 1], bs[2 * g + 1]);
+        if constexpr (WHICH == 0) {
+          x1 *= p.q_scale;
+          x2 *= p.q_scale;
+        }
+        if constexpr (WHICH < 2) {
+          const float c = u == 0 ? c4.x : u == 1 ? c4.y : u == 2 ? c4.z : c4.w;
+          const float sn = u == 0 ? s4.x : u == 1 ? s4.y : u == 2 ? s4.z : s4.w;
+          // Explicit fused forms: every instantiation (full / edge tile)
+          // rounds a row identically, whatever the compiler would contract.
+          const float y1 = __builtin_fmaf(x1, c, -(x2 * sn));
+          const float y2 = __builtin_fmaf(x2, c, x1 * sn);
+          x1 = y1;
+          x2 = y2;
+        }
+        // Offsets from the tile origin: unsigned 32-bit, so the store adds a
+        // lane offset to a uniform base.
+        const uint32_t dr = static_cast<uint32_t>(i * 32 + q * 8 + u);
+        const uint32_t off = lane_c + dr * ldc;
+        if constexpr (EPI == kEpiQkvRopeF32) {
+          float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+          *at(base, off) = x1;
+          *at(base, off + 32) = x2;
+        } else if constexpr (EPI == kEpiQkvSplit) {
+          if constexpr (WHICH == 0) {
+            x1 *= p.q_prescale;
+            x2 *= p.q_prescale;
+          }
+          uint32_t* base = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc + n0;
+          __builtin_nontemporal_store(split_f16_word(x1), at(base, off));
+          __builtin_nontemporal_store(split_f16_word(x2), at(base, off + 32));
+        } else {
+          // [M, d_model] outputs; column of the head inside its Q / K / V part.
+          const uint32_t o = lane_d + dr * dm;
+          if constexpr (WHICH == 2) {
+            uint16_t* vb = p.v_out + static_cast<size_t>(m0) * dm;
+            *at(vb, o) = f32_to_f16_bits(x1);
+            *at(vb, o + 32) = f32_to_f16_bits(x2);
+          } else {
+            uint16_t* dst = (WHICH == 0 ? p.q_out : p.k_out) + static_cast<size_t>(m0) * dm;
+            *at(dst, o) = p.qk_fp16 ? f32_to_f16_bits(x1) : f32_to_bf16_bits(x1);
+            *at(dst, o + 32) = p.qk_fp16 ? f32_to_f16_bits(x2) : f32_to_bf16_bits(x2);
+          }
+        }
+      }
+    }
+}
+
+// MAX: also reduce |out| into p.row_absmax / p.tensor_absmax (whichever is set).
+template <int EPI, bool FULL, bool MAX>
+__device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
-                                           const float* s_bs, const int* s_pos, int m0, int n0) {
+                                           const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
+                                           int n0) {
+  const int lr0 = wm * BLK_M * 32 + hi * 4;
+  const int lc0 = wn * BLK_N * 32 + l32;
+  const uint32_t ldc = p.ldc;
+  auto col_ok = [&](int lc) { return FULL || n0 + lc < p.N; };
   if constexpr (EPI == kEpiI32) {
+    int32_t* base = p.C_i32 + static_cast<size_t>(m0) * ldc + n0;
+    const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(lc0);
 #pragma unroll
     for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-      for (int j = 0; j < BLK_N; ++j) {
-        const int col = cb + j * 32 + l32;
-        if (col >= p.N) continue;
+      for (int r = 0; r < 16; ++r) {
+        const int dr = i * 32 + (r >> 2) * 8 + (r & 3);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          if (row < p.M) __builtin_nontemporal_store(acc[i][j][r], p.C_i32 + static_cast<size_t>(row) * p.ldc + col);
-        }
+        for (int j = 0; j < BLK_N; ++j)
+          if ((FULL || m0 + lr0 + dr < p.M) && col_ok(lc0 + j * 32))
+            __builtin_nontemporal_store(acc[i][j][r], at(base, lane_c + static_cast<uint32_t>(dr) * ldc + j * 32));
       }
     return;
   } else {
     float ws[BLK_N], bs[BLK_N];
 #pragma unroll
     for (int j = 0; j < BLK_N; ++j) {
-      const int c = cb + j * 32 + l32 - n0;
-      ws[j] = s_ws[c];
-      bs[j] = s_bs[c];
+      ws[j] = s_ws[lc0 + j * 32];
+      bs[j] = s_bs[lc0 + j * 32];
     }
     if constexpr (EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit) {
       static_assert(BLK_N % 2 == 0, "QKV epilogue needs whole 64-column heads per wave");
-      // Blocks (2g, 2g+1) are one head of Q, K or V: lane column l32 holds
-      // head dims l32 and 32 + l32 -- exactly a rotary pair.
 #pragma unroll
       for (int g = 0; g < BLK_N / 2; ++g) {
-        const int hc = cb + g * 64;
-        if (hc >= p.N) break;
-        const int which = hc / p.d_model;
-#pragma unroll
-        for (int i = 0; i < BLK_M; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-            if (row >= p.M) continue;
-            const float as = s_as[row - m0];
-            float x1 = __builtin_fmaf(static_cast<float>(acc[i][2 * g][r]), as * ws[2 * g], bs[2 * g]);
-            float x2 = __builtin_fmaf(static_cast<float>(acc[i][2 * g + 1][r]), as * ws[2 * g + 1], bs[2 * g + 1]);
-            if (which < 2) {
-              if (which == 0) {
-                x1 *= p.q_scale;
-                x2 *= p.q_scale;
-              }
-              const int ps = s_pos[row - m0];
-              const float* ct = p.rope_cos + static_cast<size_t>(ps) * 64;
-              const float* st = p.rope_sin + static_cast<size_t>(ps) * 64;
-              const float y1 = x1 * ct[l32] - x2 * st[l32];
-              const float y2 = x2 * ct[l32 + 32] + x1 * st[l32 + 32];
-              x1 = y1;
-              x2 = y2;
-            }
-            if constexpr (EPI == kEpiQkvRopeF32) {
-              float* dst = p.C_f32 + static_cast<size_t>(row) * p.ldc + hc + l32;
-              dst[0] = x1;
-              dst[32] = x2;
-            } else if constexpr (EPI == kEpiQkvSplit) {
-              if (which == 0) {
-                x1 *= p.q_prescale;
-                x2 *= p.q_prescale;
-              }
-              uint32_t* dst = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(row) * p.ldc + hc + l32;
-              __builtin_nontemporal_store(split_f16_word(x1), dst);
-              __builtin_nontemporal_store(split_f16_word(x2), dst + 32);
-            } else {
-              const size_t o = static_cast<size_t>(row) * p.d_model + (hc - which * p.d_model) + l32;
-              if (which == 2) {
-                p.v_out[o] = f32_to_f16_bits(x1);
-                p.v_out[o + 32] = f32_to_f16_bits(x2);
-              } else {
-                uint16_t* dst = which == 0 ? p.q_out : p.k_out;
-                dst[o] = p.qk_fp16 ? f32_to_f16_bits(x1) : f32_to_bf16_bits(x1);
-                dst[o + 32] = p.qk_fp16 ? f32_to_f16_bits(x2) : f32_to_bf16_bits(x2);
-              }
-            }
-          }
+        const int hc = wn * BLK_N * 32 + g * 64;  // uniform: the wave index is
+        if (!FULL && n0 + hc >= p.N) break;
+        const int which = (n0 + hc) / p.d_model;
+        if (which == 0)
+          qkv_head<EPI, FULL, 0>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+        else if (which == 1)
+          qkv_head<EPI, FULL, 1>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+        else
+          qkv_head<EPI, FULL, 2>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
     } else {
-      constexpr bool kMax = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
       float tmax = 0.0f;
+      const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(lc0);
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = rb + i * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          const bool rok = row < p.M;
-          const float as = s_as[row - m0];
-          float rmax = 0.0f;
+        for (int q = 0; q < 4; ++q) {
+          const int lr = lr0 + i * 32 + q * 8;
+          const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
+          const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-          for (int j = 0; j < BLK_N; ++j) {
-            const int col = cb + j * 32 + l32;
-            float v = __builtin_fmaf(static_cast<float>(acc[i][j][r]), as * ws[j], bs[j]);
-            if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
-            if (rok && col < p.N) {
-              const size_t o = static_cast<size_t>(row) * p.ldc + col;
-              if constexpr (EPI == kEpiF32Resid) {
-                p.C_f32[o] += v;
-              } else if constexpr (EPI == kEpiF32GeluQ) {
-                p.C_f16[o] = f32_to_f16_bits(v);
-                rmax = fmaxf(rmax, fabsf(v));
-              } else {
-                __builtin_nontemporal_store(v, p.C_f32 + o);
-                rmax = fmaxf(rmax, fabsf(v));
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * q + u;
+            const bool rok = FULL || m0 + lr + u < p.M;
+            float rmax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < BLK_N; ++j) {
+              float v = __builtin_fmaf(static_cast<float>(acc[i][j][r]), asv[u] * ws[j], bs[j]);
+              if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
+              if (rok && col_ok(lc0 + j * 32)) {
+                const uint32_t off = lane_c + static_cast<uint32_t>(i * 32 + q * 8 + u) * ldc + j * 32;
+                if constexpr (EPI == kEpiF32Resid) {
+                  float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+                  *at(base, off) += v;
+                } else if constexpr (EPI == kEpiF32GeluQ) {
+                  uint16_t* base = p.C_f16 + static_cast<size_t>(m0) * ldc + n0;
+                  *at(base, off) = f32_to_f16_bits(v);
+                } else {
+                  float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+                  __builtin_nontemporal_store(v, at(base, off));
+                }
+                if constexpr (MAX) rmax = fmaxf(rmax, fabsf(v));
               }
             }
-          }
-          if constexpr (kMax) {
-            if (p.row_absmax) {
-              // The 32 lanes of a half-wave hold the same row.
+            if constexpr (MAX) {
+              if (p.row_absmax) {
+                // The 32 lanes of a half-wave hold the same row.
 #pragma unroll
-              for (int off = 16; off >= 1; off >>= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, off, kWave));
-              if (l32 == 0 && rok) atomic_max_nonneg(p.row_absmax + row, rmax);
+                for (int o = 16; o >= 1; o >>= 1) rmax = fmaxf(rmax, __shfl_xor(rmax, o, kWave));
+                if (l32 == 0 && rok) atomic_max_nonneg(p.row_absmax + m0 + lr + u, rmax);
+              }
+              tmax = fmaxf(tmax, rmax);
             }
-            tmax = fmaxf(tmax, rmax);
           }
         }
-      if constexpr (kMax) {
+      if constexpr (MAX) {
         if (p.tensor_absmax) {
           tmax = wave_max(tmax);
           if ((threadIdx.x & 63) == 0) atomic_max_nonneg(p.tensor_absmax, tmax);
@@ -551,7 +615,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     }
     __syncthreads();
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform across the wave; readfirstlane tells the
+  // compiler so, keeping per-wave decisions (Q/K/V head, RoPE) scalar.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int l32 = lane & 31, hi = lane >> 5;
 
@@ -607,7 +673,49 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     }
   }
 
-  epilogue32<EPI>(p, acc, m0 + wm * BLK_M * 32, n0 + wn * BLK_N * 32, l32, hi, s_as, s_ws, s_bs, s_pos, m0, n0);
+  const float* s_cosT = nullptr;
+  const float* s_sinT = nullptr;
+  if constexpr (kRope) {
+    if (n0 < 2 * p.d_model) {
+      // The tile holds Q or K columns: stage its rows' RoPE cos / sin,
+      // transposed, in the now idle operand buffers. Thread t copies half a
+      // table row (cos for even t, sin for odd t) of tile row t / 2.
+      static_assert(kThreads == 2 * BM, "two threads per staged RoPE row");
+      static_assert(2 * 32 * kRopeTPitch * 4 <= 2 * kStage, "RoPE staging fits in the operand buffers");
+      float* cosT = reinterpret_cast<float*>(smem);
+      float* sinT = cosT + 32 * kRopeTPitch;
+      __syncthreads();
+      const int t = threadIdx.x >> 1;
+      const bool odd = threadIdx.x & 1;
+      const float4* src =
+          reinterpret_cast<const float4*>((odd ? p.rope_sin : p.rope_cos) + static_cast<size_t>(s_pos[t]) * 64);
+      float* dst = (odd ? sinT : cosT) + t;
+#pragma unroll
+      for (int c4 = 0; c4 < 8; ++c4) {
+        const float4 v = src[c4];
+        dst[(4 * c4 + 0) * kRopeTPitch] = v.x;
+        dst[(4 * c4 + 1) * kRopeTPitch] = v.y;
+        dst[(4 * c4 + 2) * kRopeTPitch] = v.z;
+        dst[(4 * c4 + 3) * kRopeTPitch] = v.w;
+      }
+      __syncthreads();
+      s_cosT = cosT;
+      s_sinT = sinT;
+    }
+  }
+  constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+  if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
+    if (full)
+      epilogue32<EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+    else
+      epilogue32<EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+  } else {
+    if (full)
+      epilogue32<EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+    else
+      epilogue32<EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+  }
 }
 
 }  // namespace v3
