@@ -302,20 +302,51 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   const int qbase = w.q0 + wave * 32;
   const bool active = qbase < L;  // wave-uniform
 
+  // K / V chunk loads into registers (K: KCX keys x 16 uint4; V: KCX/2 key
+  // pairs x 16 dim quads), clamped to the sequence's last key; the chunk
+  // after the current one is loaded while the current one is computed.
+  constexpr int kKLoads = KCX * 16 / 256, kVLoads = KCX / 2 * 16 / 256;
+  uint4 kr[kKLoads], va[kVLoads], vb[kVLoads];
+  auto load_chunk = [&](int kc) {
+    const int nk = min(KCX, L - kc);
+    const uint32_t* kbase = k + static_cast<size_t>(start + kc) * ld + hoff;
+    const uint32_t* vbase = v + static_cast<size_t>(start + kc) * ld + hoff;
+#pragma unroll
+    for (int i = 0; i < kKLoads; ++i) {
+      const int idx = tid + 256 * i;
+      const int key = idx >> 4, c4 = idx & 15;
+      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(min(key, nk - 1)) * ld + c4 * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < kVLoads; ++i) {
+      const int idx = tid + 256 * i;
+      const int dq = idx & 15, key0 = 2 * (idx >> 4);
+      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0, nk - 1)) * ld + dq * 4);
+      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0 + 1, nk - 1)) * ld + dq * 4);
+    }
+  };
+
   // Q fragments (B operand of S^T = K Q^T): lane (lr, lg) holds query lr of
-  // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8).
-  f16x8 qh[2][2], ql[2][2];
+  // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8). The Q words are
+  // loaded first and chunk 0's K / V right behind them, so both round trips
+  // overlap.
+  uint4 qw[2][2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qi = min(qbase + qb * 16 + lr, L - 1);
     const uint32_t* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-      const uint4 a = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8);
-      const uint4 b = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8 + 4);
-      unpack8(a, b, &qh[qb][half], &ql[qb][half]);
+      qw[qb][half][0] = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8);
+      qw[qb][half][1] = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8 + 4);
     }
   }
+  load_chunk(0);
+  f16x8 qh[2][2], ql[2][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) unpack8(qw[qb][half][0], qw[qb][half][1], &qh[qb][half], &ql[qb][half]);
 
   f32x4 o[2][4];
 #pragma unroll
@@ -327,27 +358,9 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 
   for (int kc0 = 0; kc0 < L; kc0 += KCX) {
     const int nkeys = min(KCX, L - kc0);
-    const uint32_t* kbase = k + static_cast<size_t>(start + kc0) * ld + hoff;
-    const uint32_t* vbase = v + static_cast<size_t>(start + kc0) * ld + hoff;
-    // Global loads for the whole chunk first (K: KCX keys x 16 uint4; V: KCX/2
-    // key pairs x 16 dim quads), clamped to the last key and zeroed past it.
-    uint4 kr[KCX * 16 / 256], va[KCX / 2 * 16 / 256], vb[KCX / 2 * 16 / 256];
-#pragma unroll
-    for (int i = 0; i < KCX * 16 / 256; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c4 = idx & 15;
-      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(min(key, nkeys - 1)) * ld + c4 * 4);
-    }
-#pragma unroll
-    for (int i = 0; i < KCX / 2 * 16 / 256; ++i) {
-      const int idx = tid + 256 * i;
-      const int dq = idx & 15, key0 = 2 * (idx >> 4);
-      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0, nkeys - 1)) * ld + dq * 4);
-      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0 + 1, nkeys - 1)) * ld + dq * 4);
-    }
     __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
-    for (int i = 0; i < KCX * 16 / 256; ++i) {
+    for (int i = 0; i < kKLoads; ++i) {
       const int idx = tid + 256 * i;
       const int key = idx >> 4, c4 = idx & 15;
       const uint4 x = key < nkeys ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
@@ -358,7 +371,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     }
     // V^T[dim][key]: each item is a key pair x 4 dims.
 #pragma unroll
-    for (int i = 0; i < KCX / 2 * 16 / 256; ++i) {
+    for (int i = 0; i < kVLoads; ++i) {
       const int idx = tid + 256 * i;
       const int dq = idx & 15, key0 = 2 * (idx >> 4);
       const uint4 a = key0 < nkeys ? va[i] : make_uint4(0u, 0u, 0u, 0u);
@@ -371,6 +384,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         *reinterpret_cast<uint32_t*>(sVl + off) = halves(xa[j], xb[j], kSelHi);
       }
     }
+    if (kc0 + KCX < L) load_chunk(kc0 + KCX);  // in flight during this chunk's compute
     __syncthreads();
     if (!active) continue;
 
