@@ -679,6 +679,12 @@ struct esm_gfx950_model {
   };
   std::vector<Part> parts = std::vector<Part>(1);
   int staged_T = 0;  // tokens of the staged batch (all parts)
+  // esm_gfx950_forward_scheduled: device and pinned host logits, two of each
+  // so one group's copy-out overlaps the next group's forward.
+  float* sched_dev[2] = {nullptr, nullptr};
+  float* sched_host[2] = {nullptr, nullptr};
+  hipEvent_t sched_copied[2] = {nullptr, nullptr};
+  size_t sched_cap = 0;  // floats per buffer
 };
 
 namespace {
@@ -757,6 +763,11 @@ void free_part(esm_gfx950_model::Part& p) {
 void free_model(esm_gfx950_model* m) {
   for (void* p : m->allocations) hipFree(p);
   for (auto& p : m->parts) free_part(p);
+  for (int i = 0; i < 2; ++i) {
+    if (m->sched_dev[i]) hipFree(m->sched_dev[i]);
+    if (m->sched_host[i]) hipHostFree(m->sched_host[i]);
+    if (m->sched_copied[i]) hipEventDestroy(m->sched_copied[i]);
+  }
   delete m;
 }
 
@@ -1409,5 +1420,138 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
       if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
   }
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+// ---------------------------------------------------------------- scheduler
+namespace {
+
+// PlanChunk (reference src/sched/scheduler.cpp:13-50): a group whose longest
+// sequence exceeds `threshold` times its mean length is sorted by length
+// (std::sort, ascending) and split at size/2, and both halves are planned
+// again; otherwise it is emitted as one group. Groups of one are emitted.
+void plan_group(std::vector<int>& idx, const int32_t* lengths, float threshold, std::vector<std::vector<int>>* out) {
+  if (idx.empty()) return;
+  if (idx.size() > 1) {
+    int longest = 0;
+    long sum = 0;
+    for (int i : idx) {
+      longest = std::max(longest, static_cast<int>(lengths[i]));
+      sum += lengths[i];
+    }
+    const float mean = static_cast<float>(sum) / static_cast<float>(idx.size());
+    if (mean > 0.0f && static_cast<float>(longest) / mean > threshold) {
+      std::sort(idx.begin(), idx.end(), [&](int a, int b) { return lengths[a] < lengths[b]; });
+      const size_t half = idx.size() / 2;
+      std::vector<int> shorter(idx.begin(), idx.begin() + static_cast<long>(half));
+      std::vector<int> longer(idx.begin() + static_cast<long>(half), idx.end());
+      plan_group(shorter, lengths, threshold, out);
+      plan_group(longer, lengths, threshold, out);
+      return;
+    }
+  }
+  out->push_back(std::move(idx));
+}
+
+// PlanBatches (reference src/sched/scheduler.cpp:54-75): caller-order chunks
+// of at most max_batch_size (all, when <= 0), each planned by plan_group.
+std::vector<std::vector<int>> plan_batches(const int32_t* lengths, int n, float threshold, int max_batch_size) {
+  std::vector<std::vector<int>> out;
+  const int chunk = max_batch_size > 0 ? max_batch_size : n;
+  for (int s = 0; s < n; s += chunk) {
+    std::vector<int> idx;
+    for (int i = s; i < std::min(n, s + chunk); ++i) idx.push_back(i);
+    plan_group(idx, lengths, threshold, &out);
+  }
+  return out;
+}
+
+}  // namespace
+
+extern "C" int esm_gfx950_plan_batches(const int32_t* lengths, int n, float imbalance_threshold,
+                                       int max_batch_size, int32_t* order, int32_t* group_sizes,
+                                       int* num_groups) {
+  if (n < 0 || !num_groups || (n > 0 && (!lengths || !order || !group_sizes))) return ESM_GFX950_INVALID_ARGUMENT;
+  for (int i = 0; i < n; ++i)
+    if (lengths[i] < 0) return ESM_GFX950_INVALID_ARGUMENT;
+  const auto plan = plan_batches(lengths, n, imbalance_threshold, max_batch_size);
+  int k = 0, g = 0;
+  for (const auto& group : plan) {
+    group_sizes[g++] = static_cast<int32_t>(group.size());
+    for (int i : group) order[k++] = i;
+  }
+  *num_groups = g;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_scheduled(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* const* ids,
+                                            const int32_t* lengths, int n, float imbalance_threshold,
+                                            int max_batch_size, float* const* logits) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, n >= 0, "forward_scheduled: negative sequence count");
+  if (n == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, lengths && ids && logits, "forward_scheduled: null argument");
+  for (int i = 0; i < n; ++i) {
+    ESM_REQUIRE(ctx, lengths[i] >= 0, "forward_scheduled: negative length at " + std::to_string(i));
+    ESM_REQUIRE(ctx, lengths[i] == 0 || (ids[i] && logits[i]),
+                "forward_scheduled: null ids or logits at " + std::to_string(i));
+  }
+  const int V = m->cfg.vocab_size;
+  const auto plan = plan_batches(lengths, n, imbalance_threshold, max_batch_size);
+  size_t need = 0;
+  for (const auto& group : plan) {
+    size_t t = 0;
+    for (int i : group) t += static_cast<size_t>(lengths[i]);
+    need = std::max(need, t * V);
+  }
+  if (need == 0) return ESM_GFX950_OK;  // every sequence is empty
+  if (need > m->sched_cap) {
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int b = 0; b < 2; ++b) {
+      if (m->sched_dev[b]) hipFree(m->sched_dev[b]);
+      if (m->sched_host[b]) hipHostFree(m->sched_host[b]);
+      m->sched_dev[b] = m->sched_host[b] = nullptr;
+    }
+    m->sched_cap = 0;
+    for (int b = 0; b < 2; ++b) {
+      ESM_HIP(ctx, hipMalloc(&m->sched_dev[b], need * 4));
+      ESM_HIP(ctx, hipHostMalloc(&m->sched_host[b], need * 4, hipHostMallocDefault));
+      if (!m->sched_copied[b]) ESM_HIP(ctx, hipEventCreateWithFlags(&m->sched_copied[b], hipEventDisableTiming));
+    }
+    m->sched_cap = need;
+  }
+  // Group g is packed, staged and launched while group g-1 still runs; its
+  // logits are then copied to pinned memory, and group g-1's are scattered to
+  // the callers' buffers once their copy has landed.
+  auto scatter = [&](int g) -> int {
+    ESM_HIP(ctx, hipEventSynchronize(m->sched_copied[g & 1]));
+    const float* src = m->sched_host[g & 1];
+    for (int i : plan[g]) {
+      const size_t rows = static_cast<size_t>(lengths[i]) * V;
+      std::memcpy(logits[i], src, rows * 4);
+      src += rows;
+    }
+    return ESM_GFX950_OK;
+  };
+  std::vector<int32_t> packed, cu;
+  for (size_t g = 0; g < plan.size(); ++g) {
+    const auto& group = plan[g];
+    packed.clear();
+    cu.assign(1, 0);
+    for (int i : group) {
+      packed.insert(packed.end(), ids[i], ids[i] + lengths[i]);
+      cu.push_back(cu.back() + lengths[i]);
+    }
+    const int B = static_cast<int>(group.size()), T = cu.back();
+    ESM_TRY(esm_gfx950_batch_upload(ctx, m, packed.data(), cu.data(), B, T));
+    if (T > 0) {
+      ESM_TRY(esm_gfx950_forward_device(ctx, m, m->sched_dev[g & 1]));
+      ESM_HIP(ctx, hipMemcpyAsync(m->sched_host[g & 1], m->sched_dev[g & 1], static_cast<size_t>(T) * V * 4,
+                                  hipMemcpyDeviceToHost, ctx->stream));
+    }
+    ESM_HIP(ctx, hipEventRecord(m->sched_copied[g & 1], ctx->stream));
+    if (g > 0) ESM_TRY(scatter(static_cast<int>(g) - 1));
+  }
+  ESM_TRY(scatter(static_cast<int>(plan.size()) - 1));
   return ESM_GFX950_OK;
 }

@@ -40,7 +40,8 @@ EXPORTED = [
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
     "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
-    "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts",
+    "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_plan_batches",
+    "esm_gfx950_forward_scheduled",
 ]
 
 
@@ -100,6 +101,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_forward_device": (i32, [vp, vp, vp]),
         "esm_gfx950_model_arena_bytes": (i32, [vp, C.POINTER(sz)]),
         "esm_gfx950_model_set_parts": (i32, [vp, vp, i32]),
+        "esm_gfx950_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
+        "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -122,6 +125,26 @@ def rope_build_tables(seq_len: int, head_dim: int):
     if rc != OK:
         raise Gfx950Error(rc, "rope_build_tables")
     return cos[:seq_len], sin[:seq_len]
+
+
+def plan_batches(lengths, max_batch_size: int = 256, imbalance_threshold: float = 1.2):
+    """PlanBatches on the host: list of groups of caller indices
+    (reference src/sched/scheduler.cpp:54-75, defaults of scheduler.h:8-21)."""
+    lib = load_library()
+    lens = np.ascontiguousarray(lengths, np.int32)
+    n = int(lens.shape[0])
+    order = np.zeros(max(n, 1), np.int32)
+    sizes = np.zeros(max(n, 1), np.int32)
+    ng = C.c_int(0)
+    rc = lib.esm_gfx950_plan_batches(_ptr(lens), n, float(imbalance_threshold), int(max_batch_size), _ptr(order),
+                                     _ptr(sizes), C.byref(ng))
+    if rc != OK:
+        raise Gfx950Error(rc, "plan_batches")
+    out, k = [], 0
+    for g in range(ng.value):
+        out.append([int(i) for i in order[k:k + sizes[g]]])
+        k += int(sizes[g])
+    return out
 
 
 class DeviceArray:
@@ -375,6 +398,22 @@ class Model:
         self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
                                                                len(cu) - 1, T, out.ptr, 1))
         return out
+
+    def forward_scheduled(self, ids_list, max_batch_size: int = 256, imbalance_threshold: float = 1.2):
+        """Scheduled forward over a list of id arrays (esm_gfx950_forward_scheduled);
+        returns one host logits array [L_i, vocab] per input, in input order."""
+        n = len(ids_list)
+        if n == 0:
+            return []
+        ids = [np.ascontiguousarray(x, np.int32) for x in ids_list]
+        lens = np.array([x.shape[0] for x in ids], np.int32)
+        outs = [np.empty((int(L), self.cfg.vocab_size), np.float32) for L in lens]
+        id_ptrs = (C.c_void_p * n)(*[x.ctypes.data for x in ids])
+        out_ptrs = (C.c_void_p * n)(*[o.ctypes.data for o in outs])
+        self.dev._check(self.dev.lib.esm_gfx950_forward_scheduled(
+            self.dev.ctx, self.handle, C.cast(id_ptrs, C.c_void_p), _ptr(lens), n, float(imbalance_threshold),
+            int(max_batch_size), C.cast(out_ptrs, C.c_void_p)))
+        return outs
 
     def upload_batch(self, ids: np.ndarray, cu: np.ndarray):
         """Stages a packed batch in device memory (esm_gfx950_batch_upload)."""

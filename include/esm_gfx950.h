@@ -272,6 +272,25 @@ int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, floa
  * row depends only on its own sequence). No reference counterpart: the
  * reference's ForwardPacked (model.cpp:1093-1255) runs one thread pool. */
 int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int parts);
+/* PlanBatches (reference src/sched/scheduler.cpp:54-75, SchedulerConfig in
+ * include/esm_cpp/scheduler.h:8-21), host only: splits n sequences of the
+ * given lengths into caller-order chunks of at most max_batch_size (all when
+ * <= 0); a chunk whose max/mean length exceeds imbalance_threshold is sorted
+ * by length and halved recursively. Writes the caller indices of every group
+ * back to back into order[n], the group sizes into group_sizes[n], and the
+ * group count into *num_groups. */
+int esm_gfx950_plan_batches(const int32_t* lengths, int n, float imbalance_threshold, int max_batch_size,
+                            int32_t* order, int32_t* group_sizes, int* num_groups);
+/* Model::ForwardScheduled (reference src/model.cpp:1298-1421) without masks:
+ * plans the n sequences (ids[i], lengths[i]; HOST arrays) with
+ * esm_gfx950_plan_batches, runs each group as one packed forward and writes
+ * sequence i's logits fp32 [lengths[i], vocab] to the HOST buffer logits[i].
+ * Group g+1 is packed and staged while group g runs, and group g's logits are
+ * copied out through pinned memory while group g+1 runs. Returns after the
+ * last group's logits are written. */
+int esm_gfx950_forward_scheduled(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* const* ids,
+                                 const int32_t* lengths, int n, float imbalance_threshold, int max_batch_size,
+                                 float* const* logits);
 /* Bytes currently held by the model's device arena (for zero-growth checks). */
 int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
 

@@ -242,6 +242,7 @@ class RefLib:
             "esmref_model_create": (vp, [C.POINTER(_OrModel)]),
             "esmref_model_free": (None, [vp]),
             "esmref_forward_packed": (i32, [vp, vp, vp, i32, i32, vp]),
+            "esmref_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -251,6 +252,21 @@ class RefLib:
 
     def isa(self) -> str:
         return self.lib.esmref_isa().decode()
+
+    def plan_batches(self, lengths, max_batch_size: int = 256, imbalance_threshold: float = 1.2):
+        """The reference's PlanBatches (src/sched/scheduler.cpp:54-75) as a list of groups."""
+        lens = _c(lengths, np.int32)
+        n = int(lens.shape[0])
+        order = np.zeros(max(n, 1), np.int32)
+        sizes = np.zeros(max(n, 1), np.int32)
+        ng = C.c_int(0)
+        self.lib.esmref_plan_batches(_p(lens), n, float(imbalance_threshold), int(max_batch_size), _p(order),
+                                     _p(sizes), C.byref(ng))
+        out, k = [], 0
+        for g in range(ng.value):
+            out.append([int(i) for i in order[k:k + sizes[g]]])
+            k += int(sizes[g])
+        return out
 
     def host_isa(self) -> str:
         return self.lib.esmref_host_isa().decode()

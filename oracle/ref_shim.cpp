@@ -24,6 +24,7 @@
 #include "esm_cpp/cpu_features.h"
 #include "esm_cpp/kernels.h"
 #include "esm_cpp/quant.h"
+#include "esm_cpp/scheduler.h"
 #include "oracle.h"
 
 namespace esm::kernels {
@@ -243,6 +244,24 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
   esm::kernels::Gelu(proj.data(), attn.data(), Td);
   esm::kernels::LayerNorm(attn.data(), r->lm_ln_w.data(), r->lm_ln_b.data(), c.eps, ln.data(), T, d);
   esm::kernels::Linear(ln.data(), r->embed.data(), r->dec_b.data(), logits, T, V, d);
+  return 0;
+}
+
+// PlanBatches (src/sched/scheduler.cpp:54-75) flattened: the caller-index
+// order of every group back to back in `order`, group sizes in `sizes`.
+int esmref_plan_batches(const int32_t* lengths, int n, float imbalance_threshold, int max_batch_size,
+                        int32_t* order, int32_t* sizes, int* num_groups) {
+  std::vector<int> len(lengths, lengths + n);
+  esm::SchedulerConfig cfg;
+  cfg.imbalance_threshold = imbalance_threshold;
+  cfg.max_batch_size = max_batch_size;
+  const auto plan = esm::PlanBatches(len, cfg);
+  int k = 0, g = 0;
+  for (const auto& group : plan) {
+    sizes[g++] = static_cast<int32_t>(group.size());
+    for (int i : group) order[k++] = i;
+  }
+  *num_groups = g;
   return 0;
 }
 
