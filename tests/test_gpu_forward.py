@@ -188,3 +188,24 @@ def test_parts_per_tensor_stays_whole(dev, w650_small, small_batch):
     dev.sync()
     np.testing.assert_array_equal(out.numpy(), want)
     m.free()
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+def test_config5_3b_shapes_vs_oracle(dev, oracle, per_token):
+    """Configuration 5's shapes (ESM-2 3B: d=2560, 40 heads, ffn 10240, K=10240
+    GEMMs, a 520-token sequence beside a short one), one layer, against the
+    oracle's same-mode forward at the W8A8 bar (corr >= 0.9999)."""
+    cfg = syn.ESM2_3B.with_layers(1)
+    w = syn.make_weights(cfg, seed=20261201 + 5, int8=True, keep_f32_linears=False)
+    batch = syn.batch_from_lengths([520, 90], seed=11)
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w, int8=True, act_mode=mode)
+    got = m.forward_packed(batch.ids, batch.cu)
+    m.free()
+    want = oracle.forward_packed(w, batch, int8=True, per_token=per_token)
+    assert np.all(np.isfinite(got))
+    c = corr(got, want)
+    agree = float(np.mean(np.argmax(got, 1) == np.argmax(want, 1)))
+    print(f"3B shapes per_token={per_token}: corr={c:.6f} argmax_agree={agree:.4f}")
+    assert c >= 0.9999, c
+    assert agree >= 0.98, agree
