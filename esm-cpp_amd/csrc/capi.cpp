@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "esm_gfx950.h"
+#include "gguf.hpp"
 #include "kernels.hpp"
 
 using namespace esm_gfx950;
@@ -1554,4 +1555,120 @@ extern "C" int esm_gfx950_forward_scheduled(esm_gfx950_ctx* ctx, esm_gfx950_mode
   }
   ESM_TRY(scatter(static_cast<int>(plan.size()) - 1));
   return ESM_GFX950_OK;
+}
+
+// ---------------------------------------------------------------- GGUF load
+// Model::LoadFromGguf (reference src/model.cpp:229-298; tensor names and
+// shapes as Model::SaveToGguf writes them, :562-700): metadata esm.* gives
+// the shape, esm.weights_quantized selects Q8_ESM ([N, K] int8 + [N] scales,
+// wire shape [K, N]) or F32 layer linears; embeddings, LayerNorms, biases and
+// the lm head are F32. Vocabulary 33 and mask id 32 are the tokenizer's
+// (include/esm_cpp/tokenizer.h:30-31).
+extern "C" int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char* path, int act_quant_mode,
+                                                 int attention_mode, esm_gfx950_model** out) {
+  if (!ctx || !out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = nullptr;
+  ESM_REQUIRE(ctx, path, "model_create_from_gguf: null path");
+  gguf::File f;
+  std::string err;
+  if (!f.open(path, &err)) return ctx->fail(ESM_GFX950_IO_ERROR, err);
+  const gguf::Value* arch = f.meta("general.architecture");
+  if (!arch || arch->kind != gguf::Value::kString || arch->s != "esm")
+    return ctx->fail(ESM_GFX950_INVALID_ARGUMENT,
+                     "gguf: not an esm-arch file (general.architecture must be 'esm')");
+  auto meta_int = [&](const char* key, int* v) -> int {
+    const gguf::Value* x = f.meta(key);
+    if (!x) return ctx->fail(ESM_GFX950_NOT_FOUND, std::string("gguf: missing metadata ") + key);
+    if (x->kind != gguf::Value::kInt) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, std::string("gguf: metadata ") + key + " is not int");
+    if (x->i <= 0 || x->i > (1 << 20)) return ctx->fail(ESM_GFX950_OUT_OF_RANGE, std::string("gguf: metadata ") + key + " out of range");
+    *v = static_cast<int>(x->i);
+    return ESM_GFX950_OK;
+  };
+  auto meta_bool = [&](const char* key) {
+    const gguf::Value* x = f.meta(key);
+    return x && x->kind == gguf::Value::kBool && x->b;
+  };
+  esm_gfx950_model_desc desc{};
+  esm_gfx950_model_config& c = desc.cfg;
+  ESM_TRY(meta_int("esm.block_count", &c.num_layers));
+  ESM_TRY(meta_int("esm.embedding_length", &c.hidden_size));
+  ESM_TRY(meta_int("esm.feed_forward_length", &c.intermediate_size));
+  ESM_TRY(meta_int("esm.attention.head_count", &c.num_heads));
+  ESM_TRY(meta_int("esm.rope.dimension_count", &c.head_dim));
+  c.layer_norm_eps = 1e-5f;
+  if (const gguf::Value* eps = f.meta("esm.attention.layer_norm_epsilon"); eps && eps->kind == gguf::Value::kFloat)
+    c.layer_norm_eps = static_cast<float>(eps->f);
+  c.vocab_size = 33;
+  c.mask_token_id = 32;
+  c.weights_int8 = meta_bool("esm.weights_quantized") ? 1 : 0;
+  c.act_quant_mode = act_quant_mode;
+  c.attention_mode = attention_mode;
+  ESM_REQUIRE(ctx, !meta_bool("esm.first_block_fc1_fp16"),
+              "gguf: esm.first_block_fc1_fp16 (layer-0 fp16 rounding of the fc1 input) is not supported");
+  const size_t d = c.hidden_size, ffn = c.intermediate_size, V = c.vocab_size;
+
+  auto f32 = [&](const std::string& name, size_t count, const float** dst) -> int {
+    const gguf::Tensor* t = f.tensor(name);
+    if (!t) return ctx->fail(ESM_GFX950_NOT_FOUND, "gguf: missing tensor " + name);
+    if (t->type != gguf::kF32) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "gguf: expected F32 for " + name);
+    if (t->bytes != count * 4)
+      return ctx->fail(ESM_GFX950_SHAPE_MISMATCH, "gguf: " + name + " holds " + std::to_string(t->bytes / 4) +
+                                                      " floats, expected " + std::to_string(count));
+    if (reinterpret_cast<uintptr_t>(t->data) % 4 != 0)
+      return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "gguf: misaligned tensor " + name);
+    *dst = reinterpret_cast<const float*>(t->data);
+    return ESM_GFX950_OK;
+  };
+  std::vector<std::vector<float>> scale_copies;  // Q8 scales realigned to 4 bytes when needed
+  auto linear = [&](const std::string& name, size_t N, size_t K, esm_gfx950_linear_desc* L) -> int {
+    if (!c.weights_int8) return f32(name + ".weight", N * K, &L->w_f32);
+    const gguf::Tensor* t = f.tensor(name + ".weight");
+    if (!t) return ctx->fail(ESM_GFX950_NOT_FOUND, "gguf: missing tensor " + name + ".weight");
+    if (t->type != gguf::kQ8Esm) return ctx->fail(ESM_GFX950_INVALID_ARGUMENT, "gguf: expected Q8_ESM for " + name + ".weight");
+    if (t->shape.size() != 2 || t->shape[0] != K || t->shape[1] != N)
+      return ctx->fail(ESM_GFX950_SHAPE_MISMATCH, "gguf: Q8_ESM " + name + ".weight shape mismatch");
+    L->w_i8 = reinterpret_cast<const int8_t*>(t->data);
+    // The scales follow the N*K int8 bytes, so they are 4-byte aligned only
+    // when N*K is; otherwise they are copied out.
+    const uint8_t* sp = t->data + N * K;
+    if (reinterpret_cast<uintptr_t>(sp) % 4 == 0) {
+      L->w_scale = reinterpret_cast<const float*>(sp);
+    } else {
+      scale_copies.emplace_back(N);
+      std::memcpy(scale_copies.back().data(), sp, N * 4);
+      L->w_scale = scale_copies.back().data();
+    }
+    return ESM_GFX950_OK;
+  };
+  std::vector<esm_gfx950_layer_desc> layers(c.num_layers);
+  ESM_TRY(f32("token_embd.weight", V * d, &desc.embed));
+  for (int i = 0; i < c.num_layers; ++i) {
+    esm_gfx950_layer_desc& L = layers[i];
+    const std::string b = "blk." + std::to_string(i) + ".";
+    ESM_TRY(f32(b + "attn_norm.weight", d, &L.attn_ln_w));
+    ESM_TRY(f32(b + "attn_norm.bias", d, &L.attn_ln_b));
+    ESM_TRY(linear(b + "attn_q", d, d, &L.q));
+    ESM_TRY(linear(b + "attn_k", d, d, &L.k));
+    ESM_TRY(linear(b + "attn_v", d, d, &L.v));
+    ESM_TRY(linear(b + "attn_output", d, d, &L.out));
+    ESM_TRY(f32(b + "attn_q.bias", d, &L.q.bias));
+    ESM_TRY(f32(b + "attn_k.bias", d, &L.k.bias));
+    ESM_TRY(f32(b + "attn_v.bias", d, &L.v.bias));
+    ESM_TRY(f32(b + "attn_output.bias", d, &L.out.bias));
+    ESM_TRY(f32(b + "ffn_norm.weight", d, &L.ffn_ln_w));
+    ESM_TRY(f32(b + "ffn_norm.bias", d, &L.ffn_ln_b));
+    ESM_TRY(linear(b + "ffn_up", ffn, d, &L.fc1));
+    ESM_TRY(linear(b + "ffn_down", d, ffn, &L.fc2));
+    ESM_TRY(f32(b + "ffn_up.bias", ffn, &L.fc1.bias));
+    ESM_TRY(f32(b + "ffn_down.bias", d, &L.fc2.bias));
+  }
+  desc.layers = layers.data();
+  ESM_TRY(f32("enc_norm.weight", d, &desc.final_ln_w));
+  ESM_TRY(f32("enc_norm.bias", d, &desc.final_ln_b));
+  ESM_TRY(f32("lm_head.weight", d * d, &desc.lm_dense_w));
+  ESM_TRY(f32("lm_head.bias", d, &desc.lm_dense_b));
+  ESM_TRY(f32("lm_head_norm.weight", d, &desc.lm_ln_w));
+  ESM_TRY(f32("lm_head_norm.bias", d, &desc.lm_ln_b));
+  ESM_TRY(f32("output.bias", V, &desc.lm_decoder_bias));
+  return esm_gfx950_model_create(ctx, &desc, out);
 }

@@ -41,7 +41,7 @@ EXPORTED = [
     "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
     "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_plan_batches",
-    "esm_gfx950_forward_scheduled",
+    "esm_gfx950_forward_scheduled", "esm_gfx950_model_create_from_gguf",
 ]
 
 
@@ -103,6 +103,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_model_set_parts": (i32, [vp, vp, i32]),
         "esm_gfx950_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
         "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
+        "esm_gfx950_model_create_from_gguf": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -377,6 +378,23 @@ class Model:
         h = C.c_void_p()
         dev._check(dev.lib.esm_gfx950_model_create(dev.ctx, C.byref(desc), C.byref(h)))
         self.dev, self.handle, self.cfg = dev, h, cfg
+
+    @classmethod
+    def from_gguf(cls, dev: Device, path: str, act_mode: int = ACT_PER_TOKEN,
+                  attention_mode: int = ATTN_MODE_F16X3) -> "Model":
+        """A model from an esm.cpp GGUF file (esm_gfx950_model_create_from_gguf)."""
+        from . import gguf
+        from .synthetic import EsmConfig
+        h = C.c_void_p()
+        dev._check(dev.lib.esm_gfx950_model_create_from_gguf(dev.ctx, os.fsencode(path), int(act_mode),
+                                                             int(attention_mode), C.byref(h)))
+        meta = gguf.read_metadata(path)
+        cfg = EsmConfig(str(meta.get("general.name", "gguf")), int(meta["esm.block_count"]),
+                        int(meta["esm.embedding_length"]), int(meta["esm.attention.head_count"]),
+                        int(meta["esm.feed_forward_length"]))
+        m = cls.__new__(cls)
+        m.dev, m.handle, m.cfg = dev, h, cfg
+        return m
 
     def set_act_mode(self, mode: int):
         self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))

@@ -244,6 +244,18 @@ typedef struct {
 int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_model_desc* desc,
                             esm_gfx950_model** out);
 int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model);
+/* Model::LoadFromGguf (reference src/model.cpp:229-298): creates a model
+ * from an esm.cpp GGUF v3 file (src/io/gguf.cpp) -- esm.* metadata for the
+ * shape; Q8_ESM layer linears ([N, K] int8 + [N] fp32 scales) when
+ * esm.weights_quantized is true, else F32; F32 embeddings, LayerNorms,
+ * biases and lm head. act_quant_mode / attention_mode as in
+ * esm_gfx950_model_config. The file is memory-mapped and released before
+ * return. Errors: IO_ERROR (open / malformed file, the reference reader's
+ * messages), NOT_FOUND (missing tensor or metadata), INVALID_ARGUMENT (not
+ * an esm file, wrong tensor type, esm.first_block_fc1_fp16 set),
+ * SHAPE_MISMATCH (tensor size against the metadata). */
+int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char* path, int act_quant_mode,
+                                      int attention_mode, esm_gfx950_model** out);
 /* Switch the activation quantisation mode of a W8A8 model. */
 int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int act_mode);
 

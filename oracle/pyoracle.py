@@ -243,6 +243,11 @@ class RefLib:
             "esmref_model_free": (None, [vp]),
             "esmref_forward_packed": (i32, [vp, vp, vp, i32, i32, vp]),
             "esmref_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
+            "esmref_gguf_save_model": (i32, [vp, C.c_char_p]),
+            "esmref_gguf_tensor": (i32, [C.c_char_p, C.c_char_p, vp, sz, C.POINTER(C.c_uint32),
+                                         C.POINTER(C.c_uint64), C.POINTER(C.c_uint32), C.POINTER(sz)]),
+            "esmref_gguf_meta": (i32, [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int64),
+                                       C.POINTER(C.c_double)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -252,6 +257,31 @@ class RefLib:
 
     def isa(self) -> str:
         return self.lib.esmref_isa().decode()
+
+    def gguf_tensor(self, path: str, name: str, cap: int = 1 << 30):
+        """(type, dims, raw bytes) of one tensor through the reference's GGUF
+        reader, None when absent; raises when the reader rejects the file."""
+        buf = np.zeros(0, np.uint8)
+        t, nd, nbytes = C.c_uint32(), C.c_uint32(), C.c_size_t()
+        shape = (C.c_uint64 * 8)()
+        rc = self.lib.esmref_gguf_tensor(os.fsencode(path), name.encode(), None, 0, C.byref(t), shape, C.byref(nd),
+                                         C.byref(nbytes))
+        if rc == 1:
+            return None
+        if rc != 0:
+            raise ValueError(f"reference GGUF reader rejected {path}")
+        buf = np.zeros(min(nbytes.value, cap), np.uint8)
+        self.lib.esmref_gguf_tensor(os.fsencode(path), name.encode(), _p(buf), buf.size, C.byref(t), shape,
+                                    C.byref(nd), C.byref(nbytes))
+        return int(t.value), tuple(int(shape[i]) for i in range(nd.value)), buf.tobytes()
+
+    def gguf_meta(self, path: str, key: str):
+        """A metadata value through the reference's reader: int, float, bool,
+        ("str", length), or None when absent."""
+        kind, iv, fv = C.c_int(), C.c_int64(), C.c_double()
+        if self.lib.esmref_gguf_meta(os.fsencode(path), key.encode(), C.byref(kind), C.byref(iv), C.byref(fv)) != 0:
+            raise ValueError(f"reference GGUF reader rejected {path}")
+        return {0: None, 1: iv.value, 2: fv.value, 3: bool(iv.value), 4: ("str", iv.value)}[kind.value]
 
     def plan_batches(self, lengths, max_batch_size: int = 256, imbalance_threshold: float = 1.2):
         """The reference's PlanBatches (src/sched/scheduler.cpp:54-75) as a list of groups."""
@@ -357,6 +387,11 @@ class RefModel:
         m, keep = make_or_model(weights, int8, per_token=False)
         self.ref, self.cfg = ref, weights.cfg
         self.handle = ref.lib.esmref_model_create(C.byref(m))
+
+    def save_gguf(self, path: str):
+        """Model::SaveToGguf's tensors and metadata through the reference's writer."""
+        if self.ref.lib.esmref_gguf_save_model(self.handle, os.fsencode(path)) != 0:
+            raise ValueError("reference GGUF writer failed")
 
     def forward_packed(self, batch):
         T = batch.total_tokens

@@ -13,8 +13,11 @@
 // is not buildable from its sources alone. esmref_forward_packed below
 // restates its call sequence (src/model.cpp:932-1066 TransformerBlock,
 // :1093-1255 ForwardPackedInto) over the reference's own kernel facade.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <unordered_map>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -22,6 +25,7 @@
 #include <vector>
 
 #include "esm_cpp/cpu_features.h"
+#include "esm_cpp/io.h"
 #include "esm_cpp/kernels.h"
 #include "esm_cpp/quant.h"
 #include "esm_cpp/scheduler.h"
@@ -245,6 +249,131 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
   esm::kernels::LayerNorm(attn.data(), r->lm_ln_w.data(), r->lm_ln_b.data(), c.eps, ln.data(), T, d);
   esm::kernels::Linear(ln.data(), r->embed.data(), r->dec_b.data(), logits, T, V, d);
   return 0;
+}
+
+// Model::SaveToGguf (src/model.cpp:562-700) restated over a RefModel: the
+// same metadata keys, tensor names, shapes and order, written by the
+// reference's own GgufFile::Write (src/io/gguf.cpp:391-465). Returns 0, or -1
+// with the exception message printed.
+int esmref_gguf_save_model(void* h, const char* path) {
+  auto* r = static_cast<RefModel*>(h);
+  const or_model& c = r->cfg;
+  using G = esm::io::GgufFile;
+  const bool q = c.weights_int8 != 0;
+  const uint64_t d = c.hidden, f = c.ffn, V = c.vocab;
+  std::unordered_map<std::string, G::MetadataValue> meta;
+  meta.emplace("general.architecture", std::string("esm"));
+  meta.emplace("general.alignment", static_cast<std::int64_t>(32));
+  meta.emplace("general.file_type", static_cast<std::int64_t>(q ? 2 : 1));
+  meta.emplace("esm.block_count", static_cast<std::int64_t>(c.num_layers));
+  meta.emplace("esm.embedding_length", static_cast<std::int64_t>(d));
+  meta.emplace("esm.feed_forward_length", static_cast<std::int64_t>(f));
+  meta.emplace("esm.attention.head_count", static_cast<std::int64_t>(c.heads));
+  meta.emplace("esm.attention.head_count_kv", static_cast<std::int64_t>(c.heads));
+  meta.emplace("esm.attention.layer_norm_epsilon", static_cast<double>(c.eps));
+  meta.emplace("esm.rope.dimension_count", static_cast<std::int64_t>(c.head_dim));
+  meta.emplace("esm.context_length", static_cast<std::int64_t>(1024));
+  meta.emplace("esm.gguf_writer", std::string("esm-cpp 0.1.0"));
+  meta.emplace("esm.weights_quantized", q);
+  meta.emplace("esm.first_block_fc1_fp16", false);
+  auto f32 = [](const std::vector<float>& w, std::vector<uint64_t> shape) {
+    G::WriteTensor t;
+    t.dtype = G::GgmlType::F32;
+    t.shape = std::move(shape);
+    t.data = w.data();
+    t.size_bytes = w.size() * sizeof(float);
+    return t;
+  };
+  std::vector<std::vector<std::byte>> blobs;
+  blobs.reserve(static_cast<size_t>(c.num_layers) * 6);
+  auto q8 = [&](const esm::quant::QuantizedTensor& qt, uint64_t K, uint64_t N) {
+    std::vector<std::byte> b(qt.packed.size() + qt.per_channel_scales.size() * sizeof(float));
+    std::memcpy(b.data(), qt.packed.data(), qt.packed.size());
+    std::memcpy(b.data() + qt.packed.size(), qt.per_channel_scales.data(), qt.per_channel_scales.size() * 4);
+    blobs.push_back(std::move(b));
+    G::WriteTensor t;
+    t.dtype = G::GgmlType::Q8_ESM;
+    t.shape = {K, N};
+    t.data = blobs.back().data();
+    t.size_bytes = blobs.back().size();
+    return t;
+  };
+  auto name = [](int i, const char* s) { return "blk." + std::to_string(i) + "." + s; };
+  std::vector<std::pair<std::string, G::WriteTensor>> t;
+  t.emplace_back("token_embd.weight", f32(r->embed, {d, V}));
+  const char* wn[6] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight", "ffn_up.weight",
+                       "ffn_down.weight"};
+  const char* bn[6] = {"attn_q.bias", "attn_k.bias", "attn_v.bias", "attn_output.bias", "ffn_up.bias",
+                       "ffn_down.bias"};
+  for (int i = 0; i < c.num_layers; ++i) {
+    const RefLayer& L = r->layers[i];
+    t.emplace_back(name(i, "attn_norm.weight"), f32(L.ln1_w, {d}));
+    t.emplace_back(name(i, "attn_norm.bias"), f32(L.ln1_b, {d}));
+    for (int j = 0; j < 4; ++j)
+      t.emplace_back(name(i, wn[j]), q ? q8(L.w8[j], d, d) : f32(L.w32[j], {d, d}));
+    for (int j = 0; j < 4; ++j) t.emplace_back(name(i, bn[j]), f32(L.bias[j], {d}));
+    t.emplace_back(name(i, "ffn_norm.weight"), f32(L.ln2_w, {d}));
+    t.emplace_back(name(i, "ffn_norm.bias"), f32(L.ln2_b, {d}));
+    t.emplace_back(name(i, wn[4]), q ? q8(L.w8[4], d, f) : f32(L.w32[4], {d, f}));
+    t.emplace_back(name(i, wn[5]), q ? q8(L.w8[5], f, d) : f32(L.w32[5], {f, d}));
+    t.emplace_back(name(i, bn[4]), f32(L.bias[4], {f}));
+    t.emplace_back(name(i, bn[5]), f32(L.bias[5], {d}));
+  }
+  t.emplace_back("enc_norm.weight", f32(r->final_ln_w, {d}));
+  t.emplace_back("enc_norm.bias", f32(r->final_ln_b, {d}));
+  t.emplace_back("lm_head.weight", f32(r->lm_dense_w, {d, d}));
+  t.emplace_back("lm_head.bias", f32(r->lm_dense_b, {d}));
+  t.emplace_back("lm_head_norm.weight", f32(r->lm_ln_w, {d}));
+  t.emplace_back("lm_head_norm.bias", f32(r->lm_ln_b, {d}));
+  t.emplace_back("output.bias", f32(r->dec_b, {V}));
+  try {
+    G::Write(path, meta, t);
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "esmref_gguf_save_model: %s\n", e.what());
+    return -1;
+  }
+  return 0;
+}
+
+// One tensor of a GGUF file through the reference's reader
+// (GgufFile::Open, src/io/gguf.cpp:251-340): type, dims, byte size, and up to
+// `cap` bytes of data. Returns 0, 1 when the tensor is absent, -1 when the
+// reader rejects the file.
+int esmref_gguf_tensor(const char* path, const char* tname, void* data, size_t cap, uint32_t* type,
+                       uint64_t* shape, uint32_t* ndim, size_t* bytes) {
+  try {
+    auto gf = esm::io::GgufFile::Open(path);
+    auto info = gf->Get(tname);
+    if (!info) return 1;
+    *type = static_cast<uint32_t>(info->dtype);
+    *ndim = static_cast<uint32_t>(info->shape.size());
+    for (size_t i = 0; i < info->shape.size() && i < 8; ++i) shape[i] = info->shape[i];
+    *bytes = info->size_bytes;
+    if (cap) std::memcpy(data, info->data, std::min(cap, info->size_bytes));
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "esmref_gguf_tensor: %s\n", e.what());
+    return -1;
+  }
+}
+
+// Integer / bool / float metadata through the reference's reader: *kind 0
+// absent, 1 int, 2 float, 3 bool, 4 string (length in *ival).
+int esmref_gguf_meta(const char* path, const char* key, int* kind, int64_t* ival, double* fval) {
+  try {
+    auto gf = esm::io::GgufFile::Open(path);
+    auto v = gf->Metadata(key);
+    *kind = 0;
+    if (!v) return 0;
+    if (auto* i = std::get_if<std::int64_t>(&*v)) { *kind = 1; *ival = *i; }
+    else if (auto* x = std::get_if<double>(&*v)) { *kind = 2; *fval = *x; }
+    else if (auto* b = std::get_if<bool>(&*v)) { *kind = 3; *ival = *b ? 1 : 0; }
+    else if (auto* s = std::get_if<std::string>(&*v)) { *kind = 4; *ival = static_cast<int64_t>(s->size()); }
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "esmref_gguf_meta: %s\n", e.what());
+    return -1;
+  }
 }
 
 // PlanBatches (src/sched/scheduler.cpp:54-75) flattened: the caller-index
