@@ -661,6 +661,9 @@ struct esm_gfx950_model {
   // W8A8 models: Q's 1/sqrt(head_dim) multiplied into the Q weight scales and
   // bias at upload (exact when it is a power of two).
   bool q_scale_folded = false;
+  // Layer 0's fc1 input rounded to fp16 (reference Config::first_block_fc1_fp16,
+  // include/esm_cpp/model.h:36-41; applied at src/model.cpp:1028-1033).
+  bool first_block_fc1_fp16 = false;
   // A staged batch is split into `parts` contiguous sequence groups; each
   // part has its own arena, metadata and (with more than one part) its own
   // HIP stream, so the parts' kernels can occupy different CUs at the same
@@ -872,6 +875,12 @@ extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_mod
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled) {
+  if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
+  model->first_block_fc1_fp16 = enabled != 0;
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes) {
   if (!model || !bytes) return ESM_GFX950_INVALID_ARGUMENT;
   size_t b = 0;
@@ -980,7 +989,8 @@ P shift(P p, const char* from, const char* to) {
 // next -- this layer's ffn LN, the next layer's attn LN, or the final LN --
 // so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
 // fc2 output of the previous layer (null for the first layer).
-int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, const Arena& a, const Meta& md,
+int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
+               const Meta& md,
                int T, int nwork, const float* resid_in) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
@@ -1093,11 +1103,11 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   // residual + ffn LN + quant
   if (tok) {
     ESM_HIP(ctx, launch_layernorm_quant(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
-                                        a.xs, s));
+                                        a.xs, s, round16));
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
     ESM_HIP(ctx, launch_layernorm(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
-                                  s));
+                                  s, round16));
     ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax + 2, a.xq, ldq_d, a.xs, s));
   }
 
@@ -1167,8 +1177,8 @@ int f32_linear(esm_gfx950_ctx* ctx, const float* A, const DevLinear& W, float* C
   return ESM_GFX950_OK;
 }
 
-int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, const Arena& a, const Meta& md,
-              int T, int nwork) {
+int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
+              const Meta& md, int T, int nwork) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, H = c.num_heads, dh = c.head_dim;
   hipStream_t s = ctx->stream;
@@ -1179,7 +1189,8 @@ int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L,
   ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d, s));
   ESM_TRY(f32_linear(ctx, a.attn, L.out, a.hidden, T, kF32Resid));
-  ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s,
+                                round16));
   ESM_TRY(f32_linear(ctx, a.ln, L.fc1, a.inter, T, kF32Gelu));
   ESM_TRY(f32_linear(ctx, a.inter, L.fc2, a.hidden, T, kF32Resid));
   return ESM_GFX950_OK;
@@ -1284,12 +1295,14 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   hipStream_t s = ctx->stream;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
   const float* pending = nullptr;  // fc2 output awaiting its residual add
-  for (const DevLayer& L : m->layers) {
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    const DevLayer& L = m->layers[li];
+    const int round16 = (li == 0 && m->first_block_fc1_fp16) ? 1 : 0;
     if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, a, md, T, nwork, pending));
+      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending));
       pending = a.ybuf;
     } else {
-      ESM_TRY(layer_f32(ctx, m, L, a, md, T, nwork));
+      ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork));
     }
   }
   // (Last residual +) final LN and lm head: dense -> GELU -> LN -> tied
@@ -1603,8 +1616,6 @@ extern "C" int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char
   c.weights_int8 = meta_bool("esm.weights_quantized") ? 1 : 0;
   c.act_quant_mode = act_quant_mode;
   c.attention_mode = attention_mode;
-  ESM_REQUIRE(ctx, !meta_bool("esm.first_block_fc1_fp16"),
-              "gguf: esm.first_block_fc1_fp16 (layer-0 fp16 rounding of the fc1 input) is not supported");
   const size_t d = c.hidden_size, ffn = c.intermediate_size, V = c.vocab_size;
 
   auto f32 = [&](const std::string& name, size_t count, const float** dst) -> int {
@@ -1670,5 +1681,7 @@ extern "C" int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char
   ESM_TRY(f32("lm_head_norm.weight", d, &desc.lm_ln_w));
   ESM_TRY(f32("lm_head_norm.bias", d, &desc.lm_ln_b));
   ESM_TRY(f32("output.bias", V, &desc.lm_decoder_bias));
-  return esm_gfx950_model_create(ctx, &desc, out);
+  ESM_TRY(esm_gfx950_model_create(ctx, &desc, out));
+  (*out)->first_block_fc1_fp16 = meta_bool("esm.first_block_fc1_fp16");
+  return ESM_GFX950_OK;
 }

@@ -22,6 +22,17 @@ __device__ __forceinline__ float act_scale_from_absmax(float amax) {
   return amax > 0.0f ? amax / 127.0f : 1.0f;
 }
 
+// Each value rounded to the nearest fp16 (ties to even) and widened back:
+// the reference's first-block fc1 escape (RoundToFp16Inplace, src/model.cpp:
+// 912-930, VCVTPS2PH round-to-nearest).
+__device__ __forceinline__ float4 round_f16(float4 y) {
+  y.x = static_cast<float>(static_cast<_Float16>(y.x));
+  y.y = static_cast<float>(static_cast<_Float16>(y.y));
+  y.z = static_cast<float>(static_cast<_Float16>(y.z));
+  y.w = static_cast<float>(static_cast<_Float16>(y.w));
+  return y;
+}
+
 // Lane's NV float4 chunks of a row (chunk j at column (j*64 + lane)*4). Every
 // load is issued before any value is used: a chunk past `cols` re-reads
 // column 0 (in bounds) and is then zeroed, so no load sits in a branch that
@@ -52,7 +63,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ out,
     int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
-    float* __restrict__ scales) {
+    float* __restrict__ scales, int round16) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -98,6 +109,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     y.y = (v[j].y - mean) * inv_std * g[j].y + bt[j].y;
     y.z = (v[j].z - mean) * inv_std * g[j].z + bt[j].z;
     y.w = (v[j].w - mean) * inv_std * g[j].w + bt[j].w;
+    if (round16) y = round_f16(y);
     v[j] = y;
     if (c < d) {
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
@@ -131,7 +143,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
 __global__ __launch_bounds__(256) void layernorm_any_kernel(
     float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ out,
-    int rows, int d, float* tensor_absmax) {
+    int rows, int d, float* tensor_absmax, int round16) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -153,7 +165,8 @@ __global__ __launch_bounds__(256) void layernorm_any_kernel(
   float amax = 0.f;
   float* yr = out + static_cast<size_t>(row) * d;
   for (int c = lane; c < d; c += 64) {
-    const float y = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+    float y = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
+    if (round16) y = static_cast<float>(static_cast<_Float16>(y));
     yr[c] = y;
     amax = fmaxf(amax, fabsf(y));
   }
@@ -370,32 +383,33 @@ inline dim3 rows_grid(int rows) { return dim3((rows + kRowsPerBlock - 1) / kRows
 }  // namespace
 
 hipError_t launch_layernorm(float* x, const float* resid, const float* gamma, const float* beta, float eps,
-                            float* out, int rows, int d, float* tensor_absmax, hipStream_t s) {
+                            float* out, int rows, int d, float* tensor_absmax, hipStream_t s, int round16) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   const dim3 g = rows_grid(rows), b(256);
   if (d % 4 == 0 && d <= 1280) {
     hipLaunchKernelGGL((layernorm_vec_kernel<5, false>), g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d,
-                       tensor_absmax, nullptr, 0, nullptr);
+                       tensor_absmax, nullptr, 0, nullptr, round16);
   } else if (d % 4 == 0 && d <= 2560) {
     hipLaunchKernelGGL((layernorm_vec_kernel<10, false>), g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d,
-                       tensor_absmax, nullptr, 0, nullptr);
+                       tensor_absmax, nullptr, 0, nullptr, round16);
   } else {
-    hipLaunchKernelGGL(layernorm_any_kernel, g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d, tensor_absmax);
+    hipLaunchKernelGGL(layernorm_any_kernel, g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d, tensor_absmax,
+                       round16);
   }
   return hipGetLastError();
 }
 
 hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gamma, const float* beta, float eps,
-                                  int rows, int d, int8_t* q, int ldq, float* scales, hipStream_t s) {
+                                  int rows, int d, int8_t* q, int ldq, float* scales, hipStream_t s, int round16) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   if (d % 4 != 0 || d > 2560) return hipErrorInvalidValue;
   const dim3 g = rows_grid(rows), b(256);
   if (d <= 1280) {
     hipLaunchKernelGGL((layernorm_vec_kernel<5, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
-                       nullptr, q, ldq, scales);
+                       nullptr, q, ldq, scales, round16);
   } else {
     hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
-                       nullptr, q, ldq, scales);
+                       nullptr, q, ldq, scales, round16);
   }
   return hipGetLastError();
 }

@@ -120,16 +120,18 @@ constexpr int kAttnF32QTile = 64;
 // ------------------------------------------------------------ elementwise
 // LayerNorm of x [rows, d]; with resid != null x is first updated in place
 // (x += resid) and normalised after the add.
+// round16: round each output to the nearest fp16 and back (the reference's
+// first-block fc1 escape, src/model.cpp:1028-1033).
 hipError_t launch_layernorm(float* x, const float* resid, const float* gamma,
                             const float* beta, float eps, float* out,
                             int rows, int d, float* tensor_absmax,
-                            hipStream_t s);
+                            hipStream_t s, int round16 = 0);
 // LayerNorm (with the same optional residual add) fused with per-token
 // symmetric int8 quantisation.
 hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gamma,
                                   const float* beta, float eps, int rows,
                                   int d, int8_t* q, int ldq, float* scales,
-                                  hipStream_t s);
+                                  hipStream_t s, int round16 = 0);
 // GELU (erf of Abramowitz & Stegun 7.1.26) fused with per-token int8
 // quantisation of fp32 rows (cols % 4 == 0, cols <= 10240).
 hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols,

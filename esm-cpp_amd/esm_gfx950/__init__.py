@@ -42,6 +42,7 @@ EXPORTED = [
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
     "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_plan_batches",
     "esm_gfx950_forward_scheduled", "esm_gfx950_model_create_from_gguf",
+    "esm_gfx950_model_set_first_block_fc1_fp16",
 ]
 
 
@@ -104,6 +105,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
         "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
         "esm_gfx950_model_create_from_gguf": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(vp)]),
+        "esm_gfx950_model_set_first_block_fc1_fp16": (i32, [vp, vp, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -395,6 +397,11 @@ class Model:
         m = cls.__new__(cls)
         m.dev, m.handle, m.cfg = dev, h, cfg
         return m
+
+    def set_first_block_fc1_fp16(self, enabled: bool):
+        """Round layer 0's fc1 input to fp16 (esm_gfx950_model_set_first_block_fc1_fp16)."""
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_first_block_fc1_fp16(self.dev.ctx, self.handle,
+                                                                             int(bool(enabled))))
 
     def set_act_mode(self, mode: int):
         self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))

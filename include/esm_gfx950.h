@@ -244,6 +244,11 @@ typedef struct {
 int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_model_desc* desc,
                             esm_gfx950_model** out);
 int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model);
+/* Model::SetFirstBlockFc1Fp16 (reference include/esm_cpp/model.h:228-230):
+ * when enabled, layer 0's fc1 input (the ffn LayerNorm output) is rounded to
+ * the nearest fp16 and back before it is quantised or multiplied
+ * (src/model.cpp:1028-1033). Off by default. */
+int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled);
 /* Model::LoadFromGguf (reference src/model.cpp:229-298): creates a model
  * from an esm.cpp GGUF v3 file (src/io/gguf.cpp) -- esm.* metadata for the
  * shape; Q8_ESM layer linears ([N, K] int8 + [N] fp32 scales) when
@@ -252,8 +257,8 @@ int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model);
  * esm_gfx950_model_config. The file is memory-mapped and released before
  * return. Errors: IO_ERROR (open / malformed file, the reference reader's
  * messages), NOT_FOUND (missing tensor or metadata), INVALID_ARGUMENT (not
- * an esm file, wrong tensor type, esm.first_block_fc1_fp16 set),
- * SHAPE_MISMATCH (tensor size against the metadata). */
+ * an esm file, wrong tensor type), SHAPE_MISMATCH (tensor size against the
+ * metadata). esm.first_block_fc1_fp16 = true enables that escape. */
 int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char* path, int act_quant_mode,
                                       int attention_mode, esm_gfx950_model** out);
 /* Switch the activation quantisation mode of a W8A8 model. */

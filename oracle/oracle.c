@@ -10,6 +10,7 @@
  */
 #include "oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -57,6 +58,13 @@ void or_quant_act_tensor(const float* x, size_t n, int8_t* q, float* scale_out) 
 
 void or_quant_act_rows(const float* x, int M, int K, int8_t* q, float* scales) {
   for (int m = 0; m < M; ++m) or_quant_act_tensor(x + (size_t)m * K, (size_t)K, q + (size_t)m * K, scales + m);
+}
+
+/* RoundToFp16Inplace (model.cpp:912-930, x86 F16C branch): each value to
+ * the nearest fp16 (ties to even) and back. */
+void or_round_fp16(float* x, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    x[i] = _cvtsh_ss(_cvtss_sh(x[i], _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
 }
 
 /* GeluRef (gelu.cpp:30-35). */
@@ -322,6 +330,7 @@ int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, 
     linear_call(m, l, 3, attn, proj, T, d, d, qbuf, sbuf, acc);
     for (size_t i = 0; i < Td; ++i) hidden[i] += proj[i];
     or_layernorm(hidden, m->ln2_w[l], m->ln2_b[l], m->eps, ln, T, d);
+    if (m->fc1_fp16 && l == 0) or_round_fp16(ln, Td);
     linear_call(m, l, 4, ln, inter, T, f, d, qbuf, sbuf, acc);
     or_gelu(inter, inter_g, Tf);
     linear_call(m, l, 5, inter_g, proj, T, d, f, qbuf, sbuf, acc);

@@ -50,6 +50,8 @@ void or_linear_int8_w8a16(const float* A, const int8_t* Wq, const float* scales,
 void or_linear_f32(const float* A, const float* W, const float* bias, float* C, int M, int N, int K);
 /* LayerNormRef (src/kernels/layernorm.cpp:23-44). */
 void or_layernorm(const float* x, const float* gamma, const float* beta, float eps, float* out, int rows, int d);
+/* RoundToFp16Inplace (src/model.cpp:912-930): nearest fp16 and back. */
+void or_round_fp16(float* x, size_t n);
 /* GeluRef (src/kernels/gelu.cpp:30-35). */
 void or_gelu(const float* x, float* out, size_t n);
 /* RopeBuildTables (src/kernels/rope_tables.cpp:14-29). */
@@ -80,6 +82,7 @@ typedef struct {
   const float* lm_dense_w; const float* lm_dense_b;
   const float* lm_ln_w; const float* lm_ln_b;
   const float* lm_decoder_bias;
+  int fc1_fp16;        /* 1: layer 0's fc1 input rounded to fp16 (model.cpp:1028-1033) */
 } or_model;
 
 /* Embed (src/model.cpp:737-778) + TransformerBlock per layer (:932-1066) +

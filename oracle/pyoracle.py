@@ -34,13 +34,13 @@ class _OrModel(C.Structure):
                 ("ln2_w", C.POINTER(vp)), ("ln2_b", C.POINTER(vp)), ("w_f32", C.POINTER(vp)),
                 ("w_i8", C.POINTER(vp)), ("w_scale", C.POINTER(vp)), ("bias", C.POINTER(vp)),
                 ("final_ln_w", vp), ("final_ln_b", vp), ("lm_dense_w", vp), ("lm_dense_b", vp),
-                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp)]
+                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp), ("fc1_fp16", i32)]
 
 
 LINEARS = ("q", "k", "v", "out", "fc1", "fc2")
 
 
-def make_or_model(weights, int8: bool, per_token: bool):
+def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False):
     """Builds the or_model descriptor (and keeps its arrays alive)."""
     cfg = weights.cfg
     keep = []
@@ -80,6 +80,7 @@ def make_or_model(weights, int8: bool, per_token: bool):
     m.lm_dense_w, m.lm_dense_b = p(F["lm_head.dense.weight"]), p(F["lm_head.dense.bias"])
     m.lm_ln_w, m.lm_ln_b = p(F["lm_head.ln.weight"]), p(F["lm_head.ln.bias"])
     m.lm_decoder_bias = p(F["lm_head.decoder.bias"])
+    m.fc1_fp16 = int(fc1_fp16)
     keep.extend([ln1w, ln1b, ln2w, ln2b, wf, wi, ws, bs])
     return m, keep
 
@@ -101,6 +102,7 @@ class Oracle:
             "or_linear_f32": [vp, vp, vp, vp, i32, i32, i32],
             "or_layernorm": [vp, vp, vp, f32, vp, i32, i32],
             "or_gelu": [vp, vp, sz],
+            "or_round_fp16": [vp, sz],
             "or_rope_tables": [i32, i32, vp, vp],
             "or_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
             "or_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
@@ -176,6 +178,11 @@ class Oracle:
         self.lib.or_layernorm(_p(x), _p(_c(g, np.float32)), _p(_c(b, np.float32)), eps, _p(out), rows, d)
         return out
 
+    def round_fp16(self, x):
+        out = _c(x, np.float32).copy()
+        self.lib.or_round_fp16(_p(out), out.size)
+        return out
+
     def gelu(self, x):
         x = _c(x, np.float32)
         out = np.empty_like(x)
@@ -200,8 +207,8 @@ class Oracle:
         self.lib.or_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
         return out
 
-    def forward_packed(self, weights, batch, int8: bool, per_token: bool):
-        m, keep = make_or_model(weights, int8, per_token)
+    def forward_packed(self, weights, batch, int8: bool, per_token: bool, fc1_fp16: bool = False):
+        m, keep = make_or_model(weights, int8, per_token, fc1_fp16)
         T = batch.total_tokens
         logits = np.empty((T, weights.cfg.vocab_size), np.float32)
         rc = self.lib.or_forward_packed(C.byref(m), _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
@@ -383,8 +390,8 @@ class RefLib:
 class RefModel:
     """Reference CPU forward (reference kernels, restated ForwardPackedInto)."""
 
-    def __init__(self, ref: RefLib, weights, int8: bool):
-        m, keep = make_or_model(weights, int8, per_token=False)
+    def __init__(self, ref: RefLib, weights, int8: bool, fc1_fp16: bool = False):
+        m, keep = make_or_model(weights, int8, per_token=False, fc1_fp16=fc1_fp16)
         self.ref, self.cfg = ref, weights.cfg
         self.handle = ref.lib.esmref_model_create(C.byref(m))
 

@@ -13,6 +13,7 @@
 // is not buildable from its sources alone. esmref_forward_packed below
 // restates its call sequence (src/model.cpp:932-1066 TransformerBlock,
 // :1093-1255 ForwardPackedInto) over the reference's own kernel facade.
+#include <immintrin.h>
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -67,6 +68,13 @@ struct RefModel {
 };
 
 std::vector<float> vec(const float* p, size_t n) { return std::vector<float>(p, p + n); }
+
+// RoundToFp16Inplace (src/model.cpp:912-930) lives in model.cpp, which is
+// not buildable here: the x86 F16C branch restated.
+void or_round_fp16_shim(float* x, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    x[i] = _cvtsh_ss(_cvtss_sh(x[i], _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+}
 
 }  // namespace
 
@@ -238,6 +246,7 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
     linear(L, 3, attn.data(), proj.data(), T);
     esm::kernels::ResidualAddInplace(hidden.data(), proj.data(), Td);
     esm::kernels::LayerNorm(hidden.data(), L.ln2_w.data(), L.ln2_b.data(), c.eps, ln.data(), T, d);
+    if (c.fc1_fp16 && &L == &r->layers.front()) or_round_fp16_shim(ln.data(), ln.size());
     linear(L, 4, ln.data(), inter.data(), T);
     esm::kernels::Gelu(inter.data(), inter_g.data(), Tf);
     linear(L, 5, inter_g.data(), proj.data(), T);
@@ -275,7 +284,7 @@ int esmref_gguf_save_model(void* h, const char* path) {
   meta.emplace("esm.context_length", static_cast<std::int64_t>(1024));
   meta.emplace("esm.gguf_writer", std::string("esm-cpp 0.1.0"));
   meta.emplace("esm.weights_quantized", q);
-  meta.emplace("esm.first_block_fc1_fp16", false);
+  meta.emplace("esm.first_block_fc1_fp16", c.fc1_fp16 != 0);
   auto f32 = [](const std::vector<float>& w, std::vector<uint64_t> shape) {
     G::WriteTensor t;
     t.dtype = G::GgmlType::F32;

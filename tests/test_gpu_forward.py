@@ -209,3 +209,34 @@ def test_config5_3b_shapes_vs_oracle(dev, oracle, per_token):
     print(f"3B shapes per_token={per_token}: corr={c:.6f} argmax_agree={agree:.4f}")
     assert c >= 0.9999, c
     assert agree >= 0.98, agree
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+def test_first_block_fc1_fp16_vs_oracle(dev, oracle, w650_small, small_batch, per_token):
+    """The first-block fp16 escape (layer 0's fc1 input rounded to fp16,
+    reference src/model.cpp:1028-1033) against the oracle with the same escape,
+    at the W8A8 bar; the escape changes the logits."""
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w650_small, int8=True, act_mode=mode)
+    plain = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.set_first_block_fc1_fp16(True)
+    got = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.free()
+    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token, fc1_fp16=True)
+    c = corr(got, want)
+    print(f"fc1 fp16 escape per_token={per_token}: corr={c:.6f}")
+    assert c >= 0.9999, c
+    assert not np.array_equal(got, plain)
+
+
+def test_first_block_fc1_fp16_fp32_model(dev, oracle, w8m):
+    """fp32 model with the escape. A LayerNorm output one fp32 ulp away from
+    an fp16 rounding boundary rounds to the neighbouring fp16 value (2^-11
+    relative) on one side, so the bar is 1e-3 instead of config 1's 1e-5."""
+    batch = syn.config1_batch()
+    m = eg.Model(dev, w8m, int8=False)
+    m.set_first_block_fc1_fp16(True)
+    got = m.forward_packed(batch.ids, batch.cu)
+    m.free()
+    want = oracle.forward_packed(w8m, batch, int8=False, per_token=False, fc1_fp16=True)
+    np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-3)

@@ -97,12 +97,28 @@ def test_gguf_missing_and_mistyped_tensors(dev, tmp_path):
     with pytest.raises(eg.Gfx950Error, match="expected Q8_ESM for blk.0.attn_q.weight"):
         eg.Model.from_gguf(dev, p)
     meta["esm.weights_quantized"] = False
-    meta["esm.first_block_fc1_fp16"] = True
-    gguf.write(p, meta, [(n, t, d, a.tobytes()) for n, (t, d, a) in ts.items()])
-    with pytest.raises(eg.Gfx950Error, match="first_block_fc1_fp16"):
-        eg.Model.from_gguf(dev, p)
-    meta["esm.first_block_fc1_fp16"] = False
     meta["esm.embedding_length"] = 640
     gguf.write(p, meta, [(n, t, d, a.tobytes()) for n, (t, d, a) in ts.items()])
     with pytest.raises(eg.Gfx950Error, match="expected"):
         eg.Model.from_gguf(dev, p)
+
+
+def test_gguf_first_block_fc1_fp16_flag(dev, ref, tmp_path, batch):
+    """esm.first_block_fc1_fp16 = true (as the reference's writer stores it)
+    turns the escape on: same logits as the directly created model with
+    set_first_block_fc1_fp16(True)."""
+    from pyoracle import RefModel
+    w = _weights(True)
+    p = str(tmp_path / "fp16.gguf")
+    rm = RefModel(ref, w, int8=True, fc1_fp16=True)
+    rm.save_gguf(p)
+    rm.free()
+    assert gguf.read_metadata(p)["esm.first_block_fc1_fp16"] is True
+    direct = eg.Model(dev, w, int8=True)
+    direct.set_first_block_fc1_fp16(True)
+    want = direct.forward_packed(batch.ids, batch.cu)
+    direct.free()
+    loaded = eg.Model.from_gguf(dev, p)
+    got = loaded.forward_packed(batch.ids, batch.cu)
+    loaded.free()
+    np.testing.assert_array_equal(got, want)

@@ -177,8 +177,10 @@ def test_vs_reference_build_w8a8_dequant(oracle, ref):
     assert sc2 == sc and np.array_equal(u8.astype(np.int32) - 128, aq.astype(np.int32))
 
 
-def test_vs_reference_build_forward_fp32(oracle, ref):
-    """Restated fp32 forward == the reference's kernels forced to the Ref ISA."""
+@pytest.mark.parametrize("fc1_fp16", [False, True])
+def test_vs_reference_build_forward_fp32(oracle, ref, fc1_fp16):
+    """Restated fp32 forward == the reference's kernels forced to the Ref ISA
+    (with and without the first-block fp16 rounding of the fc1 input)."""
     from esm_gfx950 import synthetic as syn
     from pyoracle import RefModel
     cfg = syn.EsmConfig("tiny", 2, 64, 4, 128)
@@ -186,12 +188,28 @@ def test_vs_reference_build_forward_fp32(oracle, ref):
     batch = syn.batch_from_lengths([9, 30, 2, 17], seed=5)
     os.environ["ESM_FORCE_ISA"] = "ref"
     try:
-        m = RefModel(ref, w, int8=False)
+        m = RefModel(ref, w, int8=False, fc1_fp16=fc1_fp16)
         want = m.forward_packed(batch)
         m.free()
     finally:
         del os.environ["ESM_FORCE_ISA"]
-    assert np.array_equal(oracle.forward_packed(w, batch, int8=False, per_token=False), want)
+    got = oracle.forward_packed(w, batch, int8=False, per_token=False, fc1_fp16=fc1_fp16)
+    assert np.array_equal(got, want)
+    if fc1_fp16:
+        assert not np.array_equal(got, oracle.forward_packed(w, batch, int8=False, per_token=False))
+
+
+def test_closed_form_round_fp16(oracle):
+    """RoundToFp16Inplace == numpy's IEEE round-to-nearest-even float16 cast:
+    normals, ties, subnormals, overflow to inf, NaN."""
+    r = rng(11)
+    x = np.concatenate([r.normal(0, 1, 4000), r.normal(0, 3e4, 500), r.normal(0, 1e-5, 500),
+                        [1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 65504.0, 65520.0, 7e4, -7e4, 2.0 ** -25, 0.0, -0.0]])
+    x = x.astype(np.float32)
+    with np.errstate(over="ignore"):  # the overflow to inf is one of the cases
+        want = x.astype(np.float16).astype(np.float32)
+    got = oracle.round_fp16(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 # ------------------------------------------------- independent closed forms
