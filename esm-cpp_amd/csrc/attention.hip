@@ -259,7 +259,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 // select, then the words are unpacked into hi/lo planes with v_perm.
 constexpr int KCX = 64;                 // keys per LDS chunk
 constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
-constexpr int kVPitchX = KCX * 2 + 16;  // bytes per dim row of V^T hi / lo
+// V^T hi / lo planes: one 160-byte row per dim, keys in 4-key (8-byte) quads
+// stored at quad ^ (dim / 4). The staging writes (4 bytes per lane, four dims
+// apart) and the PV fragment reads (8 bytes per lane, 16 dims by 4 quads) then
+// touch distinct LDS banks; a plain 144-byte pitch put 16 writing lanes on 4
+// banks.
+constexpr int kVPitchX = 160;
+static_assert(KCX == 64, "the V^T swizzle covers 16 key quads");
+__device__ __forceinline__ int vt_off(int dim, int key) {
+  return dim * kVPitchX + ((((key >> 2) ^ (dim >> 2)) & 15) << 3) + ((key & 3) << 1);
+}
 
 // Low (sel_lo) or high (sel_hi) 16-bit halves of two words, packed: the hi
 // or lo fp16 parts of two consecutive values.
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int off = (dq * 4 + j) * kVPitchX + key0 * 2;
+        const int off = vt_off(dq * 4 + j, key0);
         *reinterpret_cast<uint32_t*>(sVh + off) = halves(xa[j], xb[j], kSelLo);
         *reinterpret_cast<uint32_t*>(sVl + off) = halves(xa[j], xb[j], kSelHi);
       }
@@ -464,12 +473,12 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const int r = (db * 16 + lr) * kVPitchX;
-          const int ca = ((2 * kp) * 16 + lg * 4) * 2, cb = ((2 * kp + 1) * 16 + lg * 4) * 2;
-          const f16x4 vah = *reinterpret_cast<const f16x4*>(sVh + r + ca);
-          const f16x4 vbh = *reinterpret_cast<const f16x4*>(sVh + r + cb);
-          const f16x4 val = *reinterpret_cast<const f16x4*>(sVl + r + ca);
-          const f16x4 vbl = *reinterpret_cast<const f16x4*>(sVl + r + cb);
+          const int dim = db * 16 + lr;
+          const int ca = vt_off(dim, (2 * kp) * 16 + lg * 4), cb = vt_off(dim, (2 * kp + 1) * 16 + lg * 4);
+          const f16x4 vah = *reinterpret_cast<const f16x4*>(sVh + ca);
+          const f16x4 vbh = *reinterpret_cast<const f16x4*>(sVh + cb);
+          const f16x4 val = *reinterpret_cast<const f16x4*>(sVl + ca);
+          const f16x4 vbl = *reinterpret_cast<const f16x4*>(sVl + cb);
           const f16x8 vfh = f16x8{vah[0], vah[1], vah[2], vah[3], vbh[0], vbh[1], vbh[2], vbh[3]};
           const f16x8 vfl = f16x8{val[0], val[1], val[2], val[3], vbl[0], vbl[1], vbl[2], vbl[3]};
 #pragma unroll
