@@ -23,7 +23,7 @@ OBJDIR = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(LIBDIR, "libesm_gfx950.so")
 
-SOURCES = ["gemm_i8.hip", "attention.hip", "elementwise.hip", "gemm_f32.hip", "capi.cpp", "gguf.cpp"]
+SOURCES = ["gemm_i8.hip", "attention.hip", "elementwise.hip", "gemm_f32.hip", "capi.cpp", "gguf.cpp", "observer.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -6,15 +6,21 @@
 
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "esm_gfx950.h"
 #include "gguf.hpp"
 #include "kernels.hpp"
+#include "observer.hpp"
 
 using namespace esm_gfx950;
 
@@ -98,6 +104,18 @@ struct esm_gfx950_weight {
   int N = 0, K = 0, ldk = 0;
   int8_t* data = nullptr;  // [N, ldk], zero past K
   float* scales = nullptr;  // [N]
+};
+
+// Activation observer (reference esm::ActivationObserver): per-site
+// reservoirs on the host, plus device and pinned staging for the gathered
+// values, grown on demand (kReservoirSize entries per site of one call).
+struct esm_gfx950_observer {
+  std::map<std::string, obs::Reservoir> sites;
+  uint32_t* d_pos = nullptr;
+  float* d_val = nullptr;
+  uint32_t* h_pos = nullptr;
+  float* h_val = nullptr;
+  size_t cap_sites = 0;
 };
 
 #define ESM_HIP(ctx, expr)                                   \
@@ -420,6 +438,15 @@ extern "C" int esm_gfx950_quantize_act(esm_gfx950_ctx* ctx, const float* x, int 
   void* s = nullptr;
   ESM_TRY(ctx->get_scratch(256, &s));
   return quantize_into(ctx, x, M, K, mode, q, ldq, scales, static_cast<float*>(s));
+}
+
+extern "C" int esm_gfx950_gelu_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int K, int8_t* q, int ldq,
+                                            float* scales) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, x && q && scales && M >= 0 && K > 0 && ldq >= K, "gelu_quantize_act: bad arguments");
+  ESM_REQUIRE(ctx, K % 4 == 0 && K <= 10240, "gelu_quantize_act: K must be a multiple of 4 and at most 10240");
+  ESM_HIP(ctx, launch_gelu_quant_rows(x, K, M, K, q, ldq, scales, ctx->stream));
+  return ESM_GFX950_OK;
 }
 
 extern "C" int esm_gfx950_linear_i8(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
@@ -981,6 +1008,114 @@ P shift(P p, const char* from, const char* to) {
   return reinterpret_cast<P>(const_cast<char*>(to) + (reinterpret_cast<const char*>(p) - from));
 }
 
+// Capture state of one esm_gfx950_forward_with_observer call. The sites are
+// known before the forward starts (four per layer, reference
+// src/model.cpp:952-955,996-999,1023-1026,1047-1050), and Algorithm R's
+// decisions need only each site's value count, so host threads plan every
+// site's reservoir slots while the device runs; capture() waits for its
+// site's plan, then copies the positions to the device and gathers the
+// values behind the kernel that produced them. finish() copies the gathered
+// values back and stores them in the reservoirs.
+struct ObsSite {
+  obs::Reservoir* r = nullptr;
+  size_t n = 0;
+  std::vector<uint32_t> slots;
+  size_t count = 0;
+};
+
+class ObsRun {
+ public:
+  ObsRun(esm_gfx950_observer* o, std::vector<ObsSite> sites) : obs_(o), sites_(std::move(sites)) {
+    done_.assign(sites_.size(), 0);
+    size_t workers = std::thread::hardware_concurrency();
+    if (const char* e = std::getenv("ESM_NUM_THREADS")) workers = std::strtoul(e, nullptr, 10);
+    workers = std::max<size_t>(1, std::min<size_t>({workers, 16, sites_.size()}));
+    // Workers take sites in forward order from a shared counter.
+    for (size_t w = 0; w < workers; ++w) {
+      try {
+        threads_.emplace_back([this] { work(); });
+      } catch (...) {
+        break;
+      }
+    }
+    if (threads_.empty()) work();
+  }
+  ~ObsRun() { join(); }
+  void join() {
+    for (auto& t : threads_)
+      if (t.joinable()) t.join();
+  }
+  void work() {
+    for (;;) {
+      size_t k;
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        if (taken_ == sites_.size()) return;
+        k = taken_++;
+      }
+      ObsSite& st = sites_[k];
+      int ok = 1;
+      try {
+        st.slots.resize(obs::kReservoirSize);
+        st.count = obs::plan(*st.r, st.n, st.slots.data(), obs_->h_pos + k * obs::kReservoirSize);
+      } catch (...) {
+        ok = -1;
+      }
+      {
+        std::lock_guard<std::mutex> lk(mu_);
+        done_[k] = ok;
+      }
+      cv_.notify_all();
+    }
+  }
+
+  // The next site's values: x [n] fp32 on the device (gelu: GELU applied on
+  // the fly, for the per-token path whose fc1 output is stored pre-GELU).
+  int capture(esm_gfx950_ctx* ctx, const float* x, size_t n, int gelu) {
+    if (next_ >= sites_.size() || sites_[next_].n != n)
+      return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: site sequence mismatch");
+    const size_t k = next_++;
+    {
+      std::unique_lock<std::mutex> lk(mu_);
+      cv_.wait(lk, [&] { return done_[k] != 0; });
+    }
+    if (done_[k] < 0) return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: out of host memory");
+    const ObsSite& st = sites_[k];
+    const size_t off = k * obs::kReservoirSize;
+    if (st.count == 0) return ESM_GFX950_OK;
+    ESM_HIP(ctx, hipMemcpyAsync(obs_->d_pos + off, obs_->h_pos + off, st.count * 4, hipMemcpyHostToDevice,
+                                ctx->stream));
+    ESM_HIP(ctx, launch_observe_gather(x, obs_->d_pos + off, static_cast<int>(st.count), gelu, obs_->d_val + off,
+                                       ctx->stream));
+    return ESM_GFX950_OK;
+  }
+
+  // After the forward: gathered values into the reservoirs (synchronises).
+  int finish(esm_gfx950_ctx* ctx) {
+    join();
+    if (next_ != sites_.size()) return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: sites not captured");
+    ESM_HIP(ctx, hipMemcpyAsync(obs_->h_val, obs_->d_val, sites_.size() * obs::kReservoirSize * 4,
+                                hipMemcpyDeviceToHost, ctx->stream));
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (size_t k = 0; k < sites_.size(); ++k) {
+      const ObsSite& st = sites_[k];
+      const float* v = obs_->h_val + k * obs::kReservoirSize;
+      for (size_t w = 0; w < st.count; ++w) st.r->samples[st.slots[w]] = v[w];
+    }
+    return ESM_GFX950_OK;
+  }
+
+ private:
+  esm_gfx950_observer* obs_;
+  std::vector<ObsSite> sites_;
+  std::vector<int> done_;  // 0 pending, 1 planned, -1 failed
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::vector<std::thread> threads_;
+  size_t taken_ = 0;
+  size_t next_ = 0;
+};
+
 // One pre-LN encoder layer on the device (reference TransformerBlock,
 // src/model.cpp:932-1066): LN -> QKV -> Q-scale -> RoPE -> attention ->
 // out-proj -> residual -> LN -> fc1 -> GELU -> fc2 -> residual.
@@ -990,8 +1125,7 @@ P shift(P p, const char* from, const char* to) {
 // so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
 // fc2 output of the previous layer (null for the first layer).
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
-               const Meta& md,
-               int T, int nwork, const float* resid_in) {
+               const Meta& md, int T, int nwork, const float* resid_in, ObsRun* ob) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
   const int ldq_d = pad16(d), ldq_f = pad16(f);
@@ -1000,13 +1134,22 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
   int slot;
 
+  const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * f;
+
   // (residual) + attn LN + activation quant
   if (tok) {
     ESM_HIP(ctx, launch_layernorm_quant(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
                                         a.xs, s));
+    if (ob) {
+      // The fused kernel keeps the LN output in registers: recompute it
+      // (hidden already holds the residual sum) for the observer.
+      ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
+      ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+    }
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax, 1, 0.0f, s));
     ESM_HIP(ctx, launch_layernorm(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
+    if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
     ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax, a.xq, ldq_d, a.xs, s));
   }
 
@@ -1076,6 +1219,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_attention_mfma(a.qb, a.kb, a.vb, qk16, 0, d, md.cu, md.work, nwork, a.attn, d, amax_attn, s));
   }
   ESM_TRY(ctx->time_end(slot));
+  if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   if (tok) {
     ESM_HIP(ctx, launch_quant_rows(a.attn, 0, d, T, d, a.xq, ldq_d, a.xs, s));
   } else {
@@ -1100,14 +1244,25 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
   ESM_TRY(ctx->time_end(slot));
 
-  // residual + ffn LN + quant
+  // residual + ffn LN + quant. The observer sees the LN output before the
+  // first-block fp16 rounding (reference src/model.cpp:1023-1033).
   if (tok) {
     ESM_HIP(ctx, launch_layernorm_quant(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
                                         a.xs, s, round16));
+    if (ob) {
+      ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
+      ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+    }
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
     ESM_HIP(ctx, launch_layernorm(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
                                   s, round16));
+    if (ob && round16) {
+      ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
+      ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+    } else if (ob) {
+      ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+    }
     ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax + 2, a.xq, ldq_d, a.xs, s));
   }
 
@@ -1131,6 +1286,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_TRY(ctx->time_begin("fc1", &slot));
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
     ESM_TRY(ctx->time_end(slot));
+    if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 1));
     ESM_HIP(ctx, launch_gelu_quant_rows(a.inter, f, T, f, a.xq, ldq_f, a.xs, s));
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 3, 1, 0.0f, s));
@@ -1138,6 +1294,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_TRY(ctx->time_begin("fc1", &slot));
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Gelu, s));
     ESM_TRY(ctx->time_end(slot));
+    if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
     ESM_HIP(ctx, launch_quant_tensor(a.inter, f, T, f, a.absmax + 3, a.xq, ldq_f, a.xs, s));
   }
 
@@ -1178,20 +1335,30 @@ int f32_linear(esm_gfx950_ctx* ctx, const float* A, const DevLinear& W, float* C
 }
 
 int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
-              const Meta& md, int T, int nwork) {
+              const Meta& md, int T, int nwork, ObsRun* ob) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, H = c.num_heads, dh = c.head_dim;
   hipStream_t s = ctx->stream;
   const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
+  const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * c.intermediate_size;
   ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, nullptr, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
   ESM_TRY(f32_linear(ctx, a.ln, L.qkv, a.qkv, T, kF32Store));
   ESM_HIP(ctx, launch_rope_f32(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
   ESM_HIP(ctx, launch_rope_f32(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn, d, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   ESM_TRY(f32_linear(ctx, a.attn, L.out, a.hidden, T, kF32Resid));
   ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr, s,
                                 round16));
+  if (ob && round16) {
+    ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
+    ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+  } else if (ob) {
+    ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  }
   ESM_TRY(f32_linear(ctx, a.ln, L.fc1, a.inter, T, kF32Gelu));
+  if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
   ESM_TRY(f32_linear(ctx, a.inter, L.fc2, a.hidden, T, kF32Resid));
   return ESM_GFX950_OK;
 }
@@ -1284,7 +1451,8 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
 }
 
 // The whole forward of one part on ctx->stream; logits rows [0, T).
-int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx950_model::Part& P, float* logits) {
+int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx950_model::Part& P, float* logits,
+                 ObsRun* ob = nullptr) {
   const auto& c = m->cfg;
   const int T = P.T;
   const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
@@ -1299,10 +1467,10 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     const DevLayer& L = m->layers[li];
     const int round16 = (li == 0 && m->first_block_fc1_fp16) ? 1 : 0;
     if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending));
+      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending, ob));
       pending = a.ybuf;
     } else {
-      ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork));
+      ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));
     }
   }
   // (Last residual +) final LN and lm head: dense -> GELU -> LN -> tied
@@ -1345,9 +1513,11 @@ extern "C" int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model*
   return ESM_GFX950_OK;
 }
 
-extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
-                                       const int32_t* cu, int B, int T) {
-  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+namespace {
+
+// Validates and stages a packed batch in at most max_parts sequence groups.
+int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, const int32_t* cu, int B, int T,
+                int max_parts) {
   ESM_TRY(validate_batch(ctx, cu, B, T));
   m->staged_T = 0;
   for (auto& p : m->parts) p.T = p.B = 0;
@@ -1361,7 +1531,7 @@ extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m,
   // A per-tensor activation scale spans the whole batch, so that mode keeps
   // the batch in one part.
   const bool whole = m->cfg.weights_int8 && m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR;
-  const int np = whole ? 1 : std::min<int>(static_cast<int>(m->parts.size()), B);
+  const int np = whole ? 1 : std::min({static_cast<int>(m->parts.size()), B, max_parts});
   int b0 = 0;
   for (int p = 0; p < np; ++p) {
     int b1 = b0 + 1;
@@ -1373,6 +1543,14 @@ extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m,
   }
   m->staged_T = T;
   return ESM_GFX950_OK;
+}
+
+}  // namespace
+
+extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                       const int32_t* cu, int B, int T) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  return stage_batch(ctx, m, ids, cu, B, T, static_cast<int>(m->parts.size()));
 }
 
 extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* m, float* logits) {
@@ -1435,6 +1613,160 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   }
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
+}
+
+// ---------------------------------------------------------------- observer
+namespace {
+
+// Device and pinned staging for `nsites` sites' reservoir slots.
+int reserve_observer(esm_gfx950_ctx* ctx, esm_gfx950_observer* o, size_t nsites) {
+  if (nsites <= o->cap_sites) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (o->d_pos) hipFree(o->d_pos);
+  if (o->d_val) hipFree(o->d_val);
+  if (o->h_pos) hipHostFree(o->h_pos);
+  if (o->h_val) hipHostFree(o->h_val);
+  o->d_pos = o->h_pos = nullptr;
+  o->d_val = o->h_val = nullptr;
+  o->cap_sites = 0;
+  const size_t n = nsites * obs::kReservoirSize;
+  ESM_HIP(ctx, hipMalloc(&o->d_pos, n * 4));
+  ESM_HIP(ctx, hipMalloc(&o->d_val, n * 4));
+  ESM_HIP(ctx, hipHostMalloc(&o->h_pos, n * 4, hipHostMallocDefault));
+  ESM_HIP(ctx, hipHostMalloc(&o->h_val, n * 4, hipHostMallocDefault));
+  o->cap_sites = nsites;
+  return ESM_GFX950_OK;
+}
+
+void free_observer_buffers(esm_gfx950_observer* o) {
+  if (o->d_pos) hipFree(o->d_pos);
+  if (o->d_val) hipFree(o->d_val);
+  if (o->h_pos) hipHostFree(o->h_pos);
+  if (o->h_val) hipHostFree(o->h_val);
+  o->d_pos = o->h_pos = nullptr;
+  o->d_val = o->h_val = nullptr;
+  o->cap_sites = 0;
+}
+
+// Site keys in the order TransformerBlock observes them.
+constexpr const char* kObsSites[4] = {"attn_ln_output", "attn_out", "ffn_ln_output", "inter_gelu"};
+
+}  // namespace
+
+extern "C" int esm_gfx950_observer_create(esm_gfx950_ctx* ctx, esm_gfx950_observer** out) {
+  if (!ctx || !out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = new (std::nothrow) esm_gfx950_observer();
+  return *out ? ESM_GFX950_OK : ctx->fail(ESM_GFX950_INTERNAL, "observer_create: out of memory");
+}
+
+extern "C" int esm_gfx950_observer_free(esm_gfx950_ctx* ctx, esm_gfx950_observer* obs) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (!obs) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  free_observer_buffers(obs);
+  delete obs;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_observer_clear(esm_gfx950_observer* obs) {
+  if (!obs) return ESM_GFX950_INVALID_ARGUMENT;
+  obs->sites.clear();
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_observer_site_count(const esm_gfx950_observer* obs, size_t* count) {
+  if (!obs || !count) return ESM_GFX950_INVALID_ARGUMENT;
+  *count = obs->sites.size();
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_observer_site_name(const esm_gfx950_observer* obs, size_t i, const char** name) {
+  if (!obs || !name) return ESM_GFX950_INVALID_ARGUMENT;
+  if (i >= obs->sites.size()) return ESM_GFX950_OUT_OF_RANGE;
+  auto it = obs->sites.begin();
+  std::advance(it, static_cast<std::ptrdiff_t>(i));
+  *name = it->first.c_str();
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_observer_percentile(const esm_gfx950_observer* obs, const char* site, float pctile,
+                                              float* out) {
+  if (!obs || !site || !out || std::isnan(pctile)) return ESM_GFX950_INVALID_ARGUMENT;
+  auto it = obs->sites.find(site);
+  if (it == obs->sites.end()) return ESM_GFX950_NOT_FOUND;
+  try {
+    *out = obs::percentile(it->second, pctile);
+  } catch (const std::exception&) {
+    return ESM_GFX950_INTERNAL;
+  }
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_observer_observe(esm_gfx950_ctx* ctx, esm_gfx950_observer* obs, const char* site,
+                                           const float* values, size_t n) {
+  if (!ctx || !obs) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, site, "observer_observe: null site key");
+  if (n == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, values, "observer_observe: null values");
+  if (n >= UINT32_MAX) return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "observer_observe: more than 2^32 - 2 values");
+  ESM_TRY(reserve_observer(ctx, obs, 1));
+  size_t count = 0;
+  std::vector<uint32_t> slots;
+  obs::Reservoir* r = nullptr;
+  try {
+    r = &obs->sites[site];
+    slots.resize(obs::kReservoirSize);
+    count = obs::plan(*r, n, slots.data(), obs->h_pos);
+  } catch (const std::exception& e) {
+    return ctx->fail(ESM_GFX950_INTERNAL, std::string("observer_observe: ") + e.what());
+  }
+  if (count == 0) return ESM_GFX950_OK;
+  ESM_HIP(ctx, hipMemcpyAsync(obs->d_pos, obs->h_pos, count * 4, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, launch_observe_gather(values, obs->d_pos, static_cast<int>(count), 0, obs->d_val, ctx->stream));
+  ESM_HIP(ctx, hipMemcpyAsync(obs->h_val, obs->d_val, count * 4, hipMemcpyDeviceToHost, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (size_t w = 0; w < count; ++w) r->samples[slots[w]] = obs->h_val[w];
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                                const int32_t* cu, int B, int T, float* logits,
+                                                esm_gfx950_observer* obs) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, obs, "forward_with_observer: null observer");
+  // The observer sees each site's values in packed row order, so the batch
+  // is staged as one sequence group.
+  ESM_TRY(stage_batch(ctx, m, ids, cu, B, T, 1));
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, logits, "forward_with_observer: null logits");
+  const auto& c = m->cfg;
+  const size_t Td = static_cast<size_t>(T) * c.hidden_size, Tf = static_cast<size_t>(T) * c.intermediate_size;
+  if (Tf >= UINT32_MAX) return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_with_observer: batch too large");
+  const size_t nsites = 4 * m->layers.size();
+  ESM_TRY(reserve_observer(ctx, obs, nsites));
+  std::vector<ObsSite> sites(nsites);
+  try {
+    for (size_t l = 0; l < m->layers.size(); ++l)
+      for (int k = 0; k < 4; ++k) {
+        ObsSite& st = sites[4 * l + k];
+        st.r = &obs->sites["layer" + std::to_string(l) + "." + kObsSites[k]];
+        st.n = k == 3 ? Tf : Td;
+      }
+  } catch (const std::exception& e) {
+    return ctx->fail(ESM_GFX950_INTERNAL, std::string("forward_with_observer: ") + e.what());
+  }
+  esm_gfx950_model::Part& P = m->parts[0];
+  if (P.stream) {
+    ESM_HIP(ctx, hipEventRecord(P.done, ctx->stream));
+    ESM_HIP(ctx, hipStreamWaitEvent(P.stream, P.done, 0));
+  }
+  StreamScope scope(ctx, P.stream);
+  ObsRun run(obs, std::move(sites));
+  const Arena a = layout(c, P.cap_T, static_cast<char*>(P.arena));
+  ESM_TRY(forward_part(ctx, m, P, a.logits, &run));
+  ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * c.vocab_size * 4, hipMemcpyDeviceToHost,
+                              ctx->stream));
+  return run.finish(ctx);
 }
 
 // ---------------------------------------------------------------- scheduler

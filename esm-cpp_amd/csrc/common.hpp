@@ -77,25 +77,25 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return x * 0.5f * (1.0f + erff(x * 0.70710678118654752440f));
 }
 
-// GELU with erf from Abramowitz & Stegun, Handbook of Mathematical
+// Twice GELU, with erf from Abramowitz & Stegun, Handbook of Mathematical
 // Functions, eq. 7.1.26 (|error of erf| <= 1.5e-7 for every x): erf(u) =
-// 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-u^2), t = 1/(1 + p|u|),
-// odd in u. The reference's AVX-512 GELU uses the same approximation
-// (reference src/kernels/gelu.cpp:69-94); exp(-u^2) here is the hardware
-// base-2 exponential, which returns 0 (not NaN) for large |u|.
-__device__ __forceinline__ float gelu_as(float x) {
-  const float u = x * 0.70710678118654752440f;
-  const float au = fabsf(u);
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, au, 1.0f));
+// 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-u^2), t = 1/(1 + p|u|).
+// The reference's AVX-512 GELU uses the same approximation (reference
+// src/kernels/gelu.cpp:69-94). erf is odd, so 2 gelu(x) = x (1 + erf(x/√2))
+// = x + |x| erf(|x|/√2); the 1/√2 is folded into p and the exponent, and the
+// final 1/2 is left to the caller (an exact power-of-two scaling). exp(-u^2)
+// is the hardware base-2 exponential, which returns 0 (not NaN) for large |u|.
+__device__ __forceinline__ float gelu2_as(float x) {
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.70710678118654752440f, ax, 1.0f));
   float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
   poly = __builtin_fmaf(poly, t, 1.421413741f);
   poly = __builtin_fmaf(poly, t, -0.284496736f);
   poly = __builtin_fmaf(poly, t, 0.254829592f);
   poly *= t;
-  const float e = __builtin_amdgcn_exp2f(-au * au * 1.44269504088896340736f);
+  const float e = __builtin_amdgcn_exp2f((x * x) * (-0.5f * 1.44269504088896340736f));
   const float erf_abs = __builtin_fmaf(-poly, e, 1.0f);
-  const float erf_u = u < 0.0f ? -erf_abs : erf_abs;
-  return x * 0.5f * (1.0f + erf_u);
+  return __builtin_fmaf(ax, erf_abs, x);
 }
 
 // Symmetric int8 quantisation of one value with a precomputed reciprocal
@@ -104,6 +104,23 @@ __device__ __forceinline__ int quant_i8(float x, float inv) {
   float r = __builtin_rintf(x * inv);
   r = fminf(fmaxf(r, -127.0f), 127.0f);
   return static_cast<int>(r);
+}
+
+// Four values quantised exactly as quant_i8 does, packed little-endian into
+// one word. For |r| <= 127, r + 1.5*2^23 lies in [2^23, 2^24), where the
+// float spacing is 1, so the addition rounds r to the nearest integer with
+// ties to even and the low byte of the sum's bits is that integer in two's
+// complement (checked against rint + clamp for every float in [-200, 200]).
+__device__ __forceinline__ uint32_t quant_pack4(float4 v, float inv) {
+  constexpr float kMagic = 12582912.0f;
+  const uint32_t a = __float_as_uint(__builtin_amdgcn_fmed3f(v.x * inv, -127.0f, 127.0f) + kMagic);
+  const uint32_t b = __float_as_uint(__builtin_amdgcn_fmed3f(v.y * inv, -127.0f, 127.0f) + kMagic);
+  const uint32_t c = __float_as_uint(__builtin_amdgcn_fmed3f(v.z * inv, -127.0f, 127.0f) + kMagic);
+  const uint32_t d = __float_as_uint(__builtin_amdgcn_fmed3f(v.w * inv, -127.0f, 127.0f) + kMagic);
+  // v_perm_b32 byte k of the result = byte sel[k] of {src0 (bytes 4-7), src1 (bytes 0-3)}.
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a.b0, b.b0
+  const uint32_t hi = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);  // c.b0, d.b0
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 }  // namespace esm_gfx950

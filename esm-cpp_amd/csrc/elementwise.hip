@@ -124,11 +124,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     for (int j = 0; j < NV; ++j) {
       const int c = (j * 64 + lane) * 4;
       if (c < d) {
-        const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
-        const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
-        const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
-        const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
-        *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
       }
     }
     for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
@@ -224,11 +220,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
     if (c < cols) {
-      const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
-      const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
-      const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
-      const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
-      *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+      *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
     }
   }
   for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
@@ -237,8 +229,11 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
 
 // GELU fused with per-row quantisation (cols % 4 == 0, cols <= NV*256): the
 // fc1 output row is read once, GELU'd in registers, its absmax taken, and it
-// is written as int8 with the row's scale.
-template <int NV>
+// is written as int8 with the row's scale. The registers hold 2 gelu(x)
+// (gelu2_as); halving the absmax and the reciprocal scale are exact, so the
+// bytes and the scale are those of quantising gelu(x) itself. FULL: cols ==
+// NV*256, no column masking.
+template <int NV, bool FULL>
 __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
     const float* __restrict__ x, int ldx, int rows, int cols,
     int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
@@ -247,30 +242,28 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
   if (row >= rows) return;
   const float* xr = x + static_cast<size_t>(row) * ldx;
   float4 v[NV];
-  load_row_vec<NV>(xr, cols, lane, v);
+  if constexpr (FULL) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4*>(xr + (j * 64 + lane) * 4);
+  } else {
+    load_row_vec<NV>(xr, cols, lane, v);  // gelu(0) == 0: zeroed chunks stay zero
+  }
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    // gelu(0) == 0, so zeroed chunks past `cols` stay zero.
-    v[j].x = gelu_as(v[j].x);
-    v[j].y = gelu_as(v[j].y);
-    v[j].z = gelu_as(v[j].z);
-    v[j].w = gelu_as(v[j].w);
+    v[j].x = gelu2_as(v[j].x);
+    v[j].y = gelu2_as(v[j].y);
+    v[j].z = gelu2_as(v[j].z);
+    v[j].w = gelu2_as(v[j].w);
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
   }
-  const float scale = act_scale_from_absmax(wave_max(amax));
-  const float inv = 1.0f / scale;
+  const float scale = act_scale_from_absmax(0.5f * wave_max(amax));
+  const float inv = 0.5f * (1.0f / scale);
   int8_t* qr = q + static_cast<size_t>(row) * ldq;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
-    if (c < cols) {
-      const uint32_t b0 = static_cast<uint8_t>(quant_i8(v[j].x, inv));
-      const uint32_t b1 = static_cast<uint8_t>(quant_i8(v[j].y, inv));
-      const uint32_t b2 = static_cast<uint8_t>(quant_i8(v[j].z, inv));
-      const uint32_t b3 = static_cast<uint8_t>(quant_i8(v[j].w, inv));
-      *reinterpret_cast<uint32_t*>(qr + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-    }
+    if (FULL || c < cols) *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
   }
   for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
   if (lane == 0) scales[row] = scale;
@@ -307,6 +300,15 @@ __global__ void fill_kernel(float* x, size_t n, float v) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
     x[i] = v;
+}
+
+__global__ void observe_gather_kernel(const float* __restrict__ x, const uint32_t* __restrict__ pos, int count,
+                                      int gelu, float* __restrict__ out) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= count) return;
+  float v = x[pos[w]];
+  if (gelu) v = 0.5f * gelu2_as(v);
+  out[w] = fabsf(v);
 }
 
 __global__ void gelu_kernel(const float* __restrict__ x, float* __restrict__ out, size_t n) {
@@ -419,12 +421,14 @@ hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols, i
   if (rows <= 0) return hipSuccess;
   if (cols % 4 != 0 || ldx % 4 != 0 || cols > 10240) return hipErrorInvalidValue;
   const dim3 g = rows_grid(rows), b(256);
-  if (cols <= 1280) {
-    hipLaunchKernelGGL(gelu_quant_rows_kernel<5>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  if (cols == 5120) {  // ESM-2 650M's d_ff
+    hipLaunchKernelGGL((gelu_quant_rows_kernel<20, true>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+  } else if (cols <= 1280) {
+    hipLaunchKernelGGL((gelu_quant_rows_kernel<5, false>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   } else if (cols <= 5120) {
-    hipLaunchKernelGGL(gelu_quant_rows_kernel<20>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+    hipLaunchKernelGGL((gelu_quant_rows_kernel<20, false>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   } else {
-    hipLaunchKernelGGL(gelu_quant_rows_kernel<40>, g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+    hipLaunchKernelGGL((gelu_quant_rows_kernel<40, false>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   }
   return hipGetLastError();
 }
@@ -462,6 +466,13 @@ hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s)
   size_t g = (n + 255) / 256;
   if (g > 4096) g = 4096;
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_observe_gather(const float* x, const uint32_t* pos, int count, int gelu, float* out,
+                                 hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  hipLaunchKernelGGL(observe_gather_kernel, dim3((count + 255) / 256), dim3(256), 0, s, x, pos, count, gelu, out);
   return hipGetLastError();
 }
 

@@ -148,6 +148,10 @@ hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols,
 hipError_t launch_absmax(const float* x, size_t n, float* absmax,
                          hipStream_t s);
 hipError_t launch_fill_f32(float* x, size_t n, float v, hipStream_t s);
+// Activation observer gather: out[w] = |x[pos[w]]| (gelu != 0: |GELU(x[pos[w]])|
+// with the Abramowitz & Stegun erf of the fused GELU + quantisation kernel).
+hipError_t launch_observe_gather(const float* x, const uint32_t* pos, int count, int gelu, float* out,
+                                 hipStream_t s);
 hipError_t launch_gelu(const float* x, float* out, size_t n, hipStream_t s);
 hipError_t launch_residual_add(float* y, const float* x, size_t n,
                                hipStream_t s);

@@ -18,6 +18,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libesm_gfx950.so")
 
 OK = 0
+# esm::StatusCode values (status codes of include/esm_gfx950.h)
+INVALID_ARGUMENT, OUT_OF_RANGE, NOT_FOUND, IO_ERROR, SHAPE_MISMATCH, INTERNAL, HIP_ERROR = 1, 2, 3, 4, 5, 6, 7
 ACT_PER_TENSOR = 0
 ACT_PER_TOKEN = 1
 ATTN_FP32 = 0
@@ -35,6 +37,7 @@ EXPORTED = [
     "esm_gfx950_memcpy_d2h", "esm_gfx950_memcpy_d2d", "esm_gfx950_timer_start", "esm_gfx950_timer_stop",
     "esm_gfx950_kernel_timing", "esm_gfx950_kernel_timing_query", "esm_gfx950_weight_upload_i8",
     "esm_gfx950_weight_free", "esm_gfx950_gemm_i8_i32", "esm_gfx950_linear_i8_q", "esm_gfx950_quantize_act",
+    "esm_gfx950_gelu_quantize_act",
     "esm_gfx950_linear_i8", "esm_gfx950_linear_f32", "esm_gfx950_layernorm", "esm_gfx950_gelu",
     "esm_gfx950_residual_add", "esm_gfx950_scale", "esm_gfx950_rope_build_tables",
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
@@ -42,7 +45,9 @@ EXPORTED = [
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
     "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_plan_batches",
     "esm_gfx950_forward_scheduled", "esm_gfx950_model_create_from_gguf",
-    "esm_gfx950_model_set_first_block_fc1_fp16",
+    "esm_gfx950_model_set_first_block_fc1_fp16", "esm_gfx950_observer_create", "esm_gfx950_observer_free",
+    "esm_gfx950_observer_clear", "esm_gfx950_observer_observe", "esm_gfx950_observer_site_count",
+    "esm_gfx950_observer_site_name", "esm_gfx950_observer_percentile", "esm_gfx950_forward_with_observer",
 ]
 
 
@@ -84,6 +89,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_gemm_i8_i32": (i32, [vp, vp, i32, vp, i32, vp]),
         "esm_gfx950_linear_i8_q": (i32, [vp, vp, i32, vp, vp, vp, vp, i32, i32]),
         "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
+        "esm_gfx950_gelu_quantize_act": (i32, [vp, vp, i32, i32, vp, i32, vp]),
         "esm_gfx950_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
         "esm_gfx950_linear_f32": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
         "esm_gfx950_layernorm": (i32, [vp, vp, vp, vp, f32, vp, i32, i32]),
@@ -106,6 +112,14 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
         "esm_gfx950_model_create_from_gguf": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(vp)]),
         "esm_gfx950_model_set_first_block_fc1_fp16": (i32, [vp, vp, i32]),
+        "esm_gfx950_observer_create": (i32, [vp, C.POINTER(vp)]),
+        "esm_gfx950_observer_free": (i32, [vp, vp]),
+        "esm_gfx950_observer_clear": (i32, [vp]),
+        "esm_gfx950_observer_observe": (i32, [vp, vp, C.c_char_p, vp, sz]),
+        "esm_gfx950_observer_site_count": (i32, [vp, C.POINTER(sz)]),
+        "esm_gfx950_observer_site_name": (i32, [vp, sz, C.POINTER(C.c_char_p)]),
+        "esm_gfx950_observer_percentile": (i32, [vp, C.c_char_p, f32, C.POINTER(f32)]),
+        "esm_gfx950_forward_with_observer": (i32, [vp, vp, vp, vp, i32, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -267,6 +281,10 @@ class Device:
     def quantize_act(self, x: DeviceArray, M: int, K: int, mode: int, q: DeviceArray, ldq: int, scales: DeviceArray):
         self._check(self.lib.esm_gfx950_quantize_act(self.ctx, x.ptr, M, K, mode, q.ptr, ldq, scales.ptr))
 
+    def gelu_quantize_act(self, x: DeviceArray, M: int, K: int, q: DeviceArray, ldq: int, scales: DeviceArray):
+        """GELU then per-token int8 quantisation, fused (fc2's input in the INT8 FFN)."""
+        self._check(self.lib.esm_gfx950_gelu_quantize_act(self.ctx, x.ptr, M, K, q.ptr, ldq, scales.ptr))
+
     def linear_i8(self, A: DeviceArray, W: Weight, bias: Optional[DeviceArray], C_out: DeviceArray, M: int, N: int,
                   K: int, mode: int):
         self._check(self.lib.esm_gfx950_linear_i8(self.ctx, A.ptr, W.handle, bias.ptr if bias is not None else None,
@@ -305,6 +323,60 @@ class Device:
 
 
 # ------------------------------------------------------------------ model
+class ActivationObserver:
+    """esm::ActivationObserver on the device (reference include/esm_cpp/observer.h:13-47):
+    per-site reservoirs of |values| kept by Algorithm R with the reference's
+    generator; observe() takes device values."""
+
+    RESERVOIR_SIZE = 65536
+
+    def __init__(self, dev: Device):
+        self.dev = dev
+        h = C.c_void_p()
+        dev._check(dev.lib.esm_gfx950_observer_create(dev.ctx, C.byref(h)))
+        self.handle = h
+
+    def observe(self, site: str, values: DeviceArray, n: Optional[int] = None):
+        n = int(np.prod(values.shape, dtype=np.int64)) if n is None else int(n)
+        self.dev._check(self.dev.lib.esm_gfx950_observer_observe(self.dev.ctx, self.handle, site.encode(),
+                                                                 values.ptr, n))
+
+    def sites(self):
+        lib = self.dev.lib
+        n = C.c_size_t()
+        self.dev._check(lib.esm_gfx950_observer_site_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            name = C.c_char_p()
+            self.dev._check(lib.esm_gfx950_observer_site_name(self.handle, i, C.byref(name)))
+            out.append(name.value.decode())
+        return out
+
+    def percentile(self, pctile: float):
+        """{site: pctile-th percentile} (ActivationObserver::Percentile)."""
+        out = {}
+        v = C.c_float()
+        for site in self.sites():
+            self.dev._check(self.dev.lib.esm_gfx950_observer_percentile(self.handle, site.encode(), float(pctile),
+                                                                        C.byref(v)))
+            out[site] = v.value
+        return out
+
+    def clear(self):
+        self.dev._check(self.dev.lib.esm_gfx950_observer_clear(self.handle))
+
+    def free(self):
+        if self.handle:
+            self.dev.lib.esm_gfx950_observer_free(self.dev.ctx, self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class _ModelConfig(C.Structure):
     _fields_ = [("num_layers", C.c_int), ("hidden_size", C.c_int), ("num_heads", C.c_int), ("head_dim", C.c_int),
                 ("intermediate_size", C.c_int), ("vocab_size", C.c_int), ("layer_norm_eps", C.c_float),
@@ -423,6 +495,22 @@ class Model:
         self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
                                                                len(cu) - 1, T, out.ptr, 1))
         return out
+
+    def forward_packed_with_observer(self, ids: np.ndarray, cu: np.ndarray, observer: "ActivationObserver"):
+        """Packed forward that also feeds `observer` at the reference's four
+        per-layer sites (esm_gfx950_forward_with_observer); host logits [T, vocab]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        cu = np.ascontiguousarray(cu, np.int32)
+        T = int(ids.shape[0])
+        logits = np.empty((T, self.cfg.vocab_size), np.float32)
+        self.dev._check(self.dev.lib.esm_gfx950_forward_with_observer(
+            self.dev.ctx, self.handle, _ptr(ids), _ptr(cu), len(cu) - 1, T, _ptr(logits), observer.handle))
+        return logits
+
+    def forward_with_observer(self, ids: np.ndarray, observer: "ActivationObserver"):
+        """One sequence (reference Model::ForwardWithObserver, src/model.cpp:1084-1091)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        return self.forward_packed_with_observer(ids, np.array([0, ids.shape[0]], np.int32), observer)
 
     def forward_scheduled(self, ids_list, max_batch_size: int = 256, imbalance_threshold: float = 1.2):
         """Scheduled forward over a list of id arrays (esm_gfx950_forward_scheduled);

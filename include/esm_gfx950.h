@@ -77,6 +77,7 @@ enum {
 typedef struct esm_gfx950_ctx esm_gfx950_ctx;
 typedef struct esm_gfx950_weight esm_gfx950_weight;
 typedef struct esm_gfx950_model esm_gfx950_model;
+typedef struct esm_gfx950_observer esm_gfx950_observer;
 
 /* ---------------------------------------------------------------- context
  * Device selection replaces the ISA probe (reference
@@ -143,6 +144,15 @@ int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const 
  * SymmetricRef (src/quant/pack.cpp:134-147). */
 int esm_gfx950_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int K, int mode, int8_t* q,
                             int ldq, float* scales);
+
+/* The fc1 -> fc2 activation step of the INT8 FFN: kernels::Gelu
+ * (include/esm_cpp/kernels.h:35, called at src/model.cpp:1044-1045, the
+ * AVX-512 erf approximation of src/kernels/gelu.cpp:69-94) followed by the
+ * per-token activation quantisation fc2's LinearInt8 applies to its input,
+ * fused: x fp32 [M, K] -> q int8 [M, ldq] (zero padded past K) and scales
+ * fp32 [M]. K % 4 == 0, K <= 10240. */
+int esm_gfx950_gelu_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int K, int8_t* q, int ldq,
+                                 float* scales);
 
 /* esm::kernels::LinearInt8 (include/esm_cpp/kernels.h:56-57,
  * dispatch.cpp:80-103): fp32 A [M, K] -> activation quant (mode) -> INT8
@@ -308,6 +318,45 @@ int esm_gfx950_plan_batches(const int32_t* lengths, int n, float imbalance_thres
 int esm_gfx950_forward_scheduled(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* const* ids,
                                  const int32_t* lengths, int n, float imbalance_threshold, int max_batch_size,
                                  float* const* logits);
+/* ------------------------------------------------------ activation observer
+ * esm::ActivationObserver (reference include/esm_cpp/observer.h:13-47,
+ * src/quant/observer.cpp:8-51) for static-quantisation calibration on the
+ * device: per site key, a reservoir of at most 65536 |values| kept by
+ * Algorithm R with the reference's generator (std::mt19937 seeded 0xc1b1ce
+ * per site, std::uniform_int_distribution over [0, total_seen]), so that the
+ * same sequence of calls keeps the same positions. The host draws which
+ * positions survive; only those values are gathered from the device. Not
+ * thread-safe (one call at a time, like the reference). After a failed call
+ * the observer's contents are unspecified: clear it. */
+int esm_gfx950_observer_create(esm_gfx950_ctx* ctx, esm_gfx950_observer** out);
+int esm_gfx950_observer_free(esm_gfx950_ctx* ctx, esm_gfx950_observer* obs);
+/* ActivationObserver::Clear (observer.cpp:51): every site removed. */
+int esm_gfx950_observer_clear(esm_gfx950_observer* obs);
+/* ActivationObserver::Observe (observer.cpp:8-30): feeds |values[0, n)| (fp32,
+ * DEVICE memory, n < 2^32 - 1) into site's reservoir; n == 0 is a no-op that
+ * creates no site. Returns after the reservoir is updated. */
+int esm_gfx950_observer_observe(esm_gfx950_ctx* ctx, esm_gfx950_observer* obs, const char* site,
+                                const float* values, size_t n);
+/* The sites observed so far, in byte order of their keys. The name pointer
+ * stays valid until the observer is cleared or freed. */
+int esm_gfx950_observer_site_count(const esm_gfx950_observer* obs, size_t* count);
+int esm_gfx950_observer_site_name(const esm_gfx950_observer* obs, size_t i, const char** name);
+/* ActivationObserver::Percentile (observer.cpp:32-49) for one site: the
+ * sample at floor(clamp(pctile / 100, 0, 1) * (size - 1)) of the sorted
+ * reservoir (float arithmetic as the reference). NOT_FOUND for an unknown
+ * site; NaN pctile is INVALID_ARGUMENT. */
+int esm_gfx950_observer_percentile(const esm_gfx950_observer* obs, const char* site, float pctile, float* out);
+/* Model::ForwardPackedInto with an observer (reference src/model.cpp:1093-1255;
+ * Model::ForwardWithObserver :1084-1091 is the B = 1 case): the packed
+ * forward of esm_gfx950_forward_packed (HOST ids, cu, logits [T, vocab]) that
+ * also observes, per layer i, "layer{i}.attn_ln_output", "layer{i}.attn_out",
+ * "layer{i}.ffn_ln_output" (before the first-block fp16 rounding) and
+ * "layer{i}.inter_gelu" over the batch's [T, d] / [T, ffn] values in packed
+ * row order (model.cpp:952-955,996-999,1023-1026,1047-1050). The batch runs as
+ * one sequence group. T == 0 observes nothing. */
+int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                                     const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
+                                     esm_gfx950_observer* obs);
 /* Bytes currently held by the model's device arena (for zero-growth checks). */
 int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
 

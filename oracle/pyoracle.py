@@ -249,6 +249,13 @@ class RefLib:
             "esmref_model_create": (vp, [C.POINTER(_OrModel)]),
             "esmref_model_free": (None, [vp]),
             "esmref_forward_packed": (i32, [vp, vp, vp, i32, i32, vp]),
+            "esmref_forward_packed_observed": (i32, [vp, vp, vp, i32, i32, vp, vp]),
+            "esmref_observer_new": (vp, []),
+            "esmref_observer_free": (None, [vp]),
+            "esmref_observer_clear": (None, [vp]),
+            "esmref_observer_observe": (None, [vp, C.c_char_p, vp, sz]),
+            "esmref_observer_percentile": (i32, [vp, C.c_char_p, f32, C.POINTER(f32)]),
+            "esmref_observer_site_count": (i32, [vp]),
             "esmref_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
             "esmref_gguf_save_model": (i32, [vp, C.c_char_p]),
             "esmref_gguf_tensor": (i32, [C.c_char_p, C.c_char_p, vp, sz, C.POINTER(C.c_uint32),
@@ -264,6 +271,9 @@ class RefLib:
 
     def isa(self) -> str:
         return self.lib.esmref_isa().decode()
+
+    def observer(self) -> "RefObserver":
+        return RefObserver(self)
 
     def gguf_tensor(self, path: str, name: str, cap: int = 1 << 30):
         """(type, dims, raw bytes) of one tensor through the reference's GGUF
@@ -400,14 +410,54 @@ class RefModel:
         if self.ref.lib.esmref_gguf_save_model(self.handle, os.fsencode(path)) != 0:
             raise ValueError("reference GGUF writer failed")
 
-    def forward_packed(self, batch):
+    def forward_packed(self, batch, observer: Optional["RefObserver"] = None):
+        """Logits [T, vocab]; with an observer, also feeds the reference's
+        ActivationObserver at TransformerBlock's four sites."""
         T = batch.total_tokens
         logits = np.empty((T, self.cfg.vocab_size), np.float32)
-        self.ref.lib.esmref_forward_packed(self.handle, _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
-                                           len(batch.cu) - 1, T, _p(logits))
+        self.ref.lib.esmref_forward_packed_observed(self.handle, _p(_c(batch.ids, np.int32)),
+                                                    _p(_c(batch.cu, np.int32)), len(batch.cu) - 1, T, _p(logits),
+                                                    observer.handle if observer is not None else None)
         return logits
 
     def free(self):
         if self.handle:
             self.ref.lib.esmref_model_free(self.handle)
+            self.handle = None
+
+
+class RefObserver:
+    """The reference's esm::ActivationObserver (oracle/_ref)."""
+
+    def __init__(self, ref: RefLib):
+        self.ref = ref
+        self.handle = ref.lib.esmref_observer_new()
+        self.keys = set()
+
+    def observe(self, site: str, values):
+        v = _c(np.asarray(values, np.float32).ravel(), np.float32)
+        self.ref.lib.esmref_observer_observe(self.handle, site.encode(), _p(v), v.size)
+        if v.size:
+            self.keys.add(site)
+
+    def percentile(self, pctile: float, sites=None):
+        """{site: value} for the given sites (default: every site observed
+        through observe()); sites the reference does not hold are left out."""
+        out = {}
+        v = C.c_float()
+        for key in (self.keys if sites is None else sites):
+            if self.ref.lib.esmref_observer_percentile(self.handle, key.encode(), float(pctile), C.byref(v)):
+                out[key] = v.value
+        return out
+
+    def site_count(self) -> int:
+        return int(self.ref.lib.esmref_observer_site_count(self.handle))
+
+    def clear(self):
+        self.ref.lib.esmref_observer_clear(self.handle)
+        self.keys.clear()
+
+    def free(self):
+        if self.handle:
+            self.ref.lib.esmref_observer_free(self.handle)
             self.handle = None

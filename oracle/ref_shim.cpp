@@ -28,6 +28,7 @@
 #include "esm_cpp/cpu_features.h"
 #include "esm_cpp/io.h"
 #include "esm_cpp/kernels.h"
+#include "esm_cpp/observer.h"
 #include "esm_cpp/quant.h"
 #include "esm_cpp/scheduler.h"
 #include "oracle.h"
@@ -196,8 +197,12 @@ void* esmref_model_create(const or_model* m) {
 
 void esmref_model_free(void* h) { delete static_cast<RefModel*>(h); }
 
-// Restated ForwardPackedInto over the reference facade. Returns 0.
-int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B, int T, float* logits) {
+// Restated ForwardPackedInto over the reference facade, with the reference's
+// own ActivationObserver (null: none) fed at TransformerBlock's four sites
+// (src/model.cpp:952-955,996-999,1023-1026,1047-1050). Returns 0.
+int esmref_forward_packed_observed(void* h, const int32_t* ids, const int32_t* cu, int B, int T, float* logits,
+                                   void* observer) {
+  auto* obs = static_cast<esm::ActivationObserver*>(observer);
   auto* r = static_cast<RefModel*>(h);
   const or_model& c = r->cfg;
   const int d = c.hidden, H = c.heads, dh = c.head_dim, f = c.ffn, V = c.vocab;
@@ -229,11 +234,14 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
       esm::kernels::Linear(A, L.w32[j].data(), L.bias[j].data(), C, M, L.N[j], L.K[j]);
     }
   };
+  int li = 0;
   for (const RefLayer& L : r->layers) {
+    const std::string site = "layer" + std::to_string(li++) + ".";
     float* q = qkv.data();
     float* k = qkv.data() + Td;
     float* v = qkv.data() + 2 * Td;
     esm::kernels::LayerNorm(hidden.data(), L.ln1_w.data(), L.ln1_b.data(), c.eps, ln.data(), T, d);
+    if (obs) obs->Observe(site + "attn_ln_output", ln.data(), Td);
     linear(L, 0, ln.data(), q, T);
     linear(L, 1, ln.data(), k, T);
     linear(L, 2, ln.data(), v, T);
@@ -243,12 +251,15 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
     esm::kernels::RopeApplyVarlen(q, cs.data(), sn.data(), cu, B, H, dh);
     esm::kernels::RopeApplyVarlen(k, cs.data(), sn.data(), cu, B, H, dh);
     esm::kernels::AttentionVarlen(q, k, v, cu, B, H, dh, attn.data());
+    if (obs) obs->Observe(site + "attn_out", attn.data(), Td);
     linear(L, 3, attn.data(), proj.data(), T);
     esm::kernels::ResidualAddInplace(hidden.data(), proj.data(), Td);
     esm::kernels::LayerNorm(hidden.data(), L.ln2_w.data(), L.ln2_b.data(), c.eps, ln.data(), T, d);
+    if (obs) obs->Observe(site + "ffn_ln_output", ln.data(), Td);
     if (c.fc1_fp16 && &L == &r->layers.front()) or_round_fp16_shim(ln.data(), ln.size());
     linear(L, 4, ln.data(), inter.data(), T);
     esm::kernels::Gelu(inter.data(), inter_g.data(), Tf);
+    if (obs) obs->Observe(site + "inter_gelu", inter_g.data(), Tf);
     linear(L, 5, inter_g.data(), proj.data(), T);
     esm::kernels::ResidualAddInplace(hidden.data(), proj.data(), Td);
   }
@@ -258,6 +269,30 @@ int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B,
   esm::kernels::LayerNorm(attn.data(), r->lm_ln_w.data(), r->lm_ln_b.data(), c.eps, ln.data(), T, d);
   esm::kernels::Linear(ln.data(), r->embed.data(), r->dec_b.data(), logits, T, V, d);
   return 0;
+}
+
+int esmref_forward_packed(void* h, const int32_t* ids, const int32_t* cu, int B, int T, float* logits) {
+  return esmref_forward_packed_observed(h, ids, cu, B, T, logits, nullptr);
+}
+
+// The reference's ActivationObserver (src/quant/observer.cpp) behind C
+// linkage.
+void* esmref_observer_new() { return new esm::ActivationObserver(); }
+void esmref_observer_free(void* h) { delete static_cast<esm::ActivationObserver*>(h); }
+void esmref_observer_clear(void* h) { static_cast<esm::ActivationObserver*>(h)->Clear(); }
+void esmref_observer_observe(void* h, const char* key, const float* values, size_t n) {
+  static_cast<esm::ActivationObserver*>(h)->Observe(key, values, n);
+}
+// Percentile of one site: 1 and *out when the site exists, else 0.
+int esmref_observer_percentile(void* h, const char* key, float pctile, float* out) {
+  const auto all = static_cast<esm::ActivationObserver*>(h)->Percentile(pctile);
+  auto it = all.find(key);
+  if (it == all.end()) return 0;
+  *out = it->second;
+  return 1;
+}
+int esmref_observer_site_count(void* h) {
+  return static_cast<int>(static_cast<esm::ActivationObserver*>(h)->Percentile(50.0f).size());
 }
 
 // Model::SaveToGguf (src/model.cpp:562-700) restated over a RefModel: the

@@ -124,19 +124,56 @@ def test_linear_int8_zero_sizes(dev):
     w.free()
 
 
+@pytest.mark.parametrize("M,K,ldq", [(333, 1280, 1280), (70, 5120, 5136), (41, 260, 272), (9, 5121, 5136)])
 @pytest.mark.parametrize("mode", [eg.ACT_PER_TENSOR, eg.ACT_PER_TOKEN])
-def test_quantize_act(dev, oracle, mode):
-    r = rng(5 + mode)
-    M, K = 333, 1280
+def test_quantize_act(dev, oracle, mode, M, K, ldq):
+    r = rng(5 + mode + K)
     x = (r.standard_normal((M, K)) * r.uniform(0.1, 10, size=(M, 1))).astype(np.float32)
     x[7] = 0.0  # all-zero row: per-token scale 1
-    ldq = K
-    dx, dq, ds = dev.array(x), dev.empty((M, ldq), np.int8), dev.empty((M,), np.float32)
+    # exact ties of x * (127 / absmax) land on both rounding directions
+    x[3, :6] = [127.0, 0.5, -0.5, 1.5, -2.5, 126.5]
+    dx, dq, ds = dev.array(x), dev.array(np.full((M, ldq), 99, np.int8)), dev.empty((M,), np.float32)
     dev.quantize_act(dx, M, K, mode, dq, ldq, ds)
     if mode == eg.ACT_PER_TENSOR:
         q, s = oracle.quant_act_tensor(x)
         s = np.full(M, s, np.float32)
     else:
         q, s = oracle.quant_act_rows(x)
-    assert np.array_equal(dq.numpy(), q)
+    got = dq.numpy()
+    assert np.array_equal(got[:, :K], q)
+    assert np.all(got[:, K:] == 0)
     assert np.array_equal(ds.numpy(), s)
+
+
+@pytest.mark.parametrize("M,K,ldq", [(333, 5120, 5120), (65, 1280, 1296), (40, 4000, 4000), (9, 10240, 10240)])
+def test_gelu_quantize_act(dev, oracle, M, K, ldq):
+    """Fused GELU + per-token quantisation against GeluRef then the oracle's
+    per-row quantisation. The device erf is Abramowitz & Stegun 7.1.26
+    (|error| <= 1.5e-7), so a byte may differ by one where the exact product
+    sits within 1e-3 of a rounding tie; scales agree to 2e-6 relative."""
+    r = rng(11 + K)
+    x = (r.standard_normal((M, K)) * r.uniform(0.1, 4, size=(M, 1))).astype(np.float32)
+    x[3] = 0.0  # all-zero row: GELU is zero, scale 1
+    x[5, :8] = [0.0, -0.0, 10.0, -10.0, 1.0, -1.0, 2.0, -30.0]
+    dx, dq, ds = dev.array(x), dev.array(np.full((M, ldq), 99, np.int8)), dev.empty((M,), np.float32)
+    dev.gelu_quantize_act(dx, M, K, dq, ldq, ds)
+    got, s = dq.numpy(), ds.numpy()
+    g = oracle.gelu(x)
+    q_ref, s_ref = oracle.quant_act_rows(g)
+    assert s[3] == 1.0 and np.all(got[3] == 0)
+    np.testing.assert_allclose(s, s_ref, rtol=2e-6)
+    d = got[:, :K].astype(np.int32) - q_ref
+    assert np.abs(d).max() <= 1
+    prod = g.astype(np.float64) / s_ref.astype(np.float64)[:, None]
+    tie = np.abs(prod - np.floor(prod) - 0.5)
+    assert np.all(tie[d != 0] < 1e-3)
+    assert (d != 0).mean() < 1e-3
+    assert np.all(got[:, K:] == 0)
+
+
+def test_gelu_quantize_act_rejects_bad_shapes(dev):
+    dx, dq, ds = dev.empty((2, 8), np.float32), dev.empty((2, 16), np.int8), dev.empty((2,), np.float32)
+    with pytest.raises(eg.Gfx950Error):
+        dev.gelu_quantize_act(dx, 2, 6, dq, 16, ds)  # K % 4 != 0
+    with pytest.raises(eg.Gfx950Error):
+        dev.gelu_quantize_act(dx, 2, 8, dq, 4, ds)  # ldq < K
