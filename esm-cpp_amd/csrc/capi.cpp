@@ -392,6 +392,10 @@ extern "C" int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int 
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_set_gemm_tile_rows(int rows) {
+  return set_gemm_tile_rows(rows) ? ESM_GFX950_OK : ESM_GFX950_INVALID_ARGUMENT;
+}
+
 extern "C" int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const float* a_scale,
                                       const esm_gfx950_weight* W, const float* bias, float* C, int M,
                                       int gelu) {

@@ -21,6 +21,8 @@
 // so each XCD (workgroup id mod 8) walks a contiguous, M-grouped slice of
 // the tile space, which keeps the A rows and W columns it shares inside
 // that XCD's L2.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -359,15 +361,27 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_i8_kernel(const GemmI8Args
 namespace v3 {
 
 constexpr int WAVES_M = 2, WAVES_N = 4;
-constexpr int BLK_M = 4, BLK_N = 2;               // 32x32 blocks per wave
-constexpr int BM = WAVES_M * BLK_M * 32;          // 256
+constexpr int BLK_N = 2;                          // 32x32 column blocks per wave
 constexpr int BN = WAVES_N * BLK_N * 32;          // 256
 constexpr int BK = 128;
 constexpr int kThreads = WAVES_M * WAVES_N * 64;  // 512
-constexpr int kBlocks = (BM + BN) / 8;            // 1 KB blocks per stage
-constexpr int kPer = kBlocks / (WAVES_M * WAVES_N);
-constexpr int kStage = kBlocks * 1024;            // 64 KB
-static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
+
+// Tile height: BLK_M 32x32 row blocks per wave, BM = 64 * BLK_M rows (4: 256,
+// 5: 320). The launcher picks the height that needs the fewer rows' worth of
+// workgroup rounds over the CUs (a 256-row grid that spills a few tiles into
+// one more round often fits in fewer rounds as 320-row tiles).
+template <int BLK_M_>
+struct Tile {
+  static constexpr int BLK_M = BLK_M_;
+  static constexpr int BM = WAVES_M * BLK_M * 32;
+  static constexpr int kBlocks = (BM + BN) / 8;  // 1 KB blocks per stage
+  static constexpr int kPer = kBlocks / (WAVES_M * WAVES_N);
+  static constexpr int kStage = kBlocks * 1024;  // 64 KB (BM 256) / 72 KB (BM 320)
+  // RoPE cos / sin rows of a tile staged in LDS, transposed: [32 dims][BM
+  // rows + pad], so that a lane reads four consecutive rows of one dim at once.
+  static constexpr int kRopeTPitch = BM + 4;
+  static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
+};
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -386,10 +400,6 @@ __device__ __forceinline__ int soff(int R, int c) {
   const int b = R >> 3, r = R & 7;
   return b * 1024 + ((r << 3) + (c ^ r ^ (b & 1))) * 16;
 }
-
-// RoPE cos / sin rows of a tile staged in LDS, transposed: [32 dims][BM rows
-// + pad], so that a lane reads four consecutive rows of one dim at once.
-constexpr int kRopeTPitch = BM + 4;
 
 // Epilogue of one wave's BLK_M x BLK_N blocks of 32x32 int32 accumulators.
 // Element r of block (i, j) in lane l is tile row lr0 + i*32 + (r/4)*8 + r%4
@@ -412,11 +422,12 @@ __device__ __forceinline__ T* at(T* base, uint32_t off) {
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
 // rotary pair. hc: the head's first column relative to the tile origin.
-template <int EPI, bool FULL, int WHICH>
+template <int BLK_M, int EPI, bool FULL, int WHICH>
 __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int g, int hc,
                                          int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
                                          const float (&bs)[BLK_N], const float* s_cosT, const float* s_sinT, int m0,
                                          int n0) {
+  constexpr int kRopeTPitch = Tile<BLK_M>::kRopeTPitch;
   const uint32_t ldc = p.ldc;
   const uint32_t dm = p.d_model;
   // Row offsets: the lane's first row (lr0) times the stride once; the rest
@@ -489,7 +500,7 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
 }
 
 // MAX: also reduce |out| into p.row_absmax / p.tensor_absmax (whichever is set).
-template <int EPI, bool FULL, bool MAX>
+template <int BLK_M, int EPI, bool FULL, bool MAX>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
                                            const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
@@ -527,11 +538,11 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
         if (!FULL && n0 + hc >= p.N) break;
         const int which = (n0 + hc) / p.d_model;
         if (which == 0)
-          qkv_head<EPI, FULL, 0>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 0>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else if (which == 1)
-          qkv_head<EPI, FULL, 1>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 1>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else
-          qkv_head<EPI, FULL, 2>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 2>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
     } else {
@@ -589,12 +600,13 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
   }
 }
 
-template <int EPI>
+template <int BLK_M, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
+  using TL = Tile<BLK_M>;
+  constexpr int BM = TL::BM, kPer = TL::kPer, kStage = TL::kStage, kRopeTPitch = TL::kRopeTPitch;
   __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
   __shared__ float s_as[BM], s_ws[BN], s_bs[BN];
   __shared__ int s_pos[BM];
-  static_assert(kThreads == BM + BN, "one thread per staged row / column scale");
   constexpr bool kRope = EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit;
 
   int m0, n0;
@@ -602,16 +614,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   if constexpr (EPI != kEpiI32) {
     // Per-row activation scales and per-column weight scales / bias of the
     // tile, read once here instead of per element in the epilogue.
-    const int t = threadIdx.x;
-    if (t < BM) {
-      const int row = m0 + t;
-      s_as[t] = row < p.M ? p.a_scale[row] : 0.0f;
-      if constexpr (kRope) s_pos[t] = row < p.M ? p.pos[row] : 0;
-    } else {
-      const int c = t - BM, col = n0 + c;
-      const bool ok = col < p.N;
-      s_ws[c] = ok ? p.w_scale[col] : 0.0f;
-      s_bs[c] = (ok && p.bias) ? p.bias[col] : 0.0f;
+    for (int t = threadIdx.x; t < BM + BN; t += kThreads) {
+      if (t < BM) {
+        const int row = m0 + t;
+        s_as[t] = row < p.M ? p.a_scale[row] : 0.0f;
+        if constexpr (kRope) s_pos[t] = row < p.M ? p.pos[row] : 0;
+      } else {
+        const int c = t - BM, col = n0 + c;
+        const bool ok = col < p.N;
+        s_ws[c] = ok ? p.w_scale[col] : 0.0f;
+        s_bs[c] = (ok && p.bias) ? p.bias[col] : 0.0f;
+      }
     }
     __syncthreads();
   }
@@ -678,25 +691,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   if constexpr (kRope) {
     if (n0 < 2 * p.d_model) {
       // The tile holds Q or K columns: stage its rows' RoPE cos / sin,
-      // transposed, in the now idle operand buffers. Thread t copies half a
-      // table row (cos for even t, sin for odd t) of tile row t / 2.
-      static_assert(kThreads == 2 * BM, "two threads per staged RoPE row");
+      // transposed, in the now idle operand buffers. Item u copies half a
+      // table row (cos for even u, sin for odd u) of tile row u / 2.
       static_assert(2 * 32 * kRopeTPitch * 4 <= 2 * kStage, "RoPE staging fits in the operand buffers");
       float* cosT = reinterpret_cast<float*>(smem);
       float* sinT = cosT + 32 * kRopeTPitch;
       __syncthreads();
-      const int t = threadIdx.x >> 1;
-      const bool odd = threadIdx.x & 1;
-      const float4* src =
-          reinterpret_cast<const float4*>((odd ? p.rope_sin : p.rope_cos) + static_cast<size_t>(s_pos[t]) * 64);
-      float* dst = (odd ? sinT : cosT) + t;
+      for (int u = threadIdx.x; u < 2 * BM; u += kThreads) {
+        const int t = u >> 1;
+        const bool odd = u & 1;
+        const float4* src =
+            reinterpret_cast<const float4*>((odd ? p.rope_sin : p.rope_cos) + static_cast<size_t>(s_pos[t]) * 64);
+        float* dst = (odd ? sinT : cosT) + t;
 #pragma unroll
-      for (int c4 = 0; c4 < 8; ++c4) {
-        const float4 v = src[c4];
-        dst[(4 * c4 + 0) * kRopeTPitch] = v.x;
-        dst[(4 * c4 + 1) * kRopeTPitch] = v.y;
-        dst[(4 * c4 + 2) * kRopeTPitch] = v.z;
-        dst[(4 * c4 + 3) * kRopeTPitch] = v.w;
+        for (int c4 = 0; c4 < 8; ++c4) {
+          const float4 v = src[c4];
+          dst[(4 * c4 + 0) * kRopeTPitch] = v.x;
+          dst[(4 * c4 + 1) * kRopeTPitch] = v.y;
+          dst[(4 * c4 + 2) * kRopeTPitch] = v.z;
+          dst[(4 * c4 + 3) * kRopeTPitch] = v.w;
+        }
       }
       __syncthreads();
       s_cosT = cosT;
@@ -707,14 +721,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
-      epilogue32<EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
     else
-      epilogue32<EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
   } else {
     if (full)
-      epilogue32<EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
     else
-      epilogue32<EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
   }
 }
 
@@ -739,22 +753,60 @@ hipError_t launch_v1(const GemmI8Args& p, int epi, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
+template <int BLK_M>
+hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
   using namespace v3;
+  constexpr int BM = Tile<BLK_M>::BM;
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
   const dim3 grid(tiles), block(kThreads);
   switch (epi) {
-    case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiI32>), grid, block, 0, s, p); break;
-    case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32>), grid, block, 0, s, p); break;
-    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32Gelu>), grid, block, 0, s, p); break;
-    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32Resid>), grid, block, 0, s, p); break;
-    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRope>), grid, block, 0, s, p); break;
-    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiF32GeluQ>), grid, block, 0, s, p); break;
-    case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvRopeF32>), grid, block, 0, s, p); break;
-    case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<kEpiQkvSplit>), grid, block, 0, s, p); break;
+    case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiI32>), grid, block, 0, s, p); break;
+    case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32>), grid, block, 0, s, p); break;
+    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32Gelu>), grid, block, 0, s, p); break;
+    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32Resid>), grid, block, 0, s, p); break;
+    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvRope>), grid, block, 0, s, p); break;
+    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiQkvRopeF32:
+      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvRopeF32>), grid, block, 0, s, p);
+      break;
+    case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvSplit>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+std::atomic<int> g_tile_rows{0};
+
+// CUs of the current device (queried once per device).
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Workgroup rounds times tile height: the rows' worth of tile time the grid
+// needs when every round costs one tile's time.
+long tile_cost(int M, int N, int BM, int cus) {
+  const long tiles = static_cast<long>((M + BM - 1) / BM) * ((N + v3::BN - 1) / v3::BN);
+  return (tiles + cus - 1) / cus * BM;
+}
+
+hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
+  int rows = g_tile_rows.load(std::memory_order_relaxed);
+  if (rows == 0) {
+    // The 320-row tile is chosen automatically only for the plain epilogues:
+    // with BLK_M = 5 the GELU and QKV epilogues exceed 256 VGPRs and spill.
+    const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid;
+    const int cus = device_cus();
+    rows = tall_ok && tile_cost(p.M, p.N, v3::Tile<5>::BM, cus) < tile_cost(p.M, p.N, v3::Tile<4>::BM, cus) ? 320
+                                                                                                          : 256;
+  }
+  return rows == 320 ? launch_v3_tile<5>(p, epi, s) : launch_v3_tile<4>(p, epi, s);
 }
 
 }  // namespace
@@ -775,6 +827,12 @@ hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epi, int variant, hip
 
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
   return launch_gemm_i8_variant(p, epi, gemm_i8_pipelined_ok(p) ? 2 : 1, s);
+}
+
+bool set_gemm_tile_rows(int rows) {
+  if (rows != 0 && rows != 256 && rows != 320) return false;
+  g_tile_rows.store(rows, std::memory_order_relaxed);
+  return true;
 }
 
 }  // namespace esm_gfx950

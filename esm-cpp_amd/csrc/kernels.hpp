@@ -55,12 +55,16 @@ struct GemmI8Args {
   float q_prescale = 1.0f;  // kEpiQkvSplit: power of two applied to Q before the split
 };
 
-// Picks the pipelined 256x256 kernel when gemm_i8_pipelined_ok(p) (K a
+// Picks the pipelined 256- or 320-row-tile kernel when gemm_i8_pipelined_ok(p) (K a
 // multiple of 128, 16-byte aligned rows), else the general 256x128 kernel.
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epilogue, hipStream_t s);
 bool gemm_i8_pipelined_ok(const GemmI8Args& p);
 // variant 1: general kernel; 2: pipelined kernel (fails on shapes it cannot take).
 hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epilogue, int variant, hipStream_t s);
+// Row height of the pipelined kernel's tile for every later launch in the
+// process: 256, 320, or 0 to pick per launch (fewest rows' worth of
+// workgroup rounds over the device's CUs). False for other values.
+bool set_gemm_tile_rows(int rows);
 
 // ---------------------------------------------------------------- FP32 GEMM
 enum GemmF32Epilogue : int {

@@ -131,6 +131,14 @@ int esm_gfx950_weight_free(esm_gfx950_ctx* ctx, esm_gfx950_weight* w);
 int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const esm_gfx950_weight* W,
                            int M, int32_t* C);
 
+/* Row height of the INT8 GEMM's workgroup tile for every later launch in the
+ * process: 256, 320, or 0 (default) to pick per launch the height whose grid
+ * needs the fewer rows' worth of workgroup rounds over the device's CUs
+ * (320 only for the plain dequant / int32 outputs). Results do not depend on
+ * it; it exists for tuning and tests. No reference counterpart.
+ * INVALID_ARGUMENT for other values. */
+int esm_gfx950_set_gemm_tile_rows(int rows);
+
 /* Quantised-activation linear: out = fma(float(acc), a_scale[m] * w_scale[n], bias[n]),
  * optionally followed by GELU (gelu != 0). The dequant expression of
  * FinalizeStore16 (gemm_int8.cpp:109-126) with a per-row activation scale.

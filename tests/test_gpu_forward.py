@@ -75,6 +75,24 @@ def test_w8a8_forward_vs_oracle(dev, oracle, w650_small, small_batch, per_token,
     assert agree >= (0.98 if precise else 0.9), agree
 
 
+@pytest.mark.parametrize("per_token", [False, True])
+def test_gemm_tile_rows_do_not_change_logits(dev, w650_small, small_batch, per_token):
+    """The INT8 GEMM's 256- and 320-row tiles (and the automatic choice) give
+    bit-identical logits: the same int32 sums and the same dequant
+    expressions, only the workgroup tiling differs."""
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w650_small, int8=True, act_mode=mode)
+    outs = []
+    try:
+        for rows in (256, 320, 0):
+            eg.set_gemm_tile_rows(rows)
+            outs.append(m.forward_packed(small_batch.ids, small_batch.cu))
+    finally:
+        eg.set_gemm_tile_rows(0)
+        m.free()
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
 def test_packed_equals_serial(dev, w650_small, small_batch):
     """Per-token mode keeps every row independent, so packing changes nothing."""
     m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)

@@ -14,6 +14,14 @@ pytestmark = pytest.mark.gpu
 import esm_gfx950 as eg
 
 
+@pytest.fixture(params=[0, 256, 320], ids=["rows-auto", "rows-256", "rows-320"])
+def tile_rows(request):
+    """INT8 GEMM tile height (0: the per-launch choice); reset afterwards."""
+    eg.set_gemm_tile_rows(request.param)
+    yield request.param
+    eg.set_gemm_tile_rows(0)
+
+
 def _pad(a, ld):
     out = np.zeros((a.shape[0], ld), a.dtype)
     out[:, :a.shape[1]] = a
@@ -28,7 +36,7 @@ def _i8(r, shape):
     (1, 16, 16), (37, 64, 64), (5, 9, 17), (130, 260, 48), (300, 1280, 1280), (257, 3840, 1280),
     (129, 1280, 5120), (64, 5120, 1280), (31, 2560, 10240),
 ])
-def test_int32_bit_exact(dev, oracle, M, N, K):
+def test_int32_bit_exact(dev, oracle, tile_rows, M, N, K):
     r = rng(1000 + M + N + K)
     A = _i8(r, (M, K))
     W = _i8(r, (N, K))
@@ -58,7 +66,7 @@ def test_int32_extremes(dev, oracle):
     w.free()
 
 
-def test_config3_full_size_rows(dev, oracle):
+def test_config3_full_size_rows(dev, oracle, tile_rows):
     """Config 3 shape [30700 x 1280] x [5120 x 1280]^T: int32 bit-exact on a
     row sample, dequant+bias+GELU within 1e-5 on the same rows."""
     M, N, K = 30700, 5120, 1280
@@ -93,7 +101,7 @@ def test_config3_full_size_rows(dev, oracle):
 
 @pytest.mark.parametrize("mode", [eg.ACT_PER_TENSOR, eg.ACT_PER_TOKEN])
 @pytest.mark.parametrize("M,N,K", [(18, 1280, 1280), (96, 320, 320), (257, 5120, 1280), (64, 1280, 5120), (7, 33, 17)])
-def test_linear_int8_facade(dev, oracle, mode, M, N, K):
+def test_linear_int8_facade(dev, oracle, tile_rows, mode, M, N, K):
     """esm_gfx950_linear_i8 == oracle quant -> int32 GEMM -> dequant, bit-exact."""
     r = rng(77 + M + N + K + mode)
     A = r.uniform(-1, 1, size=(M, K)).astype(np.float32)
@@ -112,6 +120,11 @@ def test_linear_int8_facade(dev, oracle, mode, M, N, K):
     want = oracle.dequant(oracle.gemm_i8_i32(aq, q), scales, s, bias)
     assert np.array_equal(got, want)
     w.free()
+
+
+def test_tile_rows_rejects_other_heights():
+    with pytest.raises(eg.Gfx950Error):
+        eg.set_gemm_tile_rows(300)
 
 
 def test_linear_int8_zero_sizes(dev):
