@@ -687,6 +687,12 @@ struct esm_gfx950_model {
   std::vector<DevLayer> layers;
   float *final_ln_w = nullptr, *final_ln_b = nullptr;
   float *lm_dense_w = nullptr, *lm_dense_b = nullptr;
+  // lm head dense weight as split-fp16 planes of W * 2^shift (null when
+  // d % 32 != 0) and whether the forward uses them (split-fp16 GEMM) or the
+  // fp32 weight (fp32 MFMA).
+  uint16_t *lm_w_hi = nullptr, *lm_w_lo = nullptr;
+  float lm_w_unscale = 1.0f;
+  bool lm_dense_split = false;
   float *lm_ln_w = nullptr, *lm_ln_b = nullptr;
   float* dec_bias = nullptr;
   // W8A8 models: Q's 1/sqrt(head_dim) multiplied into the Q weight scales and
@@ -744,6 +750,33 @@ int upload_f(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const T* src, size_t n, T
 
 // Concatenates the given linears along N into one device weight.
 // part0_scale multiplies part 0's per-channel scales and bias (int8 only).
+// W [N, K] fp32 as the two fp16 planes of the split-fp16 GEMM: hi = fp16(x),
+// lo = fp16(x - hi) of x = W * 2^shift, with the shift putting max|W| in
+// [2^13, 2^14) so that the lo parts of small weights stay normal fp16.
+int upload_split(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const float* w, int N, int K) {
+  const size_t n = static_cast<size_t>(N) * K;
+  float amax = 0.0f;
+  for (size_t i = 0; i < n; ++i) amax = std::max(amax, std::fabs(w[i]));
+  int shift = 0;
+  if (amax > 0.0f && std::isfinite(amax)) {
+    int e = 0;
+    std::frexp(amax, &e);  // amax in [2^(e-1), 2^e)
+    shift = std::min(100, std::max(-100, 14 - e));
+  }
+  std::vector<uint16_t> hi(n), lo(n);
+  for (size_t i = 0; i < n; ++i) {
+    const float x = std::ldexp(w[i], shift);
+    const _Float16 h = static_cast<_Float16>(x);
+    const _Float16 l = static_cast<_Float16>(x - static_cast<float>(h));
+    hi[i] = __builtin_bit_cast(uint16_t, h);
+    lo[i] = __builtin_bit_cast(uint16_t, l);
+  }
+  ESM_TRY(upload_f(ctx, m, hi.data(), n, &m->lm_w_hi));
+  ESM_TRY(upload_f(ctx, m, lo.data(), n, &m->lm_w_lo));
+  m->lm_w_unscale = std::ldexp(1.0f, -shift);
+  return ESM_GFX950_OK;
+}
+
 int upload_linear(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const esm_gfx950_linear_desc* const* parts,
                   int nparts, int N_each, int K, bool int8, DevLinear* out, float part0_scale = 1.0f) {
   const int N = N_each * nparts;
@@ -877,6 +910,12 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   step(upload_f(ctx, m, desc->final_ln_b, d, &m->final_ln_b));
   step(upload_f(ctx, m, desc->lm_dense_w, static_cast<size_t>(d) * d, &m->lm_dense_w));
   step(upload_f(ctx, m, desc->lm_dense_b, d, &m->lm_dense_b));
+  if (rc == ESM_GFX950_OK && d % 32 == 0) {
+    step(upload_split(ctx, m, desc->lm_dense_w, d, d));
+    // W8A8 models run the dense on the split-fp16 GEMM; all-fp32 models keep
+    // the fp32 MFMA kernel (esm_gfx950_model_set_lm_dense_split switches).
+    m->lm_dense_split = i8;
+  }
   step(upload_f(ctx, m, desc->lm_ln_w, d, &m->lm_ln_w));
   step(upload_f(ctx, m, desc->lm_ln_b, d, &m->lm_ln_b));
   step(upload_f(ctx, m, desc->lm_decoder_bias, V, &m->dec_bias));
@@ -909,6 +948,13 @@ extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_mod
 extern "C" int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled) {
   if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
   model->first_block_fc1_fp16 = enabled != 0;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_model_set_lm_dense_split(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled) {
+  if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, !enabled || model->lm_w_hi, "model_set_lm_dense_split: hidden size is not a multiple of 32");
+  model->lm_dense_split = enabled != 0;
   return ESM_GFX950_OK;
 }
 
@@ -1488,7 +1534,24 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   dense.K = d;
   int slot;
   ESM_TRY(ctx->time_begin("lm_dense", &slot));
-  ESM_TRY(f32_linear(ctx, a.ln, dense, a.lm_a, T, kF32Gelu));
+  if (m->lm_dense_split) {
+    GemmX3Args x;
+    x.A = a.ln;
+    x.lda = d;
+    x.w_hi = m->lm_w_hi;
+    x.w_lo = m->lm_w_lo;
+    x.ldw = d;
+    x.w_unscale = m->lm_w_unscale;
+    x.bias = m->lm_dense_b;
+    x.C = a.lm_a;
+    x.ldc = d;
+    x.M = T;
+    x.N = d;
+    x.K = d;
+    ESM_HIP(ctx, launch_gemm_x3(x, kF32Gelu, s));
+  } else {
+    ESM_TRY(f32_linear(ctx, a.ln, dense, a.lm_a, T, kF32Gelu));
+  }
   ESM_TRY(ctx->time_end(slot));
   ESM_HIP(ctx, launch_layernorm(a.lm_a, nullptr, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr, s));
   DevLinear dec;

@@ -139,7 +139,155 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const GemmF32Args
   }
 }
 
+// ---- Split-fp16 GEMM (fp32 accuracy on fp16 MFMA), same 128x128 tile and
+// wave layout as above on v_mfma_f32_16x16x32_f16: each lane holds eight
+// consecutive k of one row for A and W, so one MFMA covers a 32-wide K stage.
+// A (fp32) is split into hi / lo fp16 planes while it is staged in LDS; W's
+// planes come split. LDS rows are 80 bytes (64 + 16 pad): the 16 rows one
+// 16-lane group reads sit 20 banks apart, so the fragment reads are
+// conflict-free.
+constexpr int kX3Pitch = 80;                    // bytes per 32-half row
+constexpr int kX3Plane = 128 * kX3Pitch;        // one 128-row plane
+constexpr int kX3Stage = 4 * kX3Plane;          // A hi, A lo, W hi, W lo
+
+__device__ __forceinline__ uint2 pack_f16x4(float a, float b, float c, float d) {
+  return make_uint2(static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16),
+                    static_cast<uint32_t>(f32_to_f16_bits(c)) | (static_cast<uint32_t>(f32_to_f16_bits(d)) << 16));
+}
+
+// One K stage of the tile from global memory: A 128 rows x 32 floats (four
+// float4 per thread), W planes 128 rows x 32 halves each (two 16-byte pieces
+// per plane per thread). Rows past the edge re-read the last valid row;
+// their results are never stored.
+__device__ __forceinline__ void x3_load(const GemmX3Args& p, int m0, int n0, int k0, f32x4 (&ra)[4],
+                                        i32x4 (&rh)[2], i32x4 (&rl)[2]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + kThreads * i;
+    const int row = min(m0 + (idx >> 3), p.M - 1);
+    ra[i] = *reinterpret_cast<const f32x4*>(p.A + static_cast<size_t>(row) * p.lda + k0 + (idx & 7) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = t + kThreads * i;
+    const int row = min(n0 + (idx >> 2), p.N - 1);
+    const size_t off = static_cast<size_t>(row) * p.ldw + k0 + (idx & 3) * 8;
+    rh[i] = *reinterpret_cast<const i32x4*>(p.w_hi + off);
+    rl[i] = *reinterpret_cast<const i32x4*>(p.w_lo + off);
+  }
+}
+
+// The stage into LDS: A split into hi / lo planes, W planes as loaded.
+__device__ __forceinline__ void x3_store(uint8_t* st, const f32x4 (&ra)[4], const i32x4 (&rh)[2],
+                                         const i32x4 (&rl)[2]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + kThreads * i;
+    const int off = (idx >> 3) * kX3Pitch + (idx & 7) * 8;
+    const f32x4 x = ra[i];
+    const float hx = f16_bits_to_f32(f32_to_f16_bits(x[0])), hy = f16_bits_to_f32(f32_to_f16_bits(x[1]));
+    const float hz = f16_bits_to_f32(f32_to_f16_bits(x[2])), hw = f16_bits_to_f32(f32_to_f16_bits(x[3]));
+    *reinterpret_cast<uint2*>(st + off) = pack_f16x4(hx, hy, hz, hw);
+    *reinterpret_cast<uint2*>(st + kX3Plane + off) = pack_f16x4(x[0] - hx, x[1] - hy, x[2] - hz, x[3] - hw);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = t + kThreads * i;
+    const int off = (idx >> 2) * kX3Pitch + (idx & 3) * 16;
+    *reinterpret_cast<i32x4*>(st + 2 * kX3Plane + off) = rh[i];
+    *reinterpret_cast<i32x4*>(st + 3 * kX3Plane + off) = rl[i];
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 2) void gemm_x3_kernel(const GemmX3Args p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kX3Stage];
+  const int tiles_n = (p.N + BN - 1) / BN;
+  const int m0 = (blockIdx.x / tiles_n) * BM;
+  const int n0 = (blockIdx.x % tiles_n) * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  f32x4 ra[4];
+  i32x4 rh[2], rl[2];
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = p.K / 32;
+  x3_load(p, m0, n0, 0, ra, rh, rl);
+  x3_store(smem, ra, rh, rl);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint8_t* cur = smem + (kt & 1) * kX3Stage;
+    const bool more = kt + 1 < nk;
+    if (more) x3_load(p, m0, n0, (kt + 1) * 32, ra, rh, rl);
+    f16x8 ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ao = (wm * 64 + i * 16 + lr) * kX3Pitch + lg * 16;
+      const int bo = (wn * 64 + i * 16 + lr) * kX3Pitch + lg * 16;
+      ah[i] = *reinterpret_cast<const f16x8*>(cur + ao);
+      al[i] = *reinterpret_cast<const f16x8*>(cur + kX3Plane + ao);
+      bh[i] = *reinterpret_cast<const f16x8*>(cur + 2 * kX3Plane + bo);
+      bl[i] = *reinterpret_cast<const f16x8*>(cur + 3 * kX3Plane + bo);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[n], acc[i][n], 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[n], c, 0, 0, 0);
+        acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[n], c, 0, 0, 0);
+      }
+    if (more) x3_store(smem + ((kt + 1) & 1) * kX3Stage, ra, rh, rl);
+    __syncthreads();
+  }
+
+  const int rb0 = m0 + wm * 64, cb0 = n0 + wn * 64;
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int col = cb0 + n * 16 + lr;
+    if (col >= p.N) continue;
+    const float b = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rb0 + i * 16 + lg * 4 + r;
+        if (row >= p.M) continue;
+        float v = __builtin_fmaf(acc[i][n][r], p.w_unscale, b);
+        if constexpr (EPI == kF32Gelu) v = gelu_erf(v);
+        float* dst = p.C + static_cast<size_t>(row) * p.ldc + col;
+        if constexpr (EPI == kF32Resid) {
+          *dst += v;
+        } else {
+          *dst = v;
+        }
+      }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_gemm_x3(const GemmX3Args& p, int epi, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (p.K <= 0 || p.K % 32 != 0 || p.lda % 4 != 0 || p.ldw % 8 != 0) return hipErrorInvalidValue;
+  const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+  const dim3 grid(tiles), block(kThreads);
+  switch (epi) {
+    case kF32Store: hipLaunchKernelGGL((gemm_x3_kernel<kF32Store>), grid, block, 0, s, p); break;
+    case kF32Gelu: hipLaunchKernelGGL((gemm_x3_kernel<kF32Gelu>), grid, block, 0, s, p); break;
+    case kF32Resid: hipLaunchKernelGGL((gemm_x3_kernel<kF32Resid>), grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_f32(const GemmF32Args& p, int epi, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;

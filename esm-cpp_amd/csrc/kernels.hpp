@@ -84,6 +84,27 @@ struct GemmF32Args {
 };
 hipError_t launch_gemm_f32(const GemmF32Args& p, int epilogue, hipStream_t s);
 
+// FP32-accurate GEMM on fp16 MFMA ("split-fp16"): every operand x is carried
+// as hi = fp16(x) and lo = fp16(x - hi), and every product as hi*hi + lo*hi +
+// hi*lo (22 significant bits per operand; the dropped lo*lo term is below
+// 2^-22 relative), accumulated in fp32. A is fp32 and split on the fly; W
+// arrives pre-split as two fp16 planes [N, ldw] holding W * 2^w_shift (the
+// shift keeps the lo parts of small weights out of the fp16 subnormal
+// range), which the epilogue undoes exactly. K % 32 == 0.
+struct GemmX3Args {
+  const float* A = nullptr;
+  int lda = 0;
+  const uint16_t* w_hi = nullptr;
+  const uint16_t* w_lo = nullptr;
+  int ldw = 0;
+  float w_unscale = 1.0f;  // 2^-w_shift
+  const float* bias = nullptr;
+  float* C = nullptr;
+  int ldc = 0;
+  int M = 0, N = 0, K = 0;
+};
+hipError_t launch_gemm_x3(const GemmX3Args& p, int epilogue, hipStream_t s);
+
 // ------------------------------------------------------------- attention
 // One work item per (sequence, head, query tile); built on the host from
 // cu_seqlens, longest sequences first.

@@ -37,7 +37,7 @@ EXPORTED = [
     "esm_gfx950_memcpy_d2h", "esm_gfx950_memcpy_d2d", "esm_gfx950_timer_start", "esm_gfx950_timer_stop",
     "esm_gfx950_kernel_timing", "esm_gfx950_kernel_timing_query", "esm_gfx950_weight_upload_i8",
     "esm_gfx950_weight_free", "esm_gfx950_gemm_i8_i32", "esm_gfx950_linear_i8_q", "esm_gfx950_quantize_act",
-    "esm_gfx950_gelu_quantize_act", "esm_gfx950_set_gemm_tile_rows",
+    "esm_gfx950_gelu_quantize_act", "esm_gfx950_set_gemm_tile_rows", "esm_gfx950_model_set_lm_dense_split",
     "esm_gfx950_linear_i8", "esm_gfx950_linear_f32", "esm_gfx950_layernorm", "esm_gfx950_gelu",
     "esm_gfx950_residual_add", "esm_gfx950_scale", "esm_gfx950_rope_build_tables",
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
@@ -91,6 +91,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
         "esm_gfx950_gelu_quantize_act": (i32, [vp, vp, i32, i32, vp, i32, vp]),
         "esm_gfx950_set_gemm_tile_rows": (i32, [i32]),
+        "esm_gfx950_model_set_lm_dense_split": (i32, [vp, vp, i32]),
         "esm_gfx950_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
         "esm_gfx950_linear_f32": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
         "esm_gfx950_layernorm": (i32, [vp, vp, vp, vp, f32, vp, i32, i32]),
@@ -485,6 +486,10 @@ class Model:
 
     def set_act_mode(self, mode: int):
         self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))
+
+    def set_lm_dense_split(self, enabled: bool):
+        """lm head dense on the split-fp16 GEMM (True) or fp32 MFMA (False)."""
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_lm_dense_split(self.dev.ctx, self.handle, int(enabled)))
 
     def set_parts(self, parts: int):
         """Concurrent sequence groups per batch (esm_gfx950_model_set_parts)."""

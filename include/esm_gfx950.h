@@ -365,6 +365,13 @@ int esm_gfx950_observer_percentile(const esm_gfx950_observer* obs, const char* s
 int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                                      const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
                                      esm_gfx950_observer* obs);
+/* The lm head's dense d x d linear (reference src/model.cpp:1209-1215, FP32
+ * Linear) on the split-fp16 GEMM (enabled != 0: each operand carried as two
+ * fp16 parts, three fp16 MFMA products per multiply, fp32 accumulation) or on
+ * fp32 MFMA (0). Both are fp32-accurate; W8A8 models start with the split
+ * form, all-fp32 models with fp32 MFMA. INVALID_ARGUMENT when the hidden size
+ * is not a multiple of 32 (no split weights). No reference counterpart. */
+int esm_gfx950_model_set_lm_dense_split(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled);
 /* Bytes currently held by the model's device arena (for zero-growth checks). */
 int esm_gfx950_model_arena_bytes(const esm_gfx950_model* model, size_t* bytes);
 

@@ -75,6 +75,33 @@ def test_w8a8_forward_vs_oracle(dev, oracle, w650_small, small_batch, per_token,
     assert agree >= (0.98 if precise else 0.9), agree
 
 
+def test_config1_lm_dense_split_fp16(dev, oracle, w8m):
+    """The lm head's dense linear on the split-fp16 GEMM (22-bit operand
+    parts, three fp16 MFMA products, fp32 accumulation) keeps the all-fp32
+    model within the config-1 bar of the oracle (rtol = atol = 1e-5)."""
+    batch = syn.config1_batch()
+    m = eg.Model(dev, w8m, int8=False)
+    m.set_lm_dense_split(True)
+    got = m.forward_packed(batch.ids, batch.cu)
+    m.free()
+    want = oracle.forward_packed(w8m, batch, int8=False, per_token=False)
+    print("max |split - oracle| =", float(np.abs(got - want).max()))
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_w8a8_lm_dense_split_matches_fp32_mfma(dev, w650_small, small_batch):
+    """W8A8 models default to the split-fp16 lm dense; against the fp32-MFMA
+    dense the logits agree to fp32 rounding noise (1e-5 of the logit range)."""
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    split = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.set_lm_dense_split(False)
+    f32 = m.forward_packed(small_batch.ids, small_batch.cu)
+    m.free()
+    scale = float(np.abs(f32).max())
+    print("max |split - fp32| / max|logit| =", float(np.abs(split - f32).max()) / scale)
+    np.testing.assert_allclose(split, f32, rtol=0, atol=1e-5 * scale)
+
+
 @pytest.mark.parametrize("per_token", [False, True])
 def test_gemm_tile_rows_do_not_change_logits(dev, w650_small, small_batch, per_token):
     """The INT8 GEMM's 256- and 320-row tiles (and the automatic choice) give
