@@ -23,6 +23,8 @@
 // exp/sum/weighted V with a double-precision sum), the reference's order.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -291,6 +293,21 @@ __device__ __forceinline__ void unpack8(const uint4& a, const uint4& b, f16x8* h
   *lo = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(l));
 }
 
+// Raw v_exp_f32: 2^x for results >= 2^-126 exactly as exp2f, 0 below (the
+// library's exp2f adds a rescale for subnormal results; probabilities under
+// 2^-126 of the row maximum do not change an fp32 softmax sum).
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Eight probabilities as split-fp16 operands: hi = fp16(p), lo = fp16(p - hi)
+// (the split of split_f16_word, in split_pair's packed form).
+__device__ __forceinline__ void split8(const float (&p)[8], f16x8* hi, f16x8* lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) split_pair(p[2 * j], p[2 * j + 1], &h[j], &l[j]);
+  *hi = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(h));
+  *lo = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(l));
+}
+
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     const uint32_t* __restrict__ q, const uint32_t* __restrict__ k,
     const uint32_t* __restrict__ v, int ld, float s2, const int* __restrict__ cu,
@@ -306,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   const int hoff = w.head * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
   const int qbase = w.q0 + wave * 32;
   const bool active = qbase < L;  // wave-uniform
@@ -314,24 +331,26 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   // K / V chunk loads into registers (K: KCX keys x 16 uint4; V: KCX/2 key
   // pairs x 16 dim quads), clamped to the sequence's last key; the chunk
   // after the current one is loaded while the current one is computed.
+  // Addresses: a uniform chunk base plus 32-bit lane byte offsets.
   constexpr int kKLoads = KCX * 16 / 256, kVLoads = KCX / 2 * 16 / 256;
+  const uint32_t ldb = static_cast<uint32_t>(ld) * 4u;  // row pitch in bytes
   uint4 kr[kKLoads], va[kVLoads], vb[kVLoads];
   auto load_chunk = [&](int kc) {
     const int nk = min(KCX, L - kc);
-    const uint32_t* kbase = k + static_cast<size_t>(start + kc) * ld + hoff;
-    const uint32_t* vbase = v + static_cast<size_t>(start + kc) * ld + hoff;
+    const char* kbase = reinterpret_cast<const char*>(k + static_cast<size_t>(start + kc) * ld + hoff);
+    const char* vbase = reinterpret_cast<const char*>(v + static_cast<size_t>(start + kc) * ld + hoff);
 #pragma unroll
     for (int i = 0; i < kKLoads; ++i) {
       const int idx = tid + 256 * i;
       const int key = idx >> 4, c4 = idx & 15;
-      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(min(key, nk - 1)) * ld + c4 * 4);
+      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<uint32_t>(min(key, nk - 1)) * ldb + c4 * 16);
     }
 #pragma unroll
     for (int i = 0; i < kVLoads; ++i) {
       const int idx = tid + 256 * i;
       const int dq = idx & 15, key0 = 2 * (idx >> 4);
-      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0, nk - 1)) * ld + dq * 4);
-      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(min(key0 + 1, nk - 1)) * ld + dq * 4);
+      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key0, nk - 1)) * ldb + dq * 16);
+      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key0 + 1, nk - 1)) * ldb + dq * 16);
     }
   };
 
@@ -365,14 +384,17 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   float mrun[2] = {-INFINITY, -INFINITY};
   float lrun[2] = {0.f, 0.f};
 
-  for (int kc0 = 0; kc0 < L; kc0 += KCX) {
-    const int nkeys = min(KCX, L - kc0);
+  // One chunk of keys; FULLC: all KCX keys are valid (every chunk but the
+  // last of a sequence whose length is not a multiple of KCX), so no key
+  // needs masking.
+  auto chunk = [&](int kc0, int nkeys, auto fullc_tag) {
+    constexpr bool FULLC = decltype(fullc_tag)::value;
     __syncthreads();  // the previous chunk's LDS reads are done
 #pragma unroll
     for (int i = 0; i < kKLoads; ++i) {
       const int idx = tid + 256 * i;
       const int key = idx >> 4, c4 = idx & 15;
-      const uint4 x = key < nkeys ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 x = (FULLC || key < nkeys) ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
       *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) =
           make_uint2(halves(x.x, x.y, kSelLo), halves(x.z, x.w, kSelLo));
       *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) =
@@ -383,8 +405,8 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     for (int i = 0; i < kVLoads; ++i) {
       const int idx = tid + 256 * i;
       const int dq = idx & 15, key0 = 2 * (idx >> 4);
-      const uint4 a = key0 < nkeys ? va[i] : make_uint4(0u, 0u, 0u, 0u);
-      const uint4 b = key0 + 1 < nkeys ? vb[i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 a = (FULLC || key0 < nkeys) ? va[i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 b = (FULLC || key0 + 1 < nkeys) ? vb[i] : make_uint4(0u, 0u, 0u, 0u);
       const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -395,9 +417,9 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     }
     if (kc0 + KCX < L) load_chunk(kc0 + KCX);  // in flight during this chunk's compute
     __syncthreads();
-    if (!active) continue;
+    if (!active) return;
 
-    const int nkb = (nkeys + 15) >> 4;
+    const int nkb = FULLC ? KCX / 16 : (nkeys + 15) >> 4;
     f32x4 s[KCX / 16][2];
 #pragma unroll
     for (int kb = 0; kb < KCX / 16; ++kb) {
@@ -433,7 +455,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kb * 16 + lg * 4 + i;
-            const float sv = key < nkeys ? s[kb][qb][i] * s2 : -INFINITY;
+            const float sv = (FULLC || key < nkeys) ? s[kb][qb][i] * s2 : -INFINITY;
             s[kb][qb][i] = sv;
             cmax = fmaxf(cmax, sv);
           }
@@ -442,7 +464,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
       mnew[qb] = fmaxf(mrun[qb], cmax);
-      const float alpha = exp2f(mrun[qb] - mnew[qb]);
+      const float alpha = exp2_raw(mrun[qb] - mnew[qb]);
       mrun[qb] = mnew[qb];
       lrun[qb] *= alpha;
 #pragma unroll
@@ -454,21 +476,18 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     for (int kp = 0; kp < KCX / 32; ++kp) {
       if (2 * kp < nkb) {
         f16x8 pfh[2], pfl[2];
-        const bool two = 2 * kp + 1 < nkb;
+        const bool two = FULLC || 2 * kp + 1 < nkb;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
+          float pr[8];
           float psum = 0.f;
-          uint32_t wd[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             const int kb = 2 * kp + (j >> 2);
-            float p = 0.f;
-            if (j < 4 || two) p = exp2f(s[kb][qb][j & 3] - mnew[qb]);
-            psum += p;
-            wd[j] = split_f16_word(p);
+            pr[j] = (j < 4 || two) ? exp2_raw(s[kb][qb][j & 3] - mnew[qb]) : 0.f;
+            psum += pr[j];
           }
-          const uint4 a = make_uint4(wd[0], wd[1], wd[2], wd[3]), b = make_uint4(wd[4], wd[5], wd[6], wd[7]);
-          unpack8(a, b, &pfh[qb], &pfl[qb]);
+          split8(pr, &pfh[qb], &pfl[qb]);
           lrun[qb] += psum;
         }
 #pragma unroll
@@ -490,6 +509,14 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         }
       }
     }
+  };
+
+  for (int kc0 = 0; kc0 < L; kc0 += KCX) {
+    const int nkeys = min(KCX, L - kc0);
+    if (nkeys == KCX)
+      chunk(kc0, nkeys, std::true_type{});
+    else
+      chunk(kc0, nkeys, std::false_type{});
   }
 
   if (!active) return;

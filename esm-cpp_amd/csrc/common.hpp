@@ -59,10 +59,29 @@ __device__ __forceinline__ float wave_max(float v) {
 // half. x - fp16(x) is exact in fp32, so hi + lo keeps 22 significant bits of
 // x (lo is subnormal when |x| < 2^-3, i.e. absolute error <= 2^-25 there).
 __device__ __forceinline__ uint32_t split_f16_word(float x) {
-  const _Float16 h = static_cast<_Float16>(x);
-  const _Float16 l = static_cast<_Float16>(x - static_cast<float>(h));
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l)) << 16);
+  // hi = fp16(x) into the low half (v_cvt_f16_f32), then lo = fp16(x - hi)
+  // into the high half (v_fma_mixhi_f16 reads hi as fp16; x - hi is exact in
+  // fp32, so its single rounding equals convert-subtract-convert). Written
+  // out so that every caller rounds x itself, never a wider intermediate the
+  // compiler could fuse into the conversion.
+  uint32_t w;
+  asm("v_cvt_f16_f32 %0, %1\n\tv_fma_mixhi_f16 %0, -%0, 1.0, %1 op_sel_hi:[1,0,0]" : "=&v"(w) : "v"(x));
+  return w;
+}
+
+// Split-fp16 parts of two values as two words: hi = (fp16(p0), fp16(p1)) and
+// lo = (fp16(p0 - hi0), fp16(p1 - hi1)), each the low / high half.
+__device__ __forceinline__ void split_pair(float p0, float p1, uint32_t* hi, uint32_t* lo) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{p0, p1}, f16x2));
+  uint32_t l;  // high half written by the second instruction
+  asm("v_fma_mixlo_f16 %0, -%1, 1.0, %2 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, -%1, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(l)
+      : "v"(h), "v"(p0), "v"(p1));
+  *hi = h;
+  *lo = l;
 }
 
 // Non-negative IEEE floats order like their bit patterns, so an unsigned
