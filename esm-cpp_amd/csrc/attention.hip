@@ -511,13 +511,10 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     }
   };
 
-  for (int kc0 = 0; kc0 < L; kc0 += KCX) {
-    const int nkeys = min(KCX, L - kc0);
-    if (nkeys == KCX)
-      chunk(kc0, nkeys, std::true_type{});
-    else
-      chunk(kc0, nkeys, std::false_type{});
-  }
+  // Whole chunks, then the sequence's partial last chunk (if any).
+  int kc0 = 0;
+  for (; kc0 + KCX <= L; kc0 += KCX) chunk(kc0, KCX, std::true_type{});
+  if (kc0 < L) chunk(kc0, L - kc0, std::false_type{});
 
   if (!active) return;
 #pragma unroll
