@@ -1554,12 +1554,28 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   }
   ESM_TRY(ctx->time_end(slot));
   ESM_HIP(ctx, launch_layernorm(a.lm_a, nullptr, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr, s));
-  DevLinear dec;
-  dec.w32 = m->embed;
-  dec.bias = m->dec_bias;
-  dec.N = V;
-  dec.K = d;
-  ESM_TRY(f32_linear(ctx, a.attn, dec, logits, T, kF32Store));
+  if (V <= 48 && d % 16 == 0) {
+    // Tied decoder (vocabulary 33): the narrow fp32 MFMA kernel.
+    GemmF32Args g;
+    g.A = a.attn;
+    g.lda = d;
+    g.W = m->embed;
+    g.ldw = d;
+    g.bias = m->dec_bias;
+    g.C = logits;
+    g.ldc = V;
+    g.M = T;
+    g.N = V;
+    g.K = d;
+    ESM_HIP(ctx, launch_gemm_narrow(g, s));
+  } else {
+    DevLinear dec;
+    dec.w32 = m->embed;
+    dec.bias = m->dec_bias;
+    dec.N = V;
+    dec.K = d;
+    ESM_TRY(f32_linear(ctx, a.attn, dec, logits, T, kF32Store));
+  }
   return ESM_GFX950_OK;
 }
 

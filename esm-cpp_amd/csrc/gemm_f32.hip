@@ -273,7 +273,73 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_x3_kernel(const GemmX3Args p
   }
 }
 
+// ---- Narrow fp32 GEMM, N <= 48 (the tied decoder, d -> 33 logits): one wave
+// per 16 rows covers all 48 (padded) columns with v_mfma_f32_16x16x4f32.
+// Lane (r, g) = (lane % 16, lane / 16) loads a float4 of row r of A at
+// k = k0 + 4g and of rows r, r + 16, r + 32 of W; MFMA step j then multiplies
+// A[r][k0 + 4g + j] with W[c][k0 + 4g + j] for every lane group g, which sums
+// all 16 k of the stage over the four steps. W (N x K, 169 KB for the ESM
+// decoder) is re-read from L2 by every wave. K % 16 == 0.
+__global__ __launch_bounds__(256) void gemm_narrow_kernel(const GemmF32Args p) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 16;
+  if (row0 >= p.M) return;
+  const int r = lane & 15, g = lane >> 4;
+  const float* arow = p.A + static_cast<size_t>(min(row0 + r, p.M - 1)) * p.lda + 4 * g;
+  const float* wrow[3];
+  bool wok[3];
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int c = nb * 16 + r;
+    wok[nb] = c < p.N;
+    wrow[nb] = p.W + static_cast<size_t>(min(c, p.N - 1)) * p.ldw + 4 * g;
+  }
+  f32x4 acc[3];
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 a = *reinterpret_cast<const f32x4*>(arow);
+  f32x4 b[3];
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) b[nb] = *reinterpret_cast<const f32x4*>(wrow[nb]);
+  for (int k0 = 0; k0 < p.K; k0 += 16) {
+    f32x4 an = a, bn[3] = {b[0], b[1], b[2]};
+    if (k0 + 16 < p.K) {
+      an = *reinterpret_cast<const f32x4*>(arow + k0 + 16);
+#pragma unroll
+      for (int nb = 0; nb < 3; ++nb) bn[nb] = *reinterpret_cast<const f32x4*>(wrow[nb] + k0 + 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nb = 0; nb < 3; ++nb)
+        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], wok[nb] ? b[nb][j] : 0.0f, acc[nb], 0, 0, 0);
+    a = an;
+#pragma unroll
+    for (int nb = 0; nb < 3; ++nb) b[nb] = bn[nb];
+  }
+  // Output element i of block nb in lane (r, g): row row0 + 4g + i, column nb*16 + r.
+#pragma unroll
+  for (int nb = 0; nb < 3; ++nb) {
+    const int col = nb * 16 + r;
+    if (col >= p.N) continue;
+    const float bias = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + 4 * g + i;
+      if (row < p.M) p.C[static_cast<size_t>(row) * p.ldc + col] = acc[nb][i] + bias;
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_gemm_narrow(const GemmF32Args& p, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (p.N > 48 || p.K <= 0 || p.K % 16 != 0 || p.lda % 4 != 0 || p.ldw % 4 != 0) return hipErrorInvalidValue;
+  const int waves = (p.M + 15) / 16;
+  hipLaunchKernelGGL(gemm_narrow_kernel, dim3((waves + 3) / 4), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_x3(const GemmX3Args& p, int epi, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;

@@ -83,6 +83,9 @@ struct GemmF32Args {
   int M = 0, N = 0, K = 0;
 };
 hipError_t launch_gemm_f32(const GemmF32Args& p, int epilogue, hipStream_t s);
+// C = A W^T + bias for N <= 48 (the tied vocabulary decoder), fp32 MFMA, one
+// wave per 16 rows; K % 16 == 0, lda and ldw multiples of 4.
+hipError_t launch_gemm_narrow(const GemmF32Args& p, hipStream_t s);
 
 // FP32-accurate GEMM on fp16 MFMA ("split-fp16"): every operand x is carried
 // as hi = fp16(x) and lo = fp16(x - hi), and every product as hi*hi + lo*hi +
