@@ -419,12 +419,22 @@ __device__ __forceinline__ T* at(T* base, uint32_t off) {
   return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + off * static_cast<uint32_t>(sizeof(T)));
 }
 
+// Element of tile row R (wave-uniform) at the lane's byte offset: the row
+// address is scalar (SGPRs), the lane offset a loop-invariant VGPR, and a
+// constant column step becomes the store's immediate offset, so a store
+// needs no per-element address arithmetic.
+template <class T>
+__device__ __forceinline__ T* row_at(T* tile, uint32_t ldc, int R, uint32_t lane_byte) {
+  char* row = reinterpret_cast<char*>(tile) + static_cast<size_t>(static_cast<uint32_t>(R) * ldc) * sizeof(T);
+  return reinterpret_cast<T*>(row + lane_byte);
+}
+
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
 // rotary pair. hc: the head's first column relative to the tile origin.
 template <int BLK_M, int EPI, bool FULL, int WHICH>
 __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int g, int hc,
-                                         int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
+                                         int wr0, int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
                                          const float (&bs)[BLK_N], const float* s_cosT, const float* s_sinT, int m0,
                                          int n0) {
   constexpr int kRopeTPitch = Tile<BLK_M>::kRopeTPitch;
@@ -432,7 +442,8 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
   const uint32_t dm = p.d_model;
   // Row offsets: the lane's first row (lr0) times the stride once; the rest
   // of each row index is a compile-time constant times a uniform stride.
-  const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(hc + l32);
+  const uint32_t lane_b =
+      (static_cast<uint32_t>(lr0 - wr0) * ldc + static_cast<uint32_t>(hc + l32)) * 4u;  // 4-byte outputs
   const uint32_t lane_d = static_cast<uint32_t>(lr0) * dm + static_cast<uint32_t>(n0 + hc - WHICH * p.d_model + l32);
 #pragma unroll
   for (int i = 0; i < BLK_M; ++i)
@@ -469,19 +480,20 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
         // Offsets from the tile origin: unsigned 32-bit, so the store adds a
         // lane offset to a uniform base.
         const uint32_t dr = static_cast<uint32_t>(i * 32 + q * 8 + u);
-        const uint32_t off = lane_c + dr * ldc;
         if constexpr (EPI == kEpiQkvRopeF32) {
-          float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
-          *at(base, off) = x1;
-          *at(base, off + 32) = x2;
+          float* tile = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+          float* dst = row_at(tile, ldc, wr0 + static_cast<int>(dr), lane_b);
+          dst[0] = x1;
+          dst[32] = x2;
         } else if constexpr (EPI == kEpiQkvSplit) {
           if constexpr (WHICH == 0) {
             x1 *= p.q_prescale;
             x2 *= p.q_prescale;
           }
-          uint32_t* base = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc + n0;
-          __builtin_nontemporal_store(split_f16_word(x1), at(base, off));
-          __builtin_nontemporal_store(split_f16_word(x2), at(base, off + 32));
+          uint32_t* tile = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc + n0;
+          uint32_t* dst = row_at(tile, ldc, wr0 + static_cast<int>(dr), lane_b);
+          __builtin_nontemporal_store(split_f16_word(x1), dst);
+          __builtin_nontemporal_store(split_f16_word(x2), dst + 32);
         } else {
           // [M, d_model] outputs; column of the head inside its Q / K / V part.
           const uint32_t o = lane_d + dr * dm;
@@ -509,18 +521,23 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
   const int lc0 = wn * BLK_N * 32 + l32;
   const uint32_t ldc = p.ldc;
   auto col_ok = [&](int lc) { return FULL || n0 + lc < p.N; };
+  // Tile rows split into a wave-uniform part (wm's rows + block offsets) and
+  // the lane's half-wave offset hi * 4, which joins the lane's column in a
+  // per-lane byte offset.
+  const int wr0 = wm * BLK_M * 32;
   if constexpr (EPI == kEpiI32) {
-    int32_t* base = p.C_i32 + static_cast<size_t>(m0) * ldc + n0;
-    const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(lc0);
+    int32_t* tile = p.C_i32 + static_cast<size_t>(m0) * ldc + n0;
+    const uint32_t lane_b = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(lc0)) * 4u;
 #pragma unroll
     for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dr = i * 32 + (r >> 2) * 8 + (r & 3);
+        int32_t* dst = row_at(tile, ldc, wr0 + dr, lane_b);
 #pragma unroll
         for (int j = 0; j < BLK_N; ++j)
           if ((FULL || m0 + lr0 + dr < p.M) && col_ok(lc0 + j * 32))
-            __builtin_nontemporal_store(acc[i][j][r], at(base, lane_c + static_cast<uint32_t>(dr) * ldc + j * 32));
+            __builtin_nontemporal_store(acc[i][j][r], dst + j * 32);
       }
     return;
   } else {
@@ -538,16 +555,17 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
         if (!FULL && n0 + hc >= p.N) break;
         const int which = (n0 + hc) / p.d_model;
         if (which == 0)
-          qkv_head<BLK_M, EPI, FULL, 0>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 0>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else if (which == 1)
-          qkv_head<BLK_M, EPI, FULL, 1>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 1>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else
-          qkv_head<BLK_M, EPI, FULL, 2>(p, acc, g, hc, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, EPI, FULL, 2>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
     } else {
       float tmax = 0.0f;
       const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(lc0);
+      const uint32_t lane_b = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(lc0)) * 4u;
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
@@ -573,8 +591,8 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
                   uint16_t* base = p.C_f16 + static_cast<size_t>(m0) * ldc + n0;
                   *at(base, off) = f32_to_f16_bits(v);
                 } else {
-                  float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
-                  __builtin_nontemporal_store(v, at(base, off));
+                  float* tile = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+                  __builtin_nontemporal_store(v, row_at(tile, ldc, wr0 + i * 32 + q * 8 + u, lane_b) + j * 32);
                 }
                 if constexpr (MAX) rmax = fmaxf(rmax, fabsf(v));
               }
