@@ -72,6 +72,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   const AttnWork w = work[blockIdx.x];
   const int start = cu[w.seq];
   const int L = cu[w.seq + 1] - start;
+  if (w.q0 >= L) return;  // padding item of the work list (uniform)
   const int hoff = w.head * 64;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -320,6 +321,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   const AttnWork w = work[blockIdx.x];
   const int start = cu[w.seq];
   const int L = cu[w.seq + 1] - start;
+  if (w.q0 >= L) return;  // padding item of the work list (uniform)
   const int hoff = w.head * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;

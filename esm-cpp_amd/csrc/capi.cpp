@@ -154,22 +154,53 @@ int validate_batch(esm_gfx950_ctx* ctx, const int32_t* cu, int batch_size, long 
 
 // Work list for the attention kernels: (sequence, head, query tile), longest
 // sequences first so the long tiles start early and the short ones fill in.
-void build_work(const int32_t* cu, int B, int H, int qtile, std::vector<AttnWork>* out) {
+//
+// xcd_queues: workgroup i runs on XCD i % 8 (the dispatcher's round-robin),
+// and each XCD has its own L2. The list is then laid out as 8 interleaved
+// queues (item i belongs to queue i % 8); every (sequence, head) goes whole
+// to the shortest queue, so its query tiles run on one XCD back to back and
+// the later tiles re-read that head's K / V from that XCD's L2 instead of
+// HBM. Queues are padded to equal length with items whose q0 lies past every
+// sequence (the kernels return at once for those).
+constexpr int kNumXcd = 8;
+constexpr int kNoQueries = 1 << 30;
+
+void build_work(const int32_t* cu, int B, int H, int qtile, std::vector<AttnWork>* out, bool xcd_queues = false) {
   std::vector<int> order(B);
   std::iota(order.begin(), order.end(), 0);
   std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
     return (cu[a + 1] - cu[a]) > (cu[b + 1] - cu[b]);
   });
   out->clear();
+  if (!xcd_queues) {
+    for (int b : order) {
+      const int L = cu[b + 1] - cu[b];
+      for (int q0 = 0; q0 < L; q0 += qtile)
+        for (int h = 0; h < H; ++h) out->push_back(AttnWork{b, h, q0, 0});
+    }
+    return;
+  }
+  std::vector<AttnWork> queue[kNumXcd];
   for (int b : order) {
     const int L = cu[b + 1] - cu[b];
-    for (int q0 = 0; q0 < L; q0 += qtile)
-      for (int h = 0; h < H; ++h) out->push_back(AttnWork{b, h, q0, 0});
+    for (int h = 0; h < H; ++h) {
+      int x = 0;
+      for (int y = 1; y < kNumXcd; ++y)
+        if (queue[y].size() < queue[x].size()) x = y;
+      for (int q0 = 0; q0 < L; q0 += qtile) queue[x].push_back(AttnWork{b, h, q0, 0});
+    }
   }
+  size_t n = 0;
+  for (const auto& qu : queue) n = std::max(n, qu.size());
+  if (n == 0) return;
+  for (auto& qu : queue) qu.resize(n, AttnWork{order[0], 0, kNoQueries, 0});
+  out->reserve(n * kNumXcd);
+  for (size_t i = 0; i < n; ++i)
+    for (const auto& qu : queue) out->push_back(qu[i]);
 }
 
 size_t max_work_items(int B, int T, int H, int qtile) {
-  return static_cast<size_t>(H) * (static_cast<size_t>(B) + static_cast<size_t>(T) / qtile + 1);
+  return static_cast<size_t>(H) * (static_cast<size_t>(B) + static_cast<size_t>(T) / qtile + 1) + kNumXcd;
 }
 
 // Position of every packed token inside its sequence.
@@ -553,9 +584,9 @@ namespace {
 // Uploads cu_seqlens and the work list into op scratch (after `reserve`
 // bytes used by the caller) and returns device pointers.
 int stage_attention_meta(esm_gfx950_ctx* ctx, const int* cu, int B, int H, int qtile, size_t reserve,
-                         int** d_cu, AttnWork** d_work, int* nwork) {
+                         int** d_cu, AttnWork** d_work, int* nwork, bool xcd_queues) {
   std::vector<AttnWork> work;
-  build_work(cu, B, H, qtile, &work);
+  build_work(cu, B, H, qtile, &work, xcd_queues);
   const size_t cu_bytes = align_up(static_cast<size_t>(B + 1) * 4, 256);
   const size_t wbytes = work.size() * sizeof(AttnWork);
   void* s = nullptr;
@@ -587,7 +618,8 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     int* d_cu;
     AttnWork* d_work;
     int nwork;
-    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnF32QTile, 0, &d_cu, &d_work, &nwork));
+    ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnF32QTile, 0, &d_cu, &d_work, &nwork,
+                                 false));
     ESM_HIP(ctx, launch_attention_f32(q, k, v, ld, head_dim, d_cu, d_work, nwork, out, ld, ctx->stream));
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
@@ -604,7 +636,7 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     AttnWork* d_work;
     int nwork;
     ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 3 * wbytes, &d_cu, &d_work,
-                                 &nwork));
+                                 &nwork, true));
     char* base = static_cast<char*>(ctx->scratch);
     auto* qw = reinterpret_cast<uint32_t*>(base);
     auto* kw = reinterpret_cast<uint32_t*>(base + wbytes);
@@ -625,7 +657,7 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
   AttnWork* d_work;
   int nwork;
   ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 3 * cbytes, &d_cu, &d_work,
-                               &nwork));
+                               &nwork, true));
   char* base = static_cast<char*>(ctx->scratch);
   auto* qb = reinterpret_cast<uint16_t*>(base);
   auto* kb = reinterpret_cast<uint16_t*>(base + cbytes);
@@ -650,7 +682,8 @@ extern "C" int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint1
   int* d_cu;
   AttnWork* d_work;
   int nwork;
-  ESM_TRY(stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork));
+  ESM_TRY(
+      stage_attention_meta(ctx, cu_seqlens, batch_size, num_heads, kAttnMfmaQTile, 0, &d_cu, &d_work, &nwork, true));
   const int ld = num_heads * kHeadDimMfma;
   int slot;
   ESM_TRY(ctx->time_begin("attention", &slot));
@@ -1484,7 +1517,7 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
   build_pos(mh.cu, B, mh.pos);
   const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
   std::vector<AttnWork> work;
-  build_work(mh.cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work);
+  build_work(mh.cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work, mfma_attn);
   std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));
   const bool new_tables = P.rope_len < maxL;
   if (new_tables) rope_tables(P.cap_L, dh, mh.cos_t, mh.sin_t);
