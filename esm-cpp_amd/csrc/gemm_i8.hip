@@ -369,7 +369,7 @@ constexpr int kThreads = WAVES_M * WAVES_N * 64;  // 512
 // Tile height: BLK_M 32x32 row blocks per wave, BM = 64 * BLK_M rows (4: 256,
 // 5: 320). The launcher picks the height that needs the fewer rows' worth of
 // workgroup rounds over the CUs (a 256-row grid that spills a few tiles into
-// one more round often fits in fewer rounds as 320-row tiles).
+// one more round often fits in fewer rounds as 320-row tiles), 320 on a tie.
 template <int BLK_M_>
 struct Tile {
   static constexpr int BLK_M = BLK_M_;
@@ -817,12 +817,15 @@ long tile_cost(int M, int N, int BM, int cus) {
 hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
   int rows = g_tile_rows.load(std::memory_order_relaxed);
   if (rows == 0) {
-    // The 320-row tile is chosen automatically only for the plain epilogues:
-    // with BLK_M = 5 the GELU and QKV epilogues exceed 256 VGPRs and spill.
-    const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid;
+    // Ties go to 320 rows: at equal rounds the taller tile re-reads less of
+    // A and W (fc1 at config 4: 270 vs 282 us). The GELU and bf16/fp32 RoPE
+    // epilogues stay at 256 rows: at BLK_M = 5 they exceed 256 VGPRs. The
+    // split-word QKV epilogue spills 72 bytes there too, but runs faster at
+    // 320 rows all the same (216 vs 224 us at config 4).
+    const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit;
     const int cus = device_cus();
-    rows = tall_ok && tile_cost(p.M, p.N, v3::Tile<5>::BM, cus) < tile_cost(p.M, p.N, v3::Tile<4>::BM, cus) ? 320
-                                                                                                          : 256;
+    rows = tall_ok && tile_cost(p.M, p.N, v3::Tile<5>::BM, cus) <= tile_cost(p.M, p.N, v3::Tile<4>::BM, cus) ? 320
+                                                                                                           : 256;
   }
   return rows == 320 ? launch_v3_tile<5>(p, epi, s) : launch_v3_tile<4>(p, epi, s);
 }
