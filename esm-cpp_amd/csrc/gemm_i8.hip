@@ -391,6 +391,21 @@ __device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds) {
 #endif
 }
 
+// The same 16-byte global -> LDS load, issued from inline asm: M0 holds the
+// wave's LDS destination (uniform), and one wait state separates the M0
+// write from the load. The compiler's wait insertion does not see this
+// write to LDS, so it does not hold the fragment reads of the other stage
+// buffer until these loads complete (it cannot tell the two buffers apart
+// and would). Completion is awaited explicitly: s_waitcnt vmcnt(0) and a
+// barrier before the stage is read.
+__device__ __forceinline__ void dma16_async(const int8_t* g, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v) : "memory", "m0");
+#endif
+}
+
 __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
@@ -668,7 +683,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   int8_t* ldst = smem + wave * kPer * 1024;
   const int nk = p.K / BK;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) dma16(gp[i], ldst + i * 1024);
+  for (int i = 0; i < kPer; ++i) dma16_async(gp[i], ldst + i * 1024);
 
   i32x16 acc[BLK_M][BLK_N];
 #pragma unroll
@@ -686,7 +701,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     if (kt + 1 < nk) {
       int8_t* dst = ldst + ((kt + 1) & 1) * kStage;
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) dma16(gp[i] + (kt + 1) * BK, dst + i * 1024);
+      for (int i = 0; i < kPer; ++i) dma16_async(gp[i] + (kt + 1) * BK, dst + i * 1024);
     }
     const int8_t* cur = smem + (kt & 1) * kStage;
 #pragma unroll
