@@ -383,21 +383,15 @@ struct Tile {
   static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
-#endif
-}
-
-// The same 16-byte global -> LDS load, issued from inline asm: M0 holds the
-// wave's LDS destination (uniform), and one wait state separates the M0
-// write from the load. The compiler's wait insertion does not see this
-// write to LDS, so it does not hold the fragment reads of the other stage
-// buffer until these loads complete (it cannot tell the two buffers apart
-// and would). Completion is awaited explicitly: s_waitcnt vmcnt(0) and a
-// barrier before the stage is read.
+// One 16-byte-per-lane global -> LDS load (global_load_lds_dwordx4), issued
+// from inline asm: M0 holds the wave's LDS destination (uniform), and one
+// wait state separates the M0 write from the load. Issued through the
+// compiler builtin instead, the compiler's wait insertion would hold the
+// fragment reads of the other stage buffer until these loads complete (it
+// cannot tell the two buffers apart), which serialises the double buffer.
+// Completion is awaited explicitly: s_waitcnt vmcnt(0) and a barrier before
+// a stage is read.
 __device__ __forceinline__ void dma16_async(const int8_t* g, int8_t* lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(
