@@ -1,6 +1,11 @@
-// W8A8 INT8 GEMM for gfx950: v_mfma_i32_16x16x64_i8 with int32
-// accumulation and fused epilogues (dequant + bias, GELU, residual add,
-// QKV split with Q-scale and rotary embedding).
+// W8A8 INT8 GEMM for gfx950 with int32 accumulation and fused epilogues
+// (dequant + bias, GELU, residual add, QKV split with Q-scale and rotary
+// embedding). Two kernels:
+//   - gemm_i8_v3_kernel (namespace v3 below): the main path whenever K is a
+//     multiple of 128 and rows are 16-byte aligned -- v_mfma_i32_32x32x32_i8,
+//     256x256 or 320x256 tiles, direct global -> LDS stage loads;
+//   - gemm_i8_kernel (TileCfg, described next): the general fallback for any
+//     other shape, v_mfma_i32_16x16x64_i8.
 //
 // Replaces the inner product of esm::kernels::LinearInt8
 // (reference src/kernels/gemm_int8.cpp:510-555 LinearVnni and
@@ -10,7 +15,7 @@
 // a per-row activation scale, which equals the per-tensor scale when every
 // row carries the tensor's scale.
 //
-// Tiling (TileCfg): a 256-thread workgroup owns a 256x128 output tile; its
+// Fallback tiling (TileCfg): a 256-thread workgroup owns a 256x128 output tile; its
 // four waves (2x2) each own 128x64 = 8x4 MFMA blocks of 16x16, so a wave
 // reads 12 fragments (192 B per lane) from LDS per 32 MFMAs. K advances 64
 // bytes per stage; A and W stages go global -> registers -> LDS, double-
