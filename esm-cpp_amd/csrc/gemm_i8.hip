@@ -405,6 +405,17 @@ __device__ __forceinline__ void dma16_async(const int8_t* g, int8_t* lds) {
 #endif
 }
 
+// The same load addressed as a wave-uniform base (SGPRs) plus a 32-bit lane
+// offset: one VGPR per load instead of a 64-bit address pair.
+__device__ __forceinline__ void dma16_async_so(const int8_t* base, uint32_t off, int8_t* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)lds)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0v)
+               : "memory", "m0");
+#endif
+}
+
 __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
@@ -669,7 +680,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   // Load blocks wave*kPer .. +kPer of each stage: blocks [0, BM/8) are A row
   // groups, the rest W row groups. Rows past the edge re-read the last valid
   // row (their products are never stored).
-  const int8_t* gp[kPer];
+  // Source of block i: a wave-uniform base (A or W) plus a 32-bit lane
+  // offset (operands are far below 4 GiB).
+  uint32_t goff[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int b = wave * kPer + i;
@@ -677,12 +690,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     const int c = (lane & 7) ^ r ^ (b & 1);
     const bool is_a = b < BM / 8;
     const int row = is_a ? min(m0 + b * 8 + r, p.M - 1) : min(n0 + (b - BM / 8) * 8 + r, p.N - 1);
-    gp[i] = (is_a ? p.A + static_cast<size_t>(row) * p.lda : p.W + static_cast<size_t>(row) * p.ldw) + c * 16;
+    goff[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? p.lda : p.ldw) + c * 16;
   }
+  auto gbase = [&](int i) { return wave * kPer + i < BM / 8 ? p.A : p.W; };
   int8_t* ldst = smem + wave * kPer * 1024;
   const int nk = p.K / BK;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) dma16_async(gp[i], ldst + i * 1024);
+  for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i), goff[i], ldst + i * 1024);
 
   i32x16 acc[BLK_M][BLK_N];
 #pragma unroll
@@ -700,7 +714,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     if (kt + 1 < nk) {
       int8_t* dst = ldst + ((kt + 1) & 1) * kStage;
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) dma16_async(gp[i] + (kt + 1) * BK, dst + i * 1024);
+      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + 1) * BK, goff[i], dst + i * 1024);
     }
     const int8_t* cur = smem + (kt & 1) * kStage;
 #pragma unroll
@@ -847,8 +861,12 @@ hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
 }  // namespace
 
 bool gemm_i8_pipelined_ok(const GemmI8Args& p) {
+  // The stage loads address A and W with 32-bit lane offsets.
+  constexpr uint64_t kOffsetLimit = 1ull << 32;
   return p.K > 0 && p.K % v3::BK == 0 && p.lda % 16 == 0 && p.ldw % 16 == 0 && p.lda >= p.K && p.ldw >= p.K &&
-         reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && reinterpret_cast<uintptr_t>(p.W) % 16 == 0;
+         reinterpret_cast<uintptr_t>(p.A) % 16 == 0 && reinterpret_cast<uintptr_t>(p.W) % 16 == 0 &&
+         static_cast<uint64_t>(p.M) * static_cast<uint64_t>(p.lda) <= kOffsetLimit &&
+         static_cast<uint64_t>(p.N) * static_cast<uint64_t>(p.ldw) <= kOffsetLimit;
 }
 
 hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epi, int variant, hipStream_t s) {

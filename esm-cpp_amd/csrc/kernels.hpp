@@ -56,7 +56,8 @@ struct GemmI8Args {
 };
 
 // Picks the pipelined 256- or 320-row-tile kernel when gemm_i8_pipelined_ok(p) (K a
-// multiple of 128, 16-byte aligned rows), else the general 256x128 kernel.
+// multiple of 128, 16-byte aligned rows, M*lda and N*ldw at most 2^32 bytes),
+// else the general 256x128 kernel.
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epilogue, hipStream_t s);
 bool gemm_i8_pipelined_ok(const GemmI8Args& p);
 // variant 1: general kernel; 2: pipelined kernel (fails on shapes it cannot take).
