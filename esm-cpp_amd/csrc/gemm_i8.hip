@@ -388,7 +388,6 @@ struct Tile {
   static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
 };
 
-
 // One 16-byte-per-lane global -> LDS load (global_load_lds_dwordx4), issued
 // from inline asm: M0 holds the wave's LDS destination (uniform), and one
 // wait state separates the M0 write from the load. Issued through the
@@ -396,24 +395,21 @@ struct Tile {
 // fragment reads of the other stage buffer until these loads complete (it
 // cannot tell the two buffers apart), which serialises the double buffer.
 // Completion is awaited explicitly: s_waitcnt vmcnt(0) and a barrier before
-// a stage is read.
-__device__ __forceinline__ void dma16_async(const int8_t* g, int8_t* lds) {
+// a stage is read. The load is addressed as a wave-uniform base (SGPRs) plus
+// a 32-bit lane offset: one VGPR per load instead of a 64-bit address pair.
+// `lds` is the destination's LDS byte address.
+__device__ __forceinline__ void dma16_async_so(const int8_t* base, uint32_t off, uint32_t lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t m0v = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)lds)));
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v) : "memory", "m0");
-#endif
-}
-
-// The same load addressed as a wave-uniform base (SGPRs) plus a 32-bit lane
-// offset: one VGPR per load instead of a 64-bit address pair.
-__device__ __forceinline__ void dma16_async_so(const int8_t* base, uint32_t off, int8_t* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t m0v = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) int8_t*)lds)));
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0v)
                : "memory", "m0");
 #endif
+}
+
+// LDS byte address of a __shared__ object (one address-space cast, made
+// once, instead of a null-checked cast per load).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
 
 __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
@@ -693,7 +689,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     goff[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? p.lda : p.ldw) + c * 16;
   }
   auto gbase = [&](int i) { return wave * kPer + i < BM / 8 ? p.A : p.W; };
-  int8_t* ldst = smem + wave * kPer * 1024;
+  const uint32_t ldst = lds_addr(smem) + static_cast<uint32_t>(wave * kPer * 1024);
   const int nk = p.K / BK;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i), goff[i], ldst + i * 1024);
@@ -712,7 +708,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (kt + 1 < nk) {
-      int8_t* dst = ldst + ((kt + 1) & 1) * kStage;
+      const uint32_t dst = ldst + ((kt + 1) & 1) * kStage;
 #pragma unroll
       for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + 1) * BK, goff[i], dst + i * 1024);
     }
