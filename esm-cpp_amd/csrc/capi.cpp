@@ -11,6 +11,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <numeric>
 #include <string>
@@ -199,8 +200,16 @@ void build_work(const int32_t* cu, int B, int H, int qtile, std::vector<AttnWork
     for (const auto& qu : queue) out->push_back(qu[i]);
 }
 
-size_t max_work_items(int B, int T, int H, int qtile) {
-  return static_cast<size_t>(H) * (static_cast<size_t>(B) + static_cast<size_t>(T) / qtile + 1) + kNumXcd;
+// Upper bound of build_work's item count for B sequences of T tokens in
+// all, the longest maxL tokens. Before padding there are at most
+// H * (T / qtile + B) items (one per started query tile). Every (sequence,
+// head) goes to the shortest queue, so no queue exceeds the mean by more
+// than one (sequence, head)'s tiles, ceil(maxL / qtile); padding all
+// kNumXcd queues to the longest adds at most kNumXcd times that.
+size_t max_work_items(int B, int T, int maxL, int H, int qtile) {
+  const size_t tiles_max = static_cast<size_t>(maxL) / qtile + 1;
+  return static_cast<size_t>(H) * (static_cast<size_t>(B) + static_cast<size_t>(T) / qtile + 1) +
+         kNumXcd * (tiles_max + 1);
 }
 
 // Position of every packed token inside its sequence.
@@ -561,6 +570,27 @@ extern "C" int esm_gfx950_rope_build_tables(int seq_len, int head_dim, float* co
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_attention_work_items(const int32_t* cu_seqlens, int batch_size, int num_heads, int mfma,
+                                               size_t* items, size_t* capacity) {
+  if (!cu_seqlens || batch_size < 1 || num_heads < 1 || !items || !capacity) return ESM_GFX950_INVALID_ARGUMENT;
+  int maxL = 0;
+  for (int b = 0; b < batch_size; ++b) {
+    if (cu_seqlens[b + 1] < cu_seqlens[b]) return ESM_GFX950_INVALID_ARGUMENT;
+    maxL = std::max(maxL, cu_seqlens[b + 1] - cu_seqlens[b]);
+  }
+  const int T = cu_seqlens[batch_size] - cu_seqlens[0];
+  std::vector<AttnWork> work;
+  try {
+    build_work(cu_seqlens, batch_size, num_heads, mfma ? kAttnMfmaQTile : kAttnF32QTile, &work, mfma != 0);
+  } catch (const std::exception&) {
+    return ESM_GFX950_INTERNAL;
+  }
+  *items = work.size();
+  *capacity = std::max(max_work_items(batch_size, T, maxL, num_heads, kAttnMfmaQTile),
+                       max_work_items(batch_size, T, maxL, num_heads, kAttnF32QTile));
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_rope_apply_varlen(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
                                             const int* cu_seqlens, int batch_size, int num_heads,
                                             int head_dim) {
@@ -902,6 +932,12 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
                 "model_create: MFMA attention needs head_dim 64 (use ESM_GFX950_ATTN_MODE_FP32)");
     ESM_REQUIRE(ctx, c.hidden_size % 4 == 0 && c.hidden_size <= 2560,
                 "model_create: fused LayerNorm+quant supports hidden_size % 4 == 0 and <= 2560");
+    // The split-fp16 QKV epilogue exists only in the pipelined GEMM, which
+    // needs K = hidden_size to be a multiple of 128.
+    ESM_REQUIRE(ctx, c.attention_mode != ESM_GFX950_ATTN_MODE_F16X3 || c.hidden_size % 128 == 0,
+                "model_create: ESM_GFX950_ATTN_MODE_F16X3 needs hidden_size % 128 == 0 (use another attention_mode)");
+    ESM_REQUIRE(ctx, c.act_quant_mode != ESM_GFX950_ACT_PER_TOKEN || c.intermediate_size <= 10240,
+                "model_create: per-token activation scales support intermediate_size <= 10240");
   }
   ESM_REQUIRE(ctx, desc->layers || c.num_layers == 0, "model_create: null layers");
   auto* m = new esm_gfx950_model();
@@ -974,6 +1010,9 @@ extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_mod
   if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_REQUIRE(ctx, act_mode == ESM_GFX950_ACT_PER_TENSOR || act_mode == ESM_GFX950_ACT_PER_TOKEN,
               "model_set_act_mode: unknown mode");
+  ESM_REQUIRE(ctx, act_mode != ESM_GFX950_ACT_PER_TOKEN || !model->cfg.weights_int8 ||
+                       model->cfg.intermediate_size <= 10240,
+              "model_set_act_mode: per-token activation scales support intermediate_size <= 10240");
   model->cfg.act_quant_mode = act_mode;
   return ESM_GFX950_OK;
 }
@@ -1061,6 +1100,7 @@ struct Meta {
   int32_t* pos;
   int32_t* cu;
   AttnWork* work;
+  size_t work_cap;  // work items the region holds
   float* cos_t;
   float* sin_t;
   size_t bytes;
@@ -1078,8 +1118,8 @@ Meta meta_layout(int T, int B, int maxL, int H, int dh, char* base) {
   m.tok_scale = reinterpret_cast<float*>(take(static_cast<size_t>(T) * 4));
   m.pos = reinterpret_cast<int32_t*>(take(static_cast<size_t>(T) * 4));
   m.cu = reinterpret_cast<int32_t*>(take(static_cast<size_t>(B + 1) * 4));
-  const size_t nw = std::max(max_work_items(B, T, H, kAttnMfmaQTile), max_work_items(B, T, H, kAttnF32QTile));
-  m.work = reinterpret_cast<AttnWork*>(take(nw * sizeof(AttnWork)));
+  m.work_cap = std::max(max_work_items(B, T, maxL, H, kAttnMfmaQTile), max_work_items(B, T, maxL, H, kAttnF32QTile));
+  m.work = reinterpret_cast<AttnWork*>(take(m.work_cap * sizeof(AttnWork)));
   m.cos_t = reinterpret_cast<float*>(take(static_cast<size_t>(maxL) * dh * 4));
   m.sin_t = reinterpret_cast<float*>(take(static_cast<size_t>(maxL) * dh * 4));
   m.bytes = off;
@@ -1110,6 +1150,10 @@ class ObsRun {
  public:
   ObsRun(esm_gfx950_observer* o, std::vector<ObsSite> sites) : obs_(o), sites_(std::move(sites)) {
     done_.assign(sites_.size(), 0);
+    // Test hook for the failure path: ESM_GFX950_TEST_OBSERVER_FAIL_SITE=k
+    // makes the capture of site k (0-based, forward order) fail on the host
+    // after the kernels before it have been enqueued.
+    if (const char* e = std::getenv("ESM_GFX950_TEST_OBSERVER_FAIL_SITE")) fail_site_ = std::strtol(e, nullptr, 10);
     size_t workers = std::thread::hardware_concurrency();
     if (const char* e = std::getenv("ESM_NUM_THREADS")) workers = std::strtoul(e, nullptr, 10);
     workers = std::max<size_t>(1, std::min<size_t>({workers, 16, sites_.size()}));
@@ -1157,6 +1201,9 @@ class ObsRun {
   int capture(esm_gfx950_ctx* ctx, const float* x, size_t n, int gelu) {
     if (next_ >= sites_.size() || sites_[next_].n != n)
       return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: site sequence mismatch");
+    if (fail_site_ >= 0 && static_cast<size_t>(fail_site_) == next_)
+      return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: failure injected at site " +
+                                                std::to_string(fail_site_) + " (test hook)");
     const size_t k = next_++;
     {
       std::unique_lock<std::mutex> lk(mu_);
@@ -1197,6 +1244,7 @@ class ObsRun {
   std::vector<std::thread> threads_;
   size_t taken_ = 0;
   size_t next_ = 0;
+  long fail_site_ = -1;
 };
 
 // One pre-LN encoder layer on the device (reference TransformerBlock,
@@ -1263,6 +1311,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     g.C_f32 = a.qkv;
     g.ldc = 3 * d;
     g.q_prescale = kQPrescale;
+    if (!gemm_i8_pipelined_ok(g))
+      return ctx->fail(ESM_GFX950_OUT_OF_RANGE,
+                       "forward: the split-fp16 QKV epilogue needs T * hidden_size <= 2^32 bytes; use a smaller "
+                       "batch or another attention_mode");
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvSplit, s));
   } else if (f32qkv && dh == kHeadDimMfma) {
     // Dequant + bias, Q scale and RoPE fused; fp32 Q|K|V rows.
@@ -1518,6 +1570,10 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
   const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
   std::vector<AttnWork> work;
   build_work(mh.cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work, mfma_attn);
+  if (work.size() > mh.work_cap)
+    return ctx->fail(ESM_GFX950_INTERNAL, "batch_upload: attention work list (" + std::to_string(work.size()) +
+                                              " items) exceeds its metadata region (" +
+                                              std::to_string(mh.work_cap) + ")");
   std::memcpy(mh.work, work.data(), work.size() * sizeof(AttnWork));
   const bool new_tables = P.rope_len < maxL;
   if (new_tables) rope_tables(P.cap_L, dh, mh.cos_t, mh.sin_t);
@@ -1826,22 +1882,31 @@ extern "C" int esm_gfx950_observer_observe(esm_gfx950_ctx* ctx, esm_gfx950_obser
   ESM_REQUIRE(ctx, values, "observer_observe: null values");
   if (n >= UINT32_MAX) return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "observer_observe: more than 2^32 - 2 values");
   ESM_TRY(reserve_observer(ctx, obs, 1));
+  // Planned on a copy of the site's reservoir; the copy replaces the site
+  // only once the gathered values are in, so a failed call changes nothing.
   size_t count = 0;
   std::vector<uint32_t> slots;
-  obs::Reservoir* r = nullptr;
+  obs::Reservoir r;
   try {
-    r = &obs->sites[site];
+    auto it = obs->sites.find(site);
+    if (it != obs->sites.end()) r = it->second;
     slots.resize(obs::kReservoirSize);
-    count = obs::plan(*r, n, slots.data(), obs->h_pos);
+    count = obs::plan(r, n, slots.data(), obs->h_pos);
   } catch (const std::exception& e) {
     return ctx->fail(ESM_GFX950_INTERNAL, std::string("observer_observe: ") + e.what());
   }
-  if (count == 0) return ESM_GFX950_OK;
-  ESM_HIP(ctx, hipMemcpyAsync(obs->d_pos, obs->h_pos, count * 4, hipMemcpyHostToDevice, ctx->stream));
-  ESM_HIP(ctx, launch_observe_gather(values, obs->d_pos, static_cast<int>(count), 0, obs->d_val, ctx->stream));
-  ESM_HIP(ctx, hipMemcpyAsync(obs->h_val, obs->d_val, count * 4, hipMemcpyDeviceToHost, ctx->stream));
-  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  for (size_t w = 0; w < count; ++w) r->samples[slots[w]] = obs->h_val[w];
+  if (count > 0) {
+    ESM_HIP(ctx, hipMemcpyAsync(obs->d_pos, obs->h_pos, count * 4, hipMemcpyHostToDevice, ctx->stream));
+    ESM_HIP(ctx, launch_observe_gather(values, obs->d_pos, static_cast<int>(count), 0, obs->d_val, ctx->stream));
+    ESM_HIP(ctx, hipMemcpyAsync(obs->h_val, obs->d_val, count * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (size_t w = 0; w < count; ++w) r.samples[slots[w]] = obs->h_val[w];
+  }
+  try {
+    obs->sites[site] = std::move(r);
+  } catch (const std::exception& e) {
+    return ctx->fail(ESM_GFX950_INTERNAL, std::string("observer_observe: ") + e.what());
+  }
   return ESM_GFX950_OK;
 }
 
@@ -1860,6 +1925,23 @@ extern "C" int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_
   if (Tf >= UINT32_MAX) return ctx->fail(ESM_GFX950_OUT_OF_RANGE, "forward_with_observer: batch too large");
   const size_t nsites = 4 * m->layers.size();
   ESM_TRY(reserve_observer(ctx, obs, nsites));
+  // The reservoirs advance while the forward runs (the host plans each
+  // site ahead of the device); a call that fails part-way puts back the
+  // state it started from, so later percentiles are unaffected.
+  struct Restore {
+    esm_gfx950_observer* o;
+    std::map<std::string, obs::Reservoir> before;
+    bool done = false;
+    ~Restore() {
+      if (!done) o->sites.swap(before);
+    }
+  };
+  std::unique_ptr<Restore> restore;
+  try {
+    restore.reset(new Restore{obs, obs->sites});
+  } catch (const std::exception& e) {
+    return ctx->fail(ESM_GFX950_INTERNAL, std::string("forward_with_observer: ") + e.what());
+  }
   std::vector<ObsSite> sites(nsites);
   try {
     for (size_t l = 0; l < m->layers.size(); ++l)
@@ -1879,10 +1961,17 @@ extern "C" int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_
   StreamScope scope(ctx, P.stream);
   ObsRun run(obs, std::move(sites));
   const Arena a = layout(c, P.cap_T, static_cast<char*>(P.arena));
-  ESM_TRY(forward_part(ctx, m, P, a.logits, &run));
+  const int rc = forward_part(ctx, m, P, a.logits, &run);
+  if (rc != ESM_GFX950_OK) {
+    // Whatever was enqueued completes before the reservoirs are restored.
+    hipStreamSynchronize(ctx->stream);
+    return rc;
+  }
   ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * c.vocab_size * 4, hipMemcpyDeviceToHost,
                               ctx->stream));
-  return run.finish(ctx);
+  ESM_TRY(run.finish(ctx));
+  restore->done = true;
+  return ESM_GFX950_OK;
 }
 
 // ---------------------------------------------------------------- scheduler

@@ -48,6 +48,7 @@ EXPORTED = [
     "esm_gfx950_model_set_first_block_fc1_fp16", "esm_gfx950_observer_create", "esm_gfx950_observer_free",
     "esm_gfx950_observer_clear", "esm_gfx950_observer_observe", "esm_gfx950_observer_site_count",
     "esm_gfx950_observer_site_name", "esm_gfx950_observer_percentile", "esm_gfx950_forward_with_observer",
+    "esm_gfx950_attention_work_items",
 ]
 
 
@@ -100,6 +101,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_scale": (i32, [vp, vp, sz, f32]),
         "esm_gfx950_rope_build_tables": (i32, [i32, i32, vp, vp]),
         "esm_gfx950_rope_apply_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+        "esm_gfx950_attention_work_items": (i32, [vp, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)]),
         "esm_gfx950_attention_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp, i32]),
         "esm_gfx950_attention_varlen_bf16": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, vp]),
         "esm_gfx950_model_create": (i32, [vp, vp, C.POINTER(vp)]),
@@ -151,6 +153,19 @@ def rope_build_tables(seq_len: int, head_dim: int):
     if rc != OK:
         raise Gfx950Error(rc, "rope_build_tables")
     return cos[:seq_len], sin[:seq_len]
+
+
+def attention_work_items(cu: np.ndarray, num_heads: int, mfma: bool = True):
+    """(items, capacity): the attention work items a batch produces and the
+    number the model's per-batch metadata reserves (host only)."""
+    lib = load_library()
+    cu = np.ascontiguousarray(cu, np.int32)
+    items, cap = C.c_size_t(), C.c_size_t()
+    rc = lib.esm_gfx950_attention_work_items(_ptr(cu), int(cu.size - 1), int(num_heads), int(mfma), C.byref(items),
+                                             C.byref(cap))
+    if rc:
+        raise Gfx950Error(rc, "attention_work_items: invalid arguments")
+    return int(items.value), int(cap.value)
 
 
 def plan_batches(lengths, max_batch_size: int = 256, imbalance_threshold: float = 1.2):

@@ -188,6 +188,14 @@ int esm_gfx950_scale(esm_gfx950_ctx* ctx, float* x, size_t n, float scale);
  * host-side: cos/sin [seq_len, head_dim] half-then-half tables written to
  * HOST memory with the reference formula. */
 int esm_gfx950_rope_build_tables(int seq_len, int head_dim, float* cos_out, float* sin_out);
+/* Host only, no counterpart in the reference (whose AttentionVarlen
+ * parallelises over (sequence, head) with no work list): the number of
+ * attention work items a batch with these cu_seqlens produces (mfma != 0:
+ * the MFMA kernels' per-XCD queues of 128-query tiles; 0: the fp32 kernel's
+ * list) and the number the model's per-batch metadata region reserves for
+ * them (items <= capacity for every valid batch). */
+int esm_gfx950_attention_work_items(const int32_t* cu_seqlens, int batch_size, int num_heads, int mfma,
+                                    size_t* items, size_t* capacity);
 /* esm::kernels::RopeApplyVarlen (kernels.h:84-92; rope.cpp:47-70):
  * x fp32 [T, H, head_dim] rotated in place with device tables cos/sin
  * [max_seqlen, head_dim]; positions restart at each cu_seqlens boundary.
@@ -334,8 +342,8 @@ int esm_gfx950_forward_scheduled(esm_gfx950_ctx* ctx, esm_gfx950_model* model, c
  * per site, std::uniform_int_distribution over [0, total_seen]), so that the
  * same sequence of calls keeps the same positions. The host draws which
  * positions survive; only those values are gathered from the device. Not
- * thread-safe (one call at a time, like the reference). After a failed call
- * the observer's contents are unspecified: clear it. */
+ * thread-safe (one call at a time, like the reference). A call that fails
+ * leaves every site as it was before the call. */
 int esm_gfx950_observer_create(esm_gfx950_ctx* ctx, esm_gfx950_observer** out);
 int esm_gfx950_observer_free(esm_gfx950_ctx* ctx, esm_gfx950_observer* obs);
 /* ActivationObserver::Clear (observer.cpp:51): every site removed. */

@@ -46,3 +46,25 @@ def test_product_does_not_reference_oracle():
             if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "pyoracle" not in text and "liboracle" not in text and "libesmref" not in text, f
+
+
+def test_attention_work_list_fits_its_metadata_region():
+    """The per-XCD queues of the MFMA attention's work list are padded to the
+    longest queue, which with few heads and one long sequence can reach 8x
+    that sequence's tiles: the metadata region must be sized for that bound
+    (esm_gfx950_batch_upload copies the list into it)."""
+    import esm_gfx950 as eg
+    from conftest import cu_from_lengths
+    rs = np.random.default_rng(5)
+    cases = [[1024], [1], [2048], [1024, 3], [300, 300, 7], [129] * 5, [4096, 1, 1, 1]]
+    cases += [list(rs.integers(1, 1100, size=n)) for n in (1, 2, 3, 8, 31, 256)]
+    for lengths in cases:
+        cu = cu_from_lengths(lengths)
+        for H in (1, 2, 3, 4, 5, 20, 40):
+            for mfma in (True, False):
+                items, cap = eg.attention_work_items(cu, H, mfma)
+                assert items <= cap, (lengths, H, mfma, items, cap)
+    # The case the bound was derived for: d = 128, H = 2, one 1024-token
+    # sequence produces 64 items (8 queues padded to 8 tiles).
+    items, cap = eg.attention_work_items(cu_from_lengths([1024]), 2, True)
+    assert items == 64 and cap >= 64

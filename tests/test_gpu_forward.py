@@ -285,3 +285,27 @@ def test_first_block_fc1_fp16_fp32_model(dev, oracle, w8m):
     m.free()
     want = oracle.forward_packed(w8m, batch, int8=False, per_token=False, fc1_fp16=True)
     np.testing.assert_allclose(got, want, rtol=1e-3, atol=1e-3)
+
+
+def test_model_create_rejects_unrunnable_w8a8_configs(dev):
+    """Configs the W8A8 forward cannot run fail at creation with a message:
+    the split-fp16 attention needs hidden_size % 128 == 0 (its QKV epilogue
+    lives in the pipelined GEMM), per-token scales need intermediate_size <=
+    10240 (the fused GELU + quantisation row kernel)."""
+    small = syn.EsmConfig("d320", 1, 320, 5, 640)
+    w = syn.make_weights(small, seed=3, int8=True, keep_f32_linears=False)
+    with pytest.raises(eg.Gfx950Error, match="hidden_size % 128"):
+        eg.Model(dev, w, int8=True, attention_mode=eg.ATTN_MODE_F16X3)
+    m = eg.Model(dev, w, int8=True, attention_mode=eg.ATTN_MODE_FP32)
+    b = syn.batch_from_lengths([40, 9], seed=1)
+    assert np.all(np.isfinite(m.forward_packed(b.ids, b.cu)))
+    m.free()
+    wide = syn.EsmConfig("ffn12k", 1, 256, 4, 12288)
+    w = syn.make_weights(wide, seed=3, int8=True, keep_f32_linears=False)
+    with pytest.raises(eg.Gfx950Error, match="intermediate_size <= 10240"):
+        eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    m = eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TENSOR)
+    with pytest.raises(eg.Gfx950Error, match="intermediate_size <= 10240"):
+        m.set_act_mode(eg.ACT_PER_TOKEN)
+    assert np.all(np.isfinite(m.forward_packed(b.ids, b.cu)))
+    m.free()

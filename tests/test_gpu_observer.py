@@ -210,3 +210,33 @@ def test_forward_with_observer_single_sequence_and_empty(dev):
 def syn_ref_model(ref, w, int8, fc1_fp16=False):
     from pyoracle import RefModel
     return RefModel(ref, w, int8, fc1_fp16=fc1_fp16)
+
+
+def test_failed_forward_leaves_observer_unchanged(dev, monkeypatch):
+    """A forward_with_observer call that fails part-way (forced on the host
+    at site 5 of 8, after the earlier sites' kernels and gathers were
+    enqueued) must leave every reservoir as before: the next successful call
+    then gives the same percentiles as an observer that never saw the failed
+    call."""
+    w = syn.make_weights(syn.ESM2_8M.with_layers(2), seed=20261201 + 1, int8=False)
+    m = eg.Model(dev, w, int8=False)
+    b1 = syn.batch_from_lengths([60, 120, 33], seed=2)
+    b2 = syn.batch_from_lengths([90, 7, 150, 41], seed=3)
+    hit, clean = eg.ActivationObserver(dev), eg.ActivationObserver(dev)
+    try:
+        for o in (hit, clean):
+            o.observe("extra", dev.array(np.arange(70000, dtype=np.float32)))
+            m.forward_packed_with_observer(b1.ids, b1.cu, o)
+        before = {p: hit.percentile(p) for p in PCTS}
+        monkeypatch.setenv("ESM_GFX950_TEST_OBSERVER_FAIL_SITE", "5")
+        with pytest.raises(eg.Gfx950Error, match="failure injected at site 5"):
+            m.forward_packed_with_observer(b2.ids, b2.cu, hit)
+        monkeypatch.delenv("ESM_GFX950_TEST_OBSERVER_FAIL_SITE")
+        assert {p: hit.percentile(p) for p in PCTS} == before
+        for o in (hit, clean):
+            m.forward_packed_with_observer(b2.ids, b2.cu, o)
+        _equal(hit, clean.percentile)
+    finally:
+        hit.free()
+        clean.free()
+        m.free()
