@@ -23,7 +23,11 @@ OBJDIR = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(LIBDIR, "libesm_gfx950.so")
 
-SOURCES = ["gemm_i8.hip", "attention.hip", "elementwise.hip", "gemm_f32.hip", "capi.cpp", "gguf.cpp", "observer.cpp"]
+SOURCES = ["gemm_i8.hip", "attention.hip", "elementwise.hip", "gemm_f32.hip", "x86_exact.hip", "capi.cpp", "gguf.cpp",
+           "observer.cpp"]
+# Per-file flags: the reference's x86 kernels are restated with every fused
+# multiply-add spelled out, so the compiler must form no others.
+EXTRA = {"x86_exact.hip": ["-ffp-contract=off"]}
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -36,7 +40,7 @@ COMMON = [
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

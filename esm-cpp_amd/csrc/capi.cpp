@@ -723,6 +723,83 @@ extern "C" int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint1
   return ESM_GFX950_OK;
 }
 
+// ------------------------------------------------- the reference's x86 kernels
+extern "C" int esm_gfx950_layernorm_avx512(esm_gfx950_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                                           float eps, float* out, int num_rows, int d) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (num_rows <= 0 || d <= 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, x && gamma && beta && out, "layernorm_avx512: null pointer");
+  ESM_REQUIRE(ctx, d <= 2560, "layernorm_avx512: d must be <= 2560");
+  ESM_HIP(ctx, launch_layernorm_x86(const_cast<float*>(x), nullptr, gamma, beta, eps, out, num_rows, d, nullptr, 0,
+                                    ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_gelu_avx512(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, n == 0 || (x && out), "gelu_avx512: null pointer");
+  ESM_HIP(ctx, launch_gelu_x86(x, out, n, nullptr, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_expf_glibc(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, n == 0 || (x && out), "expf_glibc: null pointer");
+  ESM_HIP(ctx, launch_expf_glibc(x, out, n, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_linear_f32_avx512(esm_gfx950_ctx* ctx, const float* A, const float* W, const float* bias,
+                                            float* C, int M, int N, int K) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (M <= 0 || N <= 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, A && W && C && K >= 0, "linear_f32_avx512: bad arguments");
+  ESM_HIP(ctx, launch_linear_x86(A, K, W, K, bias, C, N, M, N, K, kF32Store, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_rope_apply_varlen_avx512(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
+                                                   const int* cu_seqlens, int batch_size, int num_heads,
+                                                   int head_dim) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu_seqlens, batch_size, -1));
+  ESM_REQUIRE(ctx, head_dim > 0 && head_dim % 2 == 0 && num_heads > 0, "rope_avx512: bad head shape");
+  const int T = cu_seqlens[batch_size];
+  if (T == 0) return ESM_GFX950_OK;
+  std::vector<int32_t> pos(T);
+  build_pos(cu_seqlens, batch_size, pos.data());
+  void* sp = nullptr;
+  ESM_TRY(ctx->get_scratch(static_cast<size_t>(T) * 4, &sp));
+  ESM_HIP(ctx, hipMemcpyAsync(sp, pos.data(), static_cast<size_t>(T) * 4, hipMemcpyHostToDevice, ctx->stream));
+  ESM_HIP(ctx, launch_rope_x86(x, num_heads * head_dim, static_cast<int*>(sp), T, num_heads, head_dim, cos, sin,
+                               head_dim, 1.0f, ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_attention_varlen_avx512(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
+                                                  const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
+                                                  float* out) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(validate_batch(ctx, cu_seqlens, batch_size, -1));
+  ESM_REQUIRE(ctx, num_heads > 0 && attention_x86_supported(head_dim),
+              "attention_varlen_avx512: head_dim must be 16, 32 or 64");
+  const int T = cu_seqlens[batch_size];
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, q && k && v && out, "attention_varlen_avx512: null pointer");
+  int maxL = 0;
+  for (int b = 0; b < batch_size; ++b) maxL = std::max(maxL, cu_seqlens[b + 1] - cu_seqlens[b]);
+  void* sp = nullptr;
+  ESM_TRY(ctx->get_scratch(static_cast<size_t>(batch_size + 1) * 4, &sp));
+  ESM_HIP(ctx, hipMemcpyAsync(sp, cu_seqlens, static_cast<size_t>(batch_size + 1) * 4, hipMemcpyHostToDevice,
+                              ctx->stream));
+  const int ld = num_heads * head_dim;
+  ESM_HIP(ctx, launch_attention_x86(q, k, v, ld, head_dim, static_cast<int*>(sp), batch_size, num_heads, maxL, out, ld,
+                                    ctx->stream));
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ESM_GFX950_OK;
+}
+
 // -------------------------------------------------------------------- model
 namespace {
 
@@ -764,6 +841,10 @@ struct esm_gfx950_model {
   // Layer 0's fc1 input rounded to fp16 (reference Config::first_block_fc1_fp16,
   // include/esm_cpp/model.h:36-41; applied at src/model.cpp:1028-1033).
   bool first_block_fc1_fp16 = false;
+  // ESM_GFX950_NUMERICS_X86_AVX512: the forward reproduces the reference's
+  // x86 AVX-512 kernels bit for bit (per-tensor activation scales);
+  // ESM_GFX950_NUMERICS_X86_AMX: the same with LinearAmx's row split.
+  int numerics = ESM_GFX950_NUMERICS_DEFAULT;
   // A staged batch is split into `parts` contiguous sequence groups; each
   // part has its own arena, metadata and (with more than one part) its own
   // HIP stream, so the parts' kernels can occupy different CUs at the same
@@ -780,6 +861,7 @@ struct esm_gfx950_model {
     hipStream_t stream = nullptr;    // null: the context stream
     int rope_len = 0;                // rows currently in the device rope tables
     int T = 0, B = 0, nwork = 0, t0 = 0;
+    int maxL = 0;                    // longest sequence of the staged part
   };
   std::vector<Part> parts = std::vector<Part>(1);
   int staged_T = 0;  // tokens of the staged batch (all parts)
@@ -1023,6 +1105,35 @@ extern "C" int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, es
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_model_set_numerics(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int numerics) {
+  if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx,
+              numerics == ESM_GFX950_NUMERICS_DEFAULT || numerics == ESM_GFX950_NUMERICS_X86_AVX512 ||
+                  numerics == ESM_GFX950_NUMERICS_X86_AMX,
+              "model_set_numerics: unknown numerics");
+  const auto& c = model->cfg;
+  if (numerics != ESM_GFX950_NUMERICS_DEFAULT) {
+    ESM_REQUIRE(ctx, attention_x86_supported(c.head_dim),
+                "model_set_numerics: the x86 attention supports head_dim 16, 32 and 64");
+    ESM_REQUIRE(ctx, c.hidden_size <= 2560, "model_set_numerics: the x86 LayerNorm supports hidden_size <= 2560");
+  }
+  if (model->numerics == numerics) return ESM_GFX950_OK;
+  // The arena layout depends on the numerics (fp32 Q|K|V rows): drop the
+  // staged batch and its buffers; the next upload sizes them again.
+  ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (auto& p : model->parts) {
+    if (p.stream) ESM_HIP(ctx, hipStreamSynchronize(p.stream));
+    if (p.arena) hipFree(p.arena);
+    p.arena = nullptr;
+    p.arena_bytes = 0;
+    p.cap_T = 0;
+    p.T = 0;
+  }
+  model->staged_T = 0;
+  model->numerics = numerics;
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_model_set_lm_dense_split(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled) {
   if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
   ESM_REQUIRE(ctx, !enabled || model->lm_w_hi, "model_set_lm_dense_split: hidden size is not a multiple of 32");
@@ -1064,7 +1175,7 @@ bool qkv_is_f32(const esm_gfx950_model_config& c) {
   return c.attention_mode == ESM_GFX950_ATTN_MODE_FP32 || c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3;
 }
 
-Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
+Arena layout(const esm_gfx950_model_config& c, int T, char* base, bool x86 = false) {
   const size_t d = c.hidden_size, f = c.intermediate_size, V = c.vocab_size;
   const size_t Ts = static_cast<size_t>(T);
   const size_t wq = std::max<size_t>(pad16(c.hidden_size), pad16(c.intermediate_size));
@@ -1082,7 +1193,7 @@ Arena layout(const esm_gfx950_model_config& c, int T, char* base) {
   a.qb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.kb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
   a.vb = reinterpret_cast<uint16_t*>(take(Ts * d * 2));
-  const bool need_qkv_f32 = !c.weights_int8 || qkv_is_f32(c);
+  const bool need_qkv_f32 = !c.weights_int8 || qkv_is_f32(c) || x86;
   a.qkv = reinterpret_cast<float*>(take(need_qkv_f32 ? Ts * 3 * d * 4 : 0));
   a.attn = reinterpret_cast<float*>(take(Ts * d * 4));
   a.ybuf = reinterpret_cast<float*>(take(c.weights_int8 ? Ts * d * 4 : 0));
@@ -1124,6 +1235,11 @@ Meta meta_layout(int T, int B, int maxL, int H, int dh, char* base) {
   m.sin_t = reinterpret_cast<float*>(take(static_cast<size_t>(maxL) * dh * 4));
   m.bytes = off;
   return m;
+}
+
+// The arena of one staged part (its layout depends on the model's numerics).
+Arena part_arena(const esm_gfx950_model* m, const esm_gfx950_model::Part& P) {
+  return layout(m->cfg, P.cap_T, static_cast<char*>(P.arena), m->numerics != ESM_GFX950_NUMERICS_DEFAULT);
 }
 
 template <typename P>
@@ -1498,6 +1614,132 @@ int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L,
   return ESM_GFX950_OK;
 }
 
+// TransformerBlock (reference src/model.cpp:932-1066) on the reference's x86
+// AVX-512 VNNI kernels, bit for bit: LayerNormAvx512, LinearVnni (per-tensor
+// activation scale, QuantizeActPrefixAvx512; the INT8 GEMM's dequant
+// epilogue is FinalizeStore16's expression) or LinearAmx (numerics X86_AMX:
+// the same, with its last T % 32 rows quantised on their own, reference
+// src/kernels/gemm_amx.cpp:218-309), ScaleInplace (folded into the Q
+// weight scales when exact) and RopeApplyVarlenAvx512, AttentionVarlenAvx512,
+// GeluAvx512, ResidualAddInplace. Q, K and V come from one GEMM over the
+// concatenated weight: the reference's three LinearInt8 calls quantise the
+// same LayerNorm output to the same bytes and scale. `resid_in` as in
+// layer_int8.
+int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
+                   const Meta& md, const esm_gfx950_model::Part& P, const float* resid_in, ObsRun* ob) {
+  const auto& c = m->cfg;
+  const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim, T = P.T;
+  const int ldq_d = pad16(d), ldq_f = pad16(f);
+  const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * f;
+  hipStream_t s = ctx->stream;
+  int slot;
+  auto linear = [&](const DevLinear& W, int lda, float* C, const char* site) -> int {
+    GemmI8Args g;
+    g.A = a.xq;
+    g.lda = lda;
+    g.W = W.w8;
+    g.ldw = W.ldk;
+    g.M = T;
+    g.N = W.N;
+    g.K = W.ldk;
+    g.a_scale = a.xs;
+    g.w_scale = W.ws;
+    g.bias = W.bias;
+    g.C_f32 = C;
+    g.ldc = W.N;
+    ESM_TRY(ctx->time_begin(site, &slot));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    return ctx->time_end(slot);
+  };
+
+  // QuantizeActPrefixAvx512 of x [T, cols] with the whole tensor's absmax
+  // (amax, already reduced); for LinearAmx (numerics X86_AMX) with its
+  // shape gate met by the consuming linear (N % 32, K % 64, T >= 32), the
+  // last T % 32 rows again with their own absmax (slot: a scratch scalar).
+  const bool amx = m->numerics == ESM_GFX950_NUMERICS_X86_AMX;
+  const int t_main = T & ~31;
+  auto quant = [&](const float* x, int cols, int ldq, float* amax, int n_out, float* slot) -> int {
+    ESM_HIP(ctx, launch_quant_tensor(x, cols, T, cols, amax, a.xq, ldq, a.xs, s));
+    if (amx && T >= 32 && n_out % 32 == 0 && cols % 64 == 0 && t_main < T) {
+      const float* xt = x + static_cast<size_t>(t_main) * cols;
+      ESM_HIP(ctx, launch_fill_f32(slot, 1, 0.0f, s));
+      ESM_HIP(ctx, launch_absmax(xt, static_cast<size_t>(T - t_main) * cols, slot, s));
+      ESM_HIP(ctx, launch_quant_tensor(xt, cols, T - t_main, cols, slot, a.xq + static_cast<size_t>(t_main) * ldq, ldq,
+                                       a.xs + t_main, s));
+    }
+    return ESM_GFX950_OK;
+  };
+
+  ESM_HIP(ctx, launch_fill_f32(a.absmax, 8, 0.0f, s));
+  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, 0, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  // Q, K and V are three linears of N = d each in the reference.
+  ESM_TRY(quant(a.ln, d, ldq_d, a.absmax, d, a.absmax + 4));
+  ESM_TRY(linear(L.qkv, ldq_d, a.qkv, "qkv"));
+  const float q_scale = m->q_scale_folded ? 1.0f : 1.0f / std::sqrt(static_cast<float>(dh));
+  ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+  ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+  ESM_TRY(ctx->time_begin("attention", &slot));
+  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s));
+  ESM_TRY(ctx->time_end(slot));
+  if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
+  ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
+  ESM_TRY(quant(a.attn, d, ldq_d, a.absmax + 1, d, a.absmax + 5));
+  ESM_TRY(linear(L.out, ldq_d, a.ybuf, "out"));
+  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
+                                    round16, s));
+  if (ob && round16) {
+    // The observer sees the LayerNorm output before the fp16 rounding.
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, 0,
+                                      s));
+    ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+  } else if (ob) {
+    ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  }
+  ESM_TRY(quant(a.ln, d, ldq_d, a.absmax + 2, f, a.absmax + 6));
+  ESM_TRY(linear(L.fc1, ldq_d, a.inter, "fc1"));
+  ESM_HIP(ctx, launch_gelu_x86(a.inter, a.inter, Tf, a.absmax + 3, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
+  ESM_TRY(quant(a.inter, f, ldq_f, a.absmax + 3, d, a.absmax + 7));
+  return linear(L.fc2, ldq_f, a.ybuf, "fc2");
+}
+
+// TransformerBlock of an all-fp32 model on the reference's x86 kernels:
+// LinearAvx512 for every projection (Q|K|V as one concatenated weight: each
+// output is its own dot product), then as layer_int8_x86.
+int layer_f32_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
+                  const Meta& md, const esm_gfx950_model::Part& P, ObsRun* ob) {
+  const auto& c = m->cfg;
+  const int d = c.hidden_size, H = c.num_heads, dh = c.head_dim, T = P.T;
+  const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * c.intermediate_size;
+  hipStream_t s = ctx->stream;
+  auto linear = [&](const float* A, const DevLinear& W, float* C, int epi) -> int {
+    ESM_HIP(ctx, launch_linear_x86(A, W.K, W.w32, W.K, W.bias, C, W.N, T, W.N, W.K, epi, s));
+    return ESM_GFX950_OK;
+  };
+  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, nullptr, 0, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  ESM_TRY(linear(a.ln, L.qkv, a.qkv, kF32Store));
+  const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
+  ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+  ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s));
+  if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
+  ESM_TRY(linear(a.attn, L.out, a.hidden, kF32Resid));
+  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr,
+                                    round16, s));
+  if (ob && round16) {
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, 0,
+                                      s));
+    ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+  } else if (ob) {
+    ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  }
+  ESM_TRY(linear(a.ln, L.fc1, a.inter, kF32Gelu));
+  if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
+  return linear(a.inter, L.fc2, a.hidden, kF32Resid);
+}
+
 constexpr float kTokenDropoutMaskRatioTrain = 0.15f * 0.8f;
 
 }  // namespace
@@ -1536,7 +1778,7 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
     P.arena = P.meta_dev = P.meta_host = nullptr;
     P.arena_bytes = P.meta_bytes = 0;
     P.cap_T = P.cap_B = P.cap_L = 0;
-    const Arena probe = layout(c, nT, nullptr);
+    const Arena probe = layout(c, nT, nullptr, m->numerics != ESM_GFX950_NUMERICS_DEFAULT);
     const Meta mprobe = meta_layout(nT, nB, nL, H, dh, nullptr);
     ESM_HIP(ctx, hipMalloc(&P.arena, probe.bytes));
     P.arena_bytes = probe.bytes;
@@ -1585,6 +1827,7 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
   P.T = T;
   P.B = B;
   P.t0 = t0;
+  P.maxL = maxL;
   P.nwork = static_cast<int>(work.size());
   return ESM_GFX950_OK;
 }
@@ -1595,7 +1838,8 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   const auto& c = m->cfg;
   const int T = P.T;
   const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
-  const Arena a = layout(c, P.cap_T, static_cast<char*>(P.arena));
+  const bool x86 = m->numerics != ESM_GFX950_NUMERICS_DEFAULT;
+  const Arena a = part_arena(m, P);
   const Meta md = meta_layout(P.cap_T, P.cap_B, P.cap_L, H, dh, static_cast<char*>(P.meta_dev));
   const int nwork = P.nwork;
 
@@ -1605,12 +1849,32 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const DevLayer& L = m->layers[li];
     const int round16 = (li == 0 && m->first_block_fc1_fp16) ? 1 : 0;
-    if (c.weights_int8) {
+    if (x86 && c.weights_int8) {
+      ESM_TRY(layer_int8_x86(ctx, m, L, round16, a, md, P, pending, ob));
+      pending = a.ybuf;
+    } else if (x86) {
+      ESM_TRY(layer_f32_x86(ctx, m, L, round16, a, md, P, ob));
+    } else if (c.weights_int8) {
       ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending, ob));
       pending = a.ybuf;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));
     }
+  }
+  if (x86) {
+    // Final LN, then the lm head on the reference's x86 kernels: Linear
+    // (LinearAvx512) -> Gelu -> LayerNorm -> tied decoder Linear
+    // (reference src/model.cpp:1181-1239).
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, pending, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d,
+                                      nullptr, 0, s));
+    int slot;
+    ESM_TRY(ctx->time_begin("lm_dense", &slot));
+    ESM_HIP(ctx, launch_linear_x86(a.ln, d, m->lm_dense_w, d, m->lm_dense_b, a.lm_a, d, T, d, d, kF32Gelu, s));
+    ESM_TRY(ctx->time_end(slot));
+    ESM_HIP(ctx, launch_layernorm_x86(a.lm_a, nullptr, m->lm_ln_w, m->lm_ln_b, c.layer_norm_eps, a.attn, T, d, nullptr,
+                                      0, s));
+    ESM_HIP(ctx, launch_linear_x86(a.attn, d, m->embed, d, m->dec_bias, logits, V, T, V, d, kF32Store, s));
+    return ESM_GFX950_OK;
   }
   // (Last residual +) final LN and lm head: dense -> GELU -> LN -> tied
   // decoder + bias (reference src/model.cpp:1181-1239).
@@ -1702,7 +1966,8 @@ int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, co
   // Contiguous sequence groups of about T / parts tokens each (never empty).
   // A per-tensor activation scale spans the whole batch, so that mode keeps
   // the batch in one part.
-  const bool whole = m->cfg.weights_int8 && m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR;
+  const bool whole = m->cfg.weights_int8 && (m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR ||
+                                            m->numerics != ESM_GFX950_NUMERICS_DEFAULT);
   const int np = whole ? 1 : std::min({static_cast<int>(m->parts.size()), B, max_parts});
   int b0 = 0;
   for (int p = 0; p < np; ++p) {
@@ -1732,7 +1997,9 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   const int V = m->cfg.vocab_size;
   if (m->parts.size() == 1) return forward_part(ctx, m, m->parts[0], logits);
   ESM_REQUIRE(ctx,
-              !(m->cfg.weights_int8 && m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR) || m->parts[1].T == 0,
+              !(m->cfg.weights_int8 && (m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR ||
+                                        m->numerics != ESM_GFX950_NUMERICS_DEFAULT)) ||
+                  m->parts[1].T == 0,
               "forward_device: batch staged in several parts before the switch to per-tensor scales; upload it again");
   // Fork: every part's stream waits for the work queued so far on the
   // context stream, runs its forward, and the context stream joins them.
@@ -1763,7 +2030,7 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   const int V = m->cfg.vocab_size;
   if (m->parts.size() == 1) {
     const esm_gfx950_model::Part& P = m->parts[0];
-    const Arena a = layout(m->cfg, P.cap_T, static_cast<char*>(P.arena));
+    const Arena a = part_arena(m, P);
     ESM_TRY(forward_part(ctx, m, P, a.logits));
     ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * V * 4, hipMemcpyDeviceToHost, ctx->stream));
   } else {
@@ -1774,7 +2041,7 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
     for (auto& P : m->parts) {
       if (P.T == 0) continue;
       StreamScope scope(ctx, P.stream);
-      const Arena a = layout(m->cfg, P.cap_T, static_cast<char*>(P.arena));
+      const Arena a = part_arena(m, P);
       ESM_TRY(forward_part(ctx, m, P, a.logits));
       ESM_HIP(ctx, hipMemcpyAsync(logits + static_cast<size_t>(P.t0) * V, a.logits, static_cast<size_t>(P.T) * V * 4,
                                   hipMemcpyDeviceToHost, P.stream));
@@ -1960,7 +2227,7 @@ extern "C" int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_
   }
   StreamScope scope(ctx, P.stream);
   ObsRun run(obs, std::move(sites));
-  const Arena a = layout(c, P.cap_T, static_cast<char*>(P.arena));
+  const Arena a = part_arena(m, P);
   const int rc = forward_part(ctx, m, P, a.logits, &run);
   if (rc != ESM_GFX950_OK) {
     // Whatever was enqueued completes before the reservoirs are restored.

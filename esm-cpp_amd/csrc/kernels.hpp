@@ -198,4 +198,24 @@ hipError_t launch_embed(const int* ids, const float* tok_scale,
 hipError_t launch_cast_f32(const float* x, size_t n, uint16_t* out,
                            int to_bf16, hipStream_t s);
 
+// ------------------------------------------- the reference's x86 kernels
+// Bit-exact counterparts of the reference's AVX-512 kernels (x86_exact.hip):
+// LayerNormAvx512 (optional residual add before, per-tensor absmax and fp16
+// rounding after; d <= 2560), GeluAvx512 (optional absmax; in place
+// allowed), glibc's expf, ScaleInplace + RopeApplyVarlenAvx512,
+// AttentionVarlenAvx512 (head_dim 16, 32 or 64; q/k/v rows at t*ld + h*dh,
+// cu_seqlens on the device), LinearAvx512 (C = A W^T + bias with a kF32*
+// epilogue; GELU is GeluAvx512).
+hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma, const float* beta, float eps,
+                                float* out, int rows, int d, float* absmax, int round16, hipStream_t s);
+hipError_t launch_gelu_x86(const float* x, float* out, size_t n, float* absmax, hipStream_t s);
+hipError_t launch_expf_glibc(const float* x, float* out, size_t n, hipStream_t s);
+hipError_t launch_rope_x86(float* x, int ld, const int* pos, int T, int heads, int head_dim, const float* cos_t,
+                           const float* sin_t, int ldt, float scale, hipStream_t s);
+bool attention_x86_supported(int head_dim);
+hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
+                                int batch, int heads, int max_len, float* out, int ldo, hipStream_t s);
+hipError_t launch_linear_x86(const float* A, int lda, const float* W, int ldw, const float* bias, float* C, int ldc,
+                             int M, int N, int K, int epi, hipStream_t s);
+
 }  // namespace esm_gfx950

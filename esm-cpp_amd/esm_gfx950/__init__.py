@@ -29,6 +29,9 @@ ATTN_MODE_FP16 = 0
 ATTN_MODE_BF16 = 1
 ATTN_MODE_FP32 = 2
 ATTN_MODE_F16X3 = 3
+NUMERICS_DEFAULT = 0
+NUMERICS_X86_AVX512 = 1
+NUMERICS_X86_AMX = 2
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTED = [
@@ -48,7 +51,9 @@ EXPORTED = [
     "esm_gfx950_model_set_first_block_fc1_fp16", "esm_gfx950_observer_create", "esm_gfx950_observer_free",
     "esm_gfx950_observer_clear", "esm_gfx950_observer_observe", "esm_gfx950_observer_site_count",
     "esm_gfx950_observer_site_name", "esm_gfx950_observer_percentile", "esm_gfx950_forward_with_observer",
-    "esm_gfx950_attention_work_items",
+    "esm_gfx950_attention_work_items", "esm_gfx950_layernorm_avx512", "esm_gfx950_gelu_avx512",
+    "esm_gfx950_expf_glibc", "esm_gfx950_linear_f32_avx512", "esm_gfx950_rope_apply_varlen_avx512",
+    "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics",
 ]
 
 
@@ -102,6 +107,13 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_rope_build_tables": (i32, [i32, i32, vp, vp]),
         "esm_gfx950_rope_apply_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
         "esm_gfx950_attention_work_items": (i32, [vp, i32, i32, i32, C.POINTER(sz), C.POINTER(sz)]),
+        "esm_gfx950_layernorm_avx512": (i32, [vp, vp, vp, vp, f32, vp, i32, i32]),
+        "esm_gfx950_gelu_avx512": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_expf_glibc": (i32, [vp, vp, vp, sz]),
+        "esm_gfx950_linear_f32_avx512": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+        "esm_gfx950_rope_apply_varlen_avx512": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
+        "esm_gfx950_attention_varlen_avx512": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp]),
+        "esm_gfx950_model_set_numerics": (i32, [vp, vp, i32]),
         "esm_gfx950_attention_varlen": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, vp, i32]),
         "esm_gfx950_attention_varlen_bf16": (i32, [vp, vp, vp, vp, i32, vp, i32, i32, vp]),
         "esm_gfx950_model_create": (i32, [vp, vp, C.POINTER(vp)]),
@@ -340,6 +352,30 @@ class Device:
         self._check(self.lib.esm_gfx950_attention_varlen(self.ctx, q.ptr, k.ptr, v.ptr, _ptr(cu), len(cu) - 1, H, dh,
                                                          out.ptr, precision))
 
+    # The reference's x86 AVX-512 kernels, bit for bit.
+    def layernorm_avx512(self, x, gamma, beta, eps, out, rows, d):
+        self._check(self.lib.esm_gfx950_layernorm_avx512(self.ctx, x.ptr, gamma.ptr, beta.ptr, eps, out.ptr, rows, d))
+
+    def gelu_avx512(self, x, out, n):
+        self._check(self.lib.esm_gfx950_gelu_avx512(self.ctx, x.ptr, out.ptr, n))
+
+    def expf_glibc(self, x, out, n):
+        self._check(self.lib.esm_gfx950_expf_glibc(self.ctx, x.ptr, out.ptr, n))
+
+    def linear_f32_avx512(self, A, W, bias, C_out, M, N, K):
+        self._check(self.lib.esm_gfx950_linear_f32_avx512(self.ctx, A.ptr, W.ptr,
+                                                          bias.ptr if bias is not None else None, C_out.ptr, M, N, K))
+
+    def rope_apply_varlen_avx512(self, x, cos, sin, cu: np.ndarray, H: int, dh: int):
+        cu = np.ascontiguousarray(cu, np.int32)
+        self._check(self.lib.esm_gfx950_rope_apply_varlen_avx512(self.ctx, x.ptr, cos.ptr, sin.ptr, _ptr(cu),
+                                                                 len(cu) - 1, H, dh))
+
+    def attention_varlen_avx512(self, q, k, v, cu: np.ndarray, H: int, dh: int, out):
+        cu = np.ascontiguousarray(cu, np.int32)
+        self._check(self.lib.esm_gfx950_attention_varlen_avx512(self.ctx, q.ptr, k.ptr, v.ptr, _ptr(cu), len(cu) - 1,
+                                                                H, dh, out.ptr))
+
     def attention_varlen_bf16(self, q, k, v, cu: np.ndarray, H: int, out, v_is_fp16: bool = False):
         cu = np.ascontiguousarray(cu, np.int32)
         self._check(self.lib.esm_gfx950_attention_varlen_bf16(self.ctx, q.ptr, k.ptr, v.ptr, int(v_is_fp16),
@@ -498,6 +534,11 @@ class Model:
         """Round layer 0's fc1 input to fp16 (esm_gfx950_model_set_first_block_fc1_fp16)."""
         self.dev._check(self.dev.lib.esm_gfx950_model_set_first_block_fc1_fp16(self.dev.ctx, self.handle,
                                                                              int(bool(enabled))))
+
+    def set_numerics(self, numerics: int):
+        """NUMERICS_X86_AVX512: forward bit-equal to the reference's x86 AVX-512
+        VNNI CPU path (esm_gfx950_model_set_numerics); drops the staged batch."""
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_numerics(self.dev.ctx, self.handle, int(numerics)))
 
     def set_act_mode(self, mode: int):
         self.dev._check(self.dev.lib.esm_gfx950_model_set_act_mode(self.dev.ctx, self.handle, mode))

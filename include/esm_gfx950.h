@@ -74,6 +74,18 @@ enum {
   ESM_GFX950_ATTN_MODE_F16X3 = 3
 };
 
+/* Arithmetic of the whole forward (esm_gfx950_model_set_numerics).
+ * DEFAULT: the model's act_quant_mode / attention_mode on the fast kernels.
+ * X86_AVX512: the reference's x86 AVX-512 CPU path reproduced bit for bit
+ * -- the kernels its facade selects for Isa::Avx512Vnni
+ * (src/kernels/dispatch.cpp): LayerNormAvx512, LinearVnni with the dynamic
+ * per-tensor activation scale, RopeApplyVarlenAvx512,
+ * AttentionVarlenAvx512, GeluAvx512, LinearAvx512 (lm head).
+ * X86_AMX: the same for Isa::Amx, whose LinearAmx quantises the last T % 32
+ * rows of each input with their own scale (src/kernels/gemm_amx.cpp:
+ * 218-309; on shapes its gate admits: T >= 32, N % 32 == 0, K % 64 == 0). */
+enum { ESM_GFX950_NUMERICS_DEFAULT = 0, ESM_GFX950_NUMERICS_X86_AVX512 = 1, ESM_GFX950_NUMERICS_X86_AMX = 2 };
+
 typedef struct esm_gfx950_ctx esm_gfx950_ctx;
 typedef struct esm_gfx950_weight esm_gfx950_weight;
 typedef struct esm_gfx950_model esm_gfx950_model;
@@ -219,6 +231,35 @@ int esm_gfx950_attention_varlen_bf16(esm_gfx950_ctx* ctx, const uint16_t* q, con
                                      const uint16_t* v, int v_is_fp16, const int* cu_seqlens,
                                      int batch_size, int num_heads, float* out);
 
+/* ----------------------------------------------- the reference's x86 kernels
+ * Device counterparts of the AVX-512 arms of the reference's facade, equal
+ * to them bit for bit (same operation order lane by lane, the same fused
+ * multiply-adds, _mm512_reduce_add_ps's tree as GCC builds it). Same
+ * arguments as the plain ops above; tensors are DEVICE pointers,
+ * cu_seqlens HOST arrays.
+ * LayerNormAvx512 (src/kernels/layernorm.cpp:59-149), d <= 2560. */
+int esm_gfx950_layernorm_avx512(esm_gfx950_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                                float eps, float* out, int num_rows, int d);
+/* GeluAvx512 (src/kernels/gelu.cpp:98-148): erf of Abramowitz-Stegun 7.1.26
+ * with the file's polynomial exp (which returns garbage for |x| above about
+ * 13.2, where its 2^n exponent bits wrap -- reproduced as is). */
+int esm_gfx950_gelu_avx512(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n);
+/* std::exp as AttentionVarlenAvx512 uses it on a sequence's last L % 16 keys
+ * (src/kernels/attention.cpp:376-381): glibc's expf, restated from its
+ * published algorithm; equal to glibc 2.35's expf on every float. */
+int esm_gfx950_expf_glibc(esm_gfx950_ctx* ctx, const float* x, float* out, size_t n);
+/* LinearAvx512 (src/kernels/gemm_fp32.cpp:194-294): C = A W^T + bias. */
+int esm_gfx950_linear_f32_avx512(esm_gfx950_ctx* ctx, const float* A, const float* W, const float* bias, float* C,
+                                 int M, int N, int K);
+/* RopeApplyVarlenAvx512 (src/kernels/rope.cpp:90-152). */
+int esm_gfx950_rope_apply_varlen_avx512(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
+                                        const int* cu_seqlens, int batch_size, int num_heads, int head_dim);
+/* AttentionVarlenAvx512 (src/kernels/attention.cpp:240-430, 770-811),
+ * head_dim 16, 32 or 64. */
+int esm_gfx950_attention_varlen_avx512(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
+                                       const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
+                                       float* out);
+
 /* ------------------------------------------------------------------ model
  * Forward-level fast path: the device-resident replacement of
  * Model::ForwardPackedInto (reference src/model.cpp:1093-1255, layer body
@@ -287,6 +328,15 @@ int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_mo
  * metadata). esm.first_block_fc1_fp16 = true enables that escape. */
 int esm_gfx950_model_create_from_gguf(esm_gfx950_ctx* ctx, const char* path, int act_quant_mode,
                                       int attention_mode, esm_gfx950_model** out);
+/* ESM_GFX950_NUMERICS_*: X86_AVX512 (X86_AMX) makes every later forward
+ * reproduce the reference's ForwardPackedInto on an AVX-512-VNNI (AMX) host
+ * bit for bit: same logits, every bit, as that CPU path on the same weights
+ * and batch. W8A8 models then quantise activations per tensor whatever
+ * their act_quant_mode, and run as one sequence group. head_dim must be 16,
+ * 32 or 64 and hidden_size <= 2560. Switching drops the staged batch
+ * (upload it again). Reference counterpart: ESM_FORCE_ISA=avx512vnni / amx
+ * (src/kernels/cpu_features.cpp:130-135). */
+int esm_gfx950_model_set_numerics(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int numerics);
 /* Switch the activation quantisation mode of a W8A8 model. */
 int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int act_mode);
 

@@ -19,6 +19,7 @@
  * correction acc - 128*col_sum the VNNI/AMX accumulator is exactly
  * sum_k q[m,k] * w[n,k]; this is that closed form. */
 void or_gemm_i8_i32(const int8_t* A, int lda, const int8_t* W, int ldw, int M, int N, int K, int32_t* C) {
+#pragma omp parallel for schedule(dynamic, 4)
   for (int m = 0; m < M; ++m) {
     const int8_t* a = A + (size_t)m * lda;
     for (int n = 0; n < N; ++n) {
@@ -123,6 +124,7 @@ void or_linear_int8_w8a16(const float* A, const int8_t* Wq, const float* scales,
  * k = 0..K-1 in order. Eight outputs are carried side by side; each keeps
  * its own sequential sum, so every result is the reference's bit for bit. */
 void or_linear_f32(const float* A, const float* W, const float* bias, float* C, int M, int N, int K) {
+#pragma omp parallel for schedule(dynamic, 4)
   for (int m = 0; m < M; ++m) {
     const float* a = A + (size_t)m * K;
     int n = 0;
@@ -150,6 +152,7 @@ void or_linear_f32(const float* A, const float* W, const float* bias, float* C, 
 
 /* LayerNormRef (layernorm.cpp:23-44): mean and variance in double. */
 void or_layernorm(const float* x, const float* gamma, const float* beta, float eps, float* out, int rows, int d) {
+#pragma omp parallel for schedule(static)
   for (int r = 0; r < rows; ++r) {
     const float* xr = x + (size_t)r * d;
     float* yr = out + (size_t)r * d;
@@ -259,10 +262,23 @@ static void linear_call(const or_model* m, int layer, int j, const float* A, flo
                         int8_t* qbuf, float* sbuf, int32_t* accbuf) {
   const int idx = layer * 6 + j;
   if (!m->weights_int8) {
-    or_linear_f32(A, m->w_f32[idx], m->bias[idx], C, M, N, K);
+    (m->x86 ? or_x86_linear_f32 : or_linear_f32)(A, m->w_f32[idx], m->bias[idx], C, M, N, K);
     return;
   }
-  if (m->act_per_token) {
+  if (m->x86) {
+    float s;
+    or_x86_quant_act(A, (size_t)M * K, qbuf, &s);
+    for (int r = 0; r < M; ++r) sbuf[r] = s;
+    /* LinearAmx (gemm_amx.cpp:218-309): for M >= 32, N % 32 == 0 and
+     * K % 64 == 0 the first M & ~31 rows run on AMX with the scale of the
+     * whole input, and the last M % 32 rows go to LinearVnni as a call of
+     * their own, which quantises them with their own per-tensor scale. */
+    const int m_main = M & ~31;
+    if (m->x86 == 2 && M >= 32 && N % 32 == 0 && K % 64 == 0 && m_main < M) {
+      or_x86_quant_act(A + (size_t)m_main * K, (size_t)(M - m_main) * K, qbuf + (size_t)m_main * K, &s);
+      for (int r = m_main; r < M; ++r) sbuf[r] = s;
+    }
+  } else if (m->act_per_token) {
     or_quant_act_rows(A, M, K, qbuf, sbuf);
   } else {
     float s;
@@ -314,33 +330,42 @@ int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, 
   }
 
   const float q_scale = 1.0f / sqrtf((float)dh);
+  void (*layernorm)(const float*, const float*, const float*, float, float*, int, int) =
+      m->x86 ? or_x86_layernorm : or_layernorm;
+  void (*gelu)(const float*, float*, size_t) = m->x86 ? or_x86_gelu : or_gelu;
+  void (*rope)(float*, const float*, const float*, const int*, int, int, int) =
+      m->x86 ? or_x86_rope_varlen : or_rope_varlen;
+  void (*attention)(const float*, const float*, const float*, const int*, int, int, int, float*) =
+      m->x86 ? or_x86_attention_varlen : or_attention_varlen;
+  void (*linear_f32)(const float*, const float*, const float*, float*, int, int, int) =
+      m->x86 ? or_x86_linear_f32 : or_linear_f32;
   for (int l = 0; l < m->num_layers; ++l) {
     float* q = qkv;
     float* k = qkv + Td;
     float* v = qkv + 2 * Td;
-    or_layernorm(hidden, m->ln1_w[l], m->ln1_b[l], m->eps, ln, T, d);
+    layernorm(hidden, m->ln1_w[l], m->ln1_b[l], m->eps, ln, T, d);
     linear_call(m, l, 0, ln, q, T, d, d, qbuf, sbuf, acc);
     linear_call(m, l, 1, ln, k, T, d, d, qbuf, sbuf, acc);
     linear_call(m, l, 2, ln, v, T, d, d, qbuf, sbuf, acc);
     for (size_t i = 0; i < Td; ++i) q[i] *= q_scale;
     or_rope_tables(maxL, dh, cos_t, sin_t);
-    or_rope_varlen(q, cos_t, sin_t, cu, B, H, dh);
-    or_rope_varlen(k, cos_t, sin_t, cu, B, H, dh);
-    or_attention_varlen(q, k, v, cu, B, H, dh, attn);
+    rope(q, cos_t, sin_t, cu, B, H, dh);
+    rope(k, cos_t, sin_t, cu, B, H, dh);
+    attention(q, k, v, cu, B, H, dh, attn);
     linear_call(m, l, 3, attn, proj, T, d, d, qbuf, sbuf, acc);
     for (size_t i = 0; i < Td; ++i) hidden[i] += proj[i];
-    or_layernorm(hidden, m->ln2_w[l], m->ln2_b[l], m->eps, ln, T, d);
+    layernorm(hidden, m->ln2_w[l], m->ln2_b[l], m->eps, ln, T, d);
     if (m->fc1_fp16 && l == 0) or_round_fp16(ln, Td);
     linear_call(m, l, 4, ln, inter, T, f, d, qbuf, sbuf, acc);
-    or_gelu(inter, inter_g, Tf);
+    gelu(inter, inter_g, Tf);
     linear_call(m, l, 5, inter_g, proj, T, d, f, qbuf, sbuf, acc);
     for (size_t i = 0; i < Td; ++i) hidden[i] += proj[i];
   }
-  or_layernorm(hidden, m->final_ln_w, m->final_ln_b, m->eps, ln, T, d);
-  or_linear_f32(ln, m->lm_dense_w, m->lm_dense_b, proj, T, d, d);
-  or_gelu(proj, attn, Td);
-  or_layernorm(attn, m->lm_ln_w, m->lm_ln_b, m->eps, ln, T, d);
-  or_linear_f32(ln, m->embed, m->lm_decoder_bias, logits, T, V, d);
+  layernorm(hidden, m->final_ln_w, m->final_ln_b, m->eps, ln, T, d);
+  linear_f32(ln, m->lm_dense_w, m->lm_dense_b, proj, T, d, d);
+  gelu(proj, attn, Td);
+  layernorm(attn, m->lm_ln_w, m->lm_ln_b, m->eps, ln, T, d);
+  linear_f32(ln, m->embed, m->lm_decoder_bias, logits, T, V, d);
 
   free(hidden); free(ln); free(qkv); free(attn); free(proj); free(inter); free(inter_g);
   free(cos_t); free(sin_t); free(qbuf); free(sbuf); free(acc);

@@ -62,6 +62,30 @@ void or_rope_varlen(float* x, const float* cos_t, const float* sin_t, const int*
 void or_attention_varlen(const float* q, const float* k, const float* v, const int* cu, int B, int H, int dh,
                          float* out);
 
+/* ---- oracle_x86.c: the reference's AVX-512 kernels (the facade's choice
+ * for Isa::Avx512, Avx512Vnni and Amx, src/kernels/dispatch.cpp), lane by
+ * lane. */
+/* ExpAvx512 (gelu.cpp:40-68; attention.cpp:156-175, same code). */
+float or_x86_exp(float x);
+/* GeluAvx512 (gelu.cpp:98-148), one value and an array. */
+float or_x86_gelu1(float v);
+void or_x86_gelu(const float* x, float* out, size_t n);
+/* LayerNormAvx512 (layernorm.cpp:59-149). */
+void or_x86_layernorm(const float* x, const float* gamma, const float* beta, float eps, float* out, int rows,
+                      int d);
+/* RopeApplyVarlenAvx512 (rope.cpp:90-152). */
+void or_x86_rope_varlen(float* x, const float* cos_t, const float* sin_t, const int* cu, int B, int H, int dh);
+/* AttentionVarlenAvx512 (attention.cpp:240-430, 770-811). */
+void or_x86_attention_varlen(const float* q, const float* k, const float* v, const int* cu, int B, int H, int dh,
+                             float* out);
+/* LinearAvx512 (gemm_fp32.cpp:194-294). */
+void or_x86_linear_f32(const float* A, const float* W, const float* bias, float* C, int M, int N, int K);
+/* QuantizeActPrefixAvx512 (gemm_int8.cpp:391-508) as signed int8 (the u8
+ * offset of 128 is removed again by LinearVnni's col_sum correction). */
+void or_x86_quant_act(const float* x, size_t n, int8_t* q, float* scale_out);
+/* expf (glibc: the reference's std::exp) of every element. */
+void or_expf_array(const float* x, float* out, size_t n);
+
 /* Model descriptor for the restated forward: host pointers. */
 typedef struct {
   int num_layers, hidden, heads, head_dim, ffn, vocab;
@@ -83,6 +107,10 @@ typedef struct {
   const float* lm_ln_w; const float* lm_ln_b;
   const float* lm_decoder_bias;
   int fc1_fp16;        /* 1: layer 0's fc1 input rounded to fp16 (model.cpp:1028-1033) */
+  int x86;             /* 1: the reference's x86 AVX-512 kernels (oracle_x86.c) for LayerNorm,
+                          GELU, RoPE, attention, FP32 Linear and activation quantisation
+                          (Isa::Avx512Vnni: LinearVnni); 2: the same with LinearAmx's row
+                          split (Isa::Amx); requires weights_int8 == 0 or act_per_token == 0 */
 } or_model;
 
 /* Embed (src/model.cpp:737-778) + TransformerBlock per layer (:932-1066) +

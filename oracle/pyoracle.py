@@ -34,13 +34,13 @@ class _OrModel(C.Structure):
                 ("ln2_w", C.POINTER(vp)), ("ln2_b", C.POINTER(vp)), ("w_f32", C.POINTER(vp)),
                 ("w_i8", C.POINTER(vp)), ("w_scale", C.POINTER(vp)), ("bias", C.POINTER(vp)),
                 ("final_ln_w", vp), ("final_ln_b", vp), ("lm_dense_w", vp), ("lm_dense_b", vp),
-                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp), ("fc1_fp16", i32)]
+                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp), ("fc1_fp16", i32), ("x86", i32)]
 
 
 LINEARS = ("q", "k", "v", "out", "fc1", "fc2")
 
 
-def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False):
+def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False, x86: bool = False):
     """Builds the or_model descriptor (and keeps its arrays alive)."""
     cfg = weights.cfg
     keep = []
@@ -81,6 +81,7 @@ def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False):
     m.lm_ln_w, m.lm_ln_b = p(F["lm_head.ln.weight"]), p(F["lm_head.ln.bias"])
     m.lm_decoder_bias = p(F["lm_head.decoder.bias"])
     m.fc1_fp16 = int(fc1_fp16)
+    m.x86 = int(x86)  # 0 none, 1 avx512vnni, 2 amx
     keep.extend([ln1w, ln1b, ln2w, ln2b, wf, wi, ws, bs])
     return m, keep
 
@@ -107,6 +108,13 @@ class Oracle:
             "or_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
             "or_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
             "or_forward_packed": [C.POINTER(_OrModel), vp, vp, i32, i32, vp],
+            "or_x86_gelu": [vp, vp, sz],
+            "or_x86_layernorm": [vp, vp, vp, f32, vp, i32, i32],
+            "or_x86_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
+            "or_x86_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
+            "or_x86_linear_f32": [vp, vp, vp, vp, i32, i32, i32],
+            "or_x86_quant_act": [vp, sz, vp, vp],
+            "or_expf_array": [vp, vp, sz],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -207,8 +215,64 @@ class Oracle:
         self.lib.or_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
         return out
 
-    def forward_packed(self, weights, batch, int8: bool, per_token: bool, fc1_fp16: bool = False):
-        m, keep = make_or_model(weights, int8, per_token, fc1_fp16)
+    # The reference's x86 AVX-512 kernels (oracle_x86.c).
+    def x86_gelu(self, x):
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.or_x86_gelu(_p(x), _p(out), x.size)
+        return out
+
+    def x86_layernorm(self, x, g, b, eps=1e-5):
+        x = _c(x, np.float32)
+        rows, d = x.shape
+        out = np.empty_like(x)
+        self.lib.or_x86_layernorm(_p(x), _p(_c(g, np.float32)), _p(_c(b, np.float32)), eps, _p(out), rows, d)
+        return out
+
+    def x86_rope_varlen(self, x, cos, sin, cu, H, dh):
+        x = np.array(x, np.float32, copy=True, order="C")
+        cu = _c(cu, np.int32)
+        self.lib.or_x86_rope_varlen(_p(x), _p(_c(cos, np.float32)), _p(_c(sin, np.float32)), _p(cu), len(cu) - 1,
+                                    H, dh)
+        return x
+
+    def x86_attention_varlen(self, q, k, v, cu, H, dh):
+        q, k, v, cu = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32), _c(cu, np.int32)
+        out = np.zeros((int(cu[-1]), H * dh), np.float32)
+        self.lib.or_x86_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh, _p(out))
+        return out
+
+    def x86_linear_f32(self, A, W, bias):
+        A, W = _c(A, np.float32), _c(W, np.float32)
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.or_x86_linear_f32(_p(A), _p(W), _p(None if bias is None else _c(bias, np.float32)), _p(out), M, N,
+                                   K)
+        return out
+
+    def expf(self, x):
+        """glibc expf of every element (the reference's std::exp)."""
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.or_expf_array(_p(x), _p(out), x.size)
+        return out
+
+    def x86_quant_act(self, x):
+        x = _c(x, np.float32)
+        q = np.empty(x.shape, np.int8)
+        s = C.c_float()
+        self.lib.or_x86_quant_act(_p(x), x.size, _p(q), C.byref(s))
+        return q, float(s.value)
+
+    def forward_packed(self, weights, batch, int8: bool, per_token: bool, fc1_fp16: bool = False,
+                       x86=False):
+        """Restated packed forward. x86=True (or "avx512vnni") runs the
+        reference's x86 AVX-512 kernels, per-tensor scales and LinearVnni in
+        W8A8; x86="amx" the same with LinearAmx's row split."""
+        if x86 and int8 and per_token:
+            raise ValueError("the x86 path quantises activations per tensor")
+        m, keep = make_or_model(weights, int8, per_token, fc1_fp16, 2 if x86 == "amx" else int(bool(x86)))
         T = batch.total_tokens
         logits = np.empty((T, weights.cfg.vocab_size), np.float32)
         rc = self.lib.or_forward_packed(C.byref(m), _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
@@ -244,6 +308,7 @@ class RefLib:
             "esmref_gelu": (None, [vp, vp, sz]),
             "esmref_rope_tables": (None, [i32, i32, vp, vp]),
             "esmref_rope_varlen_ref": (None, [vp, vp, vp, vp, i32, i32, i32]),
+            "esmref_rope_varlen": (None, [vp, vp, vp, vp, i32, i32, i32]),
             "esmref_attention_varlen_ref": (None, [vp, vp, vp, vp, i32, i32, i32, vp]),
             "esmref_attention_varlen": (None, [vp, vp, vp, vp, i32, i32, i32, vp]),
             "esmref_model_create": (vp, [C.POINTER(_OrModel)]),
@@ -383,6 +448,37 @@ class RefLib:
         self.lib.esmref_rope_varlen_ref(_p(x), _p(_c(cos, np.float32)), _p(_c(sin, np.float32)), _p(cu),
                                         len(cu) - 1, H, dh)
         return x
+
+    def rope_varlen(self, x, cos, sin, cu, H, dh):
+        """The facade's RopeApplyVarlen (the current ISA's kernel)."""
+        x = np.array(x, np.float32, copy=True, order="C")
+        cu = _c(cu, np.int32)
+        self.lib.esmref_rope_varlen(_p(x), _p(_c(cos, np.float32)), _p(_c(sin, np.float32)), _p(cu), len(cu) - 1,
+                                    H, dh)
+        return x
+
+    def layernorm(self, x, g, b, eps=1e-5):
+        """The facade's LayerNorm (the current ISA's kernel)."""
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.esmref_layernorm(_p(x), _p(_c(g, np.float32)), _p(_c(b, np.float32)), eps, _p(out), *x.shape)
+        return out
+
+    def gelu(self, x):
+        """The facade's Gelu (the current ISA's kernel)."""
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.esmref_gelu(_p(x), _p(out), x.size)
+        return out
+
+    def linear(self, A, W, bias):
+        """The facade's FP32 Linear (the current ISA's kernel)."""
+        A, W = _c(A, np.float32), _c(W, np.float32)
+        M, K = A.shape
+        N = W.shape[0]
+        out = np.empty((M, N), np.float32)
+        self.lib.esmref_linear(_p(A), _p(W), _p(None if bias is None else _c(bias, np.float32)), _p(out), M, N, K)
+        return out
 
     def attention_varlen_ref(self, q, k, v, cu, H, dh):
         q, k, v, cu = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32), _c(cu, np.int32)

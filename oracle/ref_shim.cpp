@@ -149,6 +149,9 @@ void esmref_rope_tables(int L, int dh, float* c, float* s) { esm::kernels::RopeB
 void esmref_rope_varlen_ref(float* x, const float* c, const float* s, const int* cu, int B, int H, int dh) {
   esm::kernels::RopeApplyVarlenRef(x, c, s, cu, B, H, dh);
 }
+void esmref_rope_varlen(float* x, const float* c, const float* s, const int* cu, int B, int H, int dh) {
+  esm::kernels::RopeApplyVarlen(x, c, s, cu, B, H, dh);
+}
 void esmref_attention_varlen_ref(const float* q, const float* k, const float* v, const int* cu, int B, int H, int dh,
                                  float* out) {
   esm::kernels::AttentionVarlenRef(q, k, v, cu, B, H, dh, out);
