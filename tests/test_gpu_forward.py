@@ -309,3 +309,49 @@ def test_model_create_rejects_unrunnable_w8a8_configs(dev):
         m.set_act_mode(eg.ACT_PER_TOKEN)
     assert np.all(np.isfinite(m.forward_packed(b.ids, b.cu)))
     m.free()
+
+
+# The reference's own 33-layer spread on the full-depth fixture's batch: its
+# AVX-512-VNNI and AMX paths agree at logit correlation 0.999134, VNNI and
+# the scalar Ref ISA at 0.999172, AMX and Ref at 0.999192
+# (tests/test_x86_oracle.py pins these figures). A W8A8 forward re-quantises
+# every linear's input, so one ulp anywhere flips int8 roundings that later
+# layers amplify: arithmetic that is not the reference's own, bit for bit
+# (that is ESM_GFX950_NUMERICS_X86_*, tests/test_gpu_x86.py), can be held at
+# full depth to the reference's spread against itself, not to 0.9999.
+FULL_DEPTH_FLOOR = 0.999134
+
+
+@pytest.fixture(scope="module")
+def full_depth():
+    import os
+    from conftest import ROOT
+    path = os.path.join(ROOT, "tests", "golden", "full_depth_650m.npz")
+    with np.load(path) as z:
+        data = {k: z[k] for k in z.files}
+    w = syn.make_weights(syn.ESM2_650M, seed=20261201 + 4, int8=True, keep_f32_linears=False)
+    return data, w
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+@pytest.mark.parametrize("attn", [eg.ATTN_MODE_F16X3, eg.ATTN_MODE_FP32])
+def test_w8a8_forward_full_depth(dev, full_depth, per_token, attn):
+    """All 33 layers of the 650M model on the fixture's 446-token batch, the
+    default (fast) numerics: against the oracle's same-mode 33-layer logits
+    and, per tensor, against the reference's own AVX-512-VNNI CPU logits,
+    logit correlation >= the reference's spread against itself. Measured:
+    per-token 0.99949 (F16X3) / 0.99949 (FP32 attention) vs the oracle;
+    per-tensor 0.99927 / 0.99925 vs the reference."""
+    data, w = full_depth
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w, int8=True, act_mode=mode, attention_mode=attn)
+    got = m.forward_packed(data["ids"], data["cu"])
+    m.free()
+    assert np.all(np.isfinite(got))
+    keys = ["oracle_per_token"] if per_token else ["oracle_per_tensor", "ref_avx512vnni"]
+    for key in keys:
+        c = corr(got, data[key])
+        agree = float(np.mean(got.argmax(1) == data[key].argmax(1)))
+        print(f"per_token={per_token} attn={attn} vs {key}: corr {c:.6f} argmax {agree:.4f}")
+        assert c >= FULL_DEPTH_FLOOR, (key, c)
+        assert agree >= 0.94, (key, agree)
