@@ -37,12 +37,46 @@ int pad16(int k) { return (k + 15) & ~15; }
 
 }  // namespace
 
+// Device scratch of esm_gfx950_linear_i8_noalloc (the allocation-free
+// LinearInt8): the quantised activations, their scales and one absmax
+// scalar. Every GPU the library runs on holds its own copy until the
+// process ends. In host code `scratch` names a host-side stand-in, not device
+// memory: its device address is taken once per device at esm_gfx950_init
+// (hipGetSymbolAddress, that device current) and only that address is used.
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// The device address of `scratch` on `device` (the current device), taken
+// on the first call for that device.
+hipError_t scratch_address(int device, void** out) {
+  *out = nullptr;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_addr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_addr[device] = p;
+  }
+  *out = g_scratch_addr[device];
+  return hipSuccess;
+}
+}  // namespace
+
 struct esm_gfx950_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string err;
   std::string arch;
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  // Device address of the static `scratch` array on this context's device.
+  void* noalloc_scratch = nullptr;
   // Op-level scratch (grown on demand; the forward uses its own arena).
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
@@ -250,8 +284,11 @@ extern "C" int esm_gfx950_init(int device, esm_gfx950_ctx** out) {
   if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ESM_GFX950_HIP_ERROR;
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ESM_GFX950_HIP_ERROR;
   if (hipSetDevice(device) != hipSuccess) return ESM_GFX950_HIP_ERROR;
+  void* noalloc = nullptr;
+  if (scratch_address(device, &noalloc) != hipSuccess) return ESM_GFX950_HIP_ERROR;
   auto* ctx = new esm_gfx950_ctx();
   ctx->device = device;
+  ctx->noalloc_scratch = noalloc;
   ctx->arch = prop.gcnArchName;
   if (hipStreamCreate(&ctx->stream) != hipSuccess || hipEventCreate(&ctx->t0) != hipSuccess ||
       hipEventCreate(&ctx->t1) != hipSuccess) {
@@ -511,6 +548,34 @@ extern "C" int esm_gfx950_linear_i8(esm_gfx950_ctx* ctx, const float* A, const e
   auto* q = static_cast<int8_t*>(s);
   auto* scales = reinterpret_cast<float*>(static_cast<char*>(s) + qbytes);
   auto* amax = reinterpret_cast<float*>(static_cast<char*>(s) + qbytes + sbytes);
+  ESM_TRY(quantize_into(ctx, A, M, K, act_mode, q, ldq, scales, amax));
+  return esm_gfx950_linear_i8_q(ctx, q, ldq, scales, W, bias, C, M, 0);
+}
+
+extern "C" int esm_gfx950_linear_i8_noalloc(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
+                                            const float* bias, float* C, int M, int N, int K, int act_mode) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  if (M <= 0 || N <= 0 || K <= 0) {
+    if (M > 0 && N > 0 && C) ESM_HIP(ctx, launch_fill_f32(C, static_cast<size_t>(M) * N, 0.0f, ctx->stream));
+    return ESM_GFX950_OK;
+  }
+  ESM_REQUIRE(ctx, A && W && C, "linear_i8_noalloc: null pointer");
+  if (W->N != N || W->K != K)
+    return ctx->fail(ESM_GFX950_SHAPE_MISMATCH, "linear_i8_noalloc: weight shape does not match N, K");
+  if (!ctx->noalloc_scratch) return ctx->fail(ESM_GFX950_HIP_ERROR, "linear_i8_noalloc: no device scratch");
+  // Layout in the static scratch: q [M, ldq] int8, scales [M] fp32, absmax.
+  const int ldq = W->ldk;
+  const size_t qbytes = align_up(static_cast<size_t>(M) * ldq, 256);
+  const size_t sbytes = align_up(static_cast<size_t>(M) * sizeof(float), 256);
+  if (qbytes + sbytes + 256 > kNoAllocScratchBytes)
+    return ctx->fail(ESM_GFX950_OUT_OF_RANGE,
+                     "linear_i8_noalloc: M * pad16(K) + 4 * M = " + std::to_string(qbytes + sbytes) +
+                         " bytes of quantised activations exceed its " +
+                         std::to_string(kNoAllocScratchBytes >> 20) + " MiB static scratch (use esm_gfx950_linear_i8)");
+  char* base = static_cast<char*>(ctx->noalloc_scratch);
+  auto* q = reinterpret_cast<int8_t*>(base);
+  auto* scales = reinterpret_cast<float*>(base + qbytes);
+  auto* amax = reinterpret_cast<float*>(base + qbytes + sbytes);  // zeroed by quantize_into (fill kernel)
   ESM_TRY(quantize_into(ctx, A, M, K, act_mode, q, ldq, scales, amax));
   return esm_gfx950_linear_i8_q(ctx, q, ldq, scales, W, bias, C, M, 0);
 }

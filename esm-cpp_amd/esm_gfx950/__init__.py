@@ -53,7 +53,7 @@ EXPORTED = [
     "esm_gfx950_observer_site_name", "esm_gfx950_observer_percentile", "esm_gfx950_forward_with_observer",
     "esm_gfx950_attention_work_items", "esm_gfx950_layernorm_avx512", "esm_gfx950_gelu_avx512",
     "esm_gfx950_expf_glibc", "esm_gfx950_linear_f32_avx512", "esm_gfx950_rope_apply_varlen_avx512",
-    "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics",
+    "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics", "esm_gfx950_linear_i8_noalloc",
 ]
 
 
@@ -99,6 +99,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_set_gemm_tile_rows": (i32, [i32]),
         "esm_gfx950_model_set_lm_dense_split": (i32, [vp, vp, i32]),
         "esm_gfx950_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
+        "esm_gfx950_linear_i8_noalloc": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
         "esm_gfx950_linear_f32": (i32, [vp, vp, vp, vp, vp, i32, i32, i32]),
         "esm_gfx950_layernorm": (i32, [vp, vp, vp, vp, f32, vp, i32, i32]),
         "esm_gfx950_gelu": (i32, [vp, vp, vp, sz]),
@@ -325,6 +326,13 @@ class Device:
                   K: int, mode: int):
         self._check(self.lib.esm_gfx950_linear_i8(self.ctx, A.ptr, W.handle, bias.ptr if bias is not None else None,
                                                   C_out.ptr, M, N, K, mode))
+
+    def linear_i8_noalloc(self, A: DeviceArray, W: Weight, bias: Optional[DeviceArray], C_out: DeviceArray, M: int,
+                          N: int, K: int, mode: int):
+        """linear_i8 without any device allocation (static 64 MiB scratch)."""
+        self._check(self.lib.esm_gfx950_linear_i8_noalloc(self.ctx, A.ptr, W.handle,
+                                                          bias.ptr if bias is not None else None, C_out.ptr, M, N, K,
+                                                          mode))
 
     def linear_f32(self, A, W, bias, C_out, M, N, K):
         self._check(self.lib.esm_gfx950_linear_f32(self.ctx, A.ptr, W.ptr, bias.ptr if bias is not None else None,

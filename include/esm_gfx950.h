@@ -181,6 +181,19 @@ int esm_gfx950_gelu_quantize_act(esm_gfx950_ctx* ctx, const float* x, int M, int
 int esm_gfx950_linear_i8(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
                          const float* bias, float* C, int M, int N, int K, int act_mode);
 
+/* esm_gfx950_linear_i8 for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): no counterpart in the reference. Same arguments, arithmetic
+ * and results as esm_gfx950_linear_i8, but its quantised activations and
+ * scales live in a static device array of 64 MiB that every GPU the library
+ * runs on holds until the process ends, so it never allocates. Limit:
+ * align256(M * pad16(K)) + align256(4 * M) + 256 <= 64 MiB (e.g. M = 30,700
+ * at K = 1280); larger calls return ESM_GFX950_OUT_OF_RANGE. All calls on
+ * one GPU share the array: calls that overlap on one GPU (contexts on
+ * different streams) race. */
+int esm_gfx950_linear_i8_noalloc(esm_gfx950_ctx* ctx, const float* A, const esm_gfx950_weight* W,
+                                 const float* bias, float* C, int M, int N, int K, int act_mode);
+
 /* ----------------------------------------------------------- FP32 / misc ops
  * esm::kernels::Linear (kernels.h:19-20; LinearRef gemm_fp32.cpp:33-46):
  * C[M, N] = A[M, K] W[N, K]^T + bias (bias may be NULL). */
