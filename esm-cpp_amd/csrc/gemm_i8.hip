@@ -702,30 +702,81 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
+  // Fragments are double-buffered in registers: the reads of K sub-step
+  // q + 1 (32 bytes of K) are issued between the MFMAs of sub-step q, one
+  // read after each MFMA, so the LDS latency runs under the matrix cores
+  // instead of in front of them. Across a stage boundary the first sub-step
+  // of the next stage is read during the last sub-step's MFMAs, after the
+  // barrier that publishes that stage.
+  // Row R + 32 i of a stage sits 4 KB after row R (same r = R & 7 and
+  // parity of R >> 3), so one lane offset per 16-byte chunk addresses every
+  // fragment of a sub-step, the block index becoming an immediate offset.
   const int arow = wm * BLK_M * 32 + l32;       // A fragment rows (+ i*32)
   const int brow = BM + wn * BLK_N * 32 + l32;  // W fragment rows (+ j*32)
+  constexpr int kSub = BK / 32;                 // MFMA sub-steps per stage
+  int aoff[kSub], boff[kSub];
+#pragma unroll
+  for (int q = 0; q < kSub; ++q) {
+    aoff[q] = soff(arow, 2 * q + hi);
+    boff[q] = soff(brow, 2 * q + hi);
+  }
+  auto read_frags = [&](const int8_t* buf, int q, i32x4(&fa)[BLK_M], i32x4(&fb)[BLK_N]) {
+#pragma unroll
+    for (int i = 0; i < BLK_M; ++i) fa[i] = *reinterpret_cast<const i32x4*>(buf + aoff[q] + i * 4096);
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j) fb[j] = *reinterpret_cast<const i32x4*>(buf + boff[q] + j * 4096);
+  };
+  auto mfmas = [&](const i32x4(&fa)[BLK_M], const i32x4(&fb)[BLK_N]) {
+#pragma unroll
+    for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+  };
+  // Order the reads issued during a sub-step's MFMAs: read, MFMA, read,
+  // MFMA ... then the remaining MFMAs.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int u = 0; u < BLK_M + BLK_N; ++u) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, BLK_M * BLK_N - (BLK_M + BLK_N), 0);
+  };
+  i32x4 fa0[BLK_M], fb0[BLK_N], fa1[BLK_M], fb1[BLK_N];
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (nk > 1) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + BK, goff[i], ldst + kStage + i * 1024);
+  }
+  read_frags(smem, 0, fa0, fb0);
+  static_assert(kSub == 4, "the sub-step rotation below assumes four 32-byte sub-steps per stage");
   for (int kt = 0; kt < nk; ++kt) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    if (kt + 1 < nk) {
-      const uint32_t dst = ldst + ((kt + 1) & 1) * kStage;
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + 1) * BK, goff[i], dst + i * 1024);
-    }
     const int8_t* cur = smem + (kt & 1) * kStage;
+    read_frags(cur, 1, fa1, fb1);
+    mfmas(fa0, fb0);
+    interleave();
+    read_frags(cur, 2, fa0, fb0);
+    mfmas(fa1, fb1);
+    interleave();
+    read_frags(cur, 3, fa1, fb1);
+    mfmas(fa0, fb0);
+    interleave();
+    // Stage kt + 1 has landed (own loads, then the barrier for everyone
+    // else's) and every wave has finished reading stage kt, whose buffer
+    // then receives stage kt + 2. The body has no other branch: the last
+    // iteration reads sub-step 0 of the other, stale buffer into fa0 / fb0
+    // and never uses it (a branch around those reads would split the
+    // last sub-step's MFMAs over two blocks, and the accumulators' copies at
+    // the join spill).
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 2 < nk) {
+      const uint32_t dst = ldst + (kt & 1) * kStage;
 #pragma unroll
-    for (int q = 0; q < BK / 32; ++q) {
-      const int c = 2 * q + hi;
-      i32x4 fa[BLK_M], fb[BLK_N];
-#pragma unroll
-      for (int i = 0; i < BLK_M; ++i) fa[i] = *reinterpret_cast<const i32x4*>(cur + soff(arow + i * 32, c));
-#pragma unroll
-      for (int j = 0; j < BLK_N; ++j) fb[j] = *reinterpret_cast<const i32x4*>(cur + soff(brow + j * 32, c));
-#pragma unroll
-      for (int i = 0; i < BLK_M; ++i)
-#pragma unroll
-        for (int j = 0; j < BLK_N; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
+      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + 2) * BK, goff[i], dst + i * 1024);
     }
+    read_frags(smem + ((kt + 1) & 1) * kStage, 0, fa0, fb0);
+    mfmas(fa1, fb1);
+    interleave();
   }
 
   const float* s_cosT = nullptr;
