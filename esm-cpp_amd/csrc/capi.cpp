@@ -1437,7 +1437,7 @@ class ObsRun {
 // so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
 // fc2 output of the previous layer (null for the first layer).
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
-               const Meta& md, int T, int nwork, const float* resid_in, ObsRun* ob) {
+               const Meta& md, int T, int nwork, const float* resid_in, ObsRun* ob, int cus) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
   const int ldq_d = pad16(d), ldq_f = pad16(f);
@@ -1472,6 +1472,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.W = L.qkv.w8;
   g.ldw = L.qkv.ldk;
   g.M = T;
+  g.cus = cus;
   g.N = 3 * d;
   g.K = L.qkv.ldk;
   g.a_scale = a.xs;
@@ -1549,6 +1550,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.W = L.out.w8;
   g.ldw = L.out.ldk;
   g.M = T;
+  g.cus = cus;
   g.N = d;
   g.K = L.out.ldk;
   g.a_scale = a.xs;
@@ -1589,6 +1591,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.W = L.fc1.w8;
   g.ldw = L.fc1.ldk;
   g.M = T;
+  g.cus = cus;
   g.N = f;
   g.K = L.fc1.ldk;
   g.a_scale = a.xs;
@@ -1621,6 +1624,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.W = L.fc2.w8;
   g.ldw = L.fc2.ldk;
   g.M = T;
+  g.cus = cus;
   g.N = d;
   g.K = L.fc2.ldk;
   g.a_scale = a.xs;
@@ -1909,6 +1913,11 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   const int nwork = P.nwork;
 
   hipStream_t s = ctx->stream;
+  // Parts staged together run concurrently on their own streams: each
+  // part's GEMMs pick their tile heights for its share of the CUs.
+  int active = 0;
+  for (const auto& q : m->parts) active += q.T > 0 ? 1 : 0;
+  const int cus = active > 1 ? std::max(1, device_cus() / active) : 0;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
   const float* pending = nullptr;  // fc2 output awaiting its residual add
   for (size_t li = 0; li < m->layers.size(); ++li) {
@@ -1920,7 +1929,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     } else if (x86) {
       ESM_TRY(layer_f32_x86(ctx, m, L, round16, a, md, P, ob));
     } else if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending, ob));
+      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending, ob, cus));
       pending = a.ybuf;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));

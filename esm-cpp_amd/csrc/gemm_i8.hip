@@ -365,27 +365,36 @@ __global__ __launch_bounds__(C::THREADS, 2) void gemm_i8_kernel(const GemmI8Args
 // kt's 64 MFMAs per wave run.
 namespace v3 {
 
-constexpr int WAVES_M = 2, WAVES_N = 4;
-constexpr int BLK_N = 2;                          // 32x32 column blocks per wave
-constexpr int BN = WAVES_N * BLK_N * 32;          // 256
+constexpr int WAVES_M = 2;  // waves down the tile
+constexpr int BN = 256;     // tile width
 constexpr int BK = 128;
-constexpr int kThreads = WAVES_M * WAVES_N * 64;  // 512
 
-// Tile height: BLK_M 32x32 row blocks per wave, BM = 64 * BLK_M rows (4: 256,
-// 5: 320). The launcher picks the height that needs the fewer rows' worth of
-// workgroup rounds over the CUs (a 256-row grid that spills a few tiles into
-// one more round often fits in fewer rounds as 320-row tiles), 320 on a tie.
-template <int BLK_M_>
+// Tile height: BLK_M 32x32 row blocks per wave, BM = 64 * BLK_M rows (1: 64,
+// 2: 128, 4: 256, 5: 320). For grids that fill the CUs the launcher picks the
+// height that needs the fewer rows' worth of workgroup rounds (a 256-row grid
+// that spills a few tiles into one more round often fits in fewer rounds as
+// 320-row tiles), 320 on a tie; small-M grids take shorter tiles so that
+// more CUs share the rows (gemm_i8_tile_rows).
+// Wave layout: BLK_N 32x32 column blocks per wave, WAVES_N = 8 / BLK_N waves
+// across the 256 columns. Every launch uses BLK_N 2: eight waves, two per
+// SIMD. (BLK_N 4, four waves of 128x128 with the accumulators in AGPRs, reads
+// 29% fewer LDS bytes per MFMA but ran 11-27% slower: one wave per SIMD
+// leaves the matrix core idle at every barrier and LDS wait.)
+template <int BLK_M_, int BLK_N_ = 2>
 struct Tile {
-  static constexpr int BLK_M = BLK_M_;
+  static constexpr int BLK_M = BLK_M_, BLK_N = BLK_N_;
+  static constexpr int WAVES_N = 8 / BLK_N;
+  static constexpr int kWaves = WAVES_M * WAVES_N;
+  static constexpr int kThreads = kWaves * 64;
+  static_assert(WAVES_N * BLK_N * 32 == BN, "waves x blocks must cover the 256 tile columns");
   static constexpr int BM = WAVES_M * BLK_M * 32;
   static constexpr int kBlocks = (BM + BN) / 8;  // 1 KB blocks per stage
-  static constexpr int kPer = kBlocks / (WAVES_M * WAVES_N);
+  static constexpr int kPer = kBlocks / kWaves;
   static constexpr int kStage = kBlocks * 1024;  // 64 KB (BM 256) / 72 KB (BM 320)
   // RoPE cos / sin rows of a tile staged in LDS, transposed: [32 dims][BM
   // rows + pad], so that a lane reads four consecutive rows of one dim at once.
   static constexpr int kRopeTPitch = BM + 4;
-  static_assert(kBlocks % (WAVES_M * WAVES_N) == 0, "load blocks per wave");
+  static_assert(kBlocks % kWaves == 0, "load blocks per wave");
 };
 
 // One 16-byte-per-lane global -> LDS load (global_load_lds_dwordx4), issued
@@ -453,12 +462,12 @@ __device__ __forceinline__ T* row_at(T* tile, uint32_t ldc, int R, uint32_t lane
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
 // rotary pair. hc: the head's first column relative to the tile origin.
-template <int BLK_M, int EPI, bool FULL, int WHICH>
+template <int BLK_M, int BLK_N, int EPI, bool FULL, int WHICH>
 __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int g, int hc,
                                          int wr0, int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
                                          const float (&bs)[BLK_N], const float* s_cosT, const float* s_sinT, int m0,
                                          int n0) {
-  constexpr int kRopeTPitch = Tile<BLK_M>::kRopeTPitch;
+  constexpr int kRopeTPitch = Tile<BLK_M, BLK_N>::kRopeTPitch;
   const uint32_t ldc = p.ldc;
   const uint32_t dm = p.d_model;
   // Row offsets: the lane's first row (lr0) times the stride once; the rest
@@ -533,7 +542,7 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
 }
 
 // MAX: also reduce |out| into p.row_absmax / p.tensor_absmax (whichever is set).
-template <int BLK_M, int EPI, bool FULL, bool MAX>
+template <int BLK_M, int BLK_N, int EPI, bool FULL, bool MAX>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
                                            const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
@@ -576,11 +585,11 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
         if (!FULL && n0 + hc >= p.N) break;
         const int which = (n0 + hc) / p.d_model;
         if (which == 0)
-          qkv_head<BLK_M, EPI, FULL, 0>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, BLK_N, EPI, FULL, 0>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else if (which == 1)
-          qkv_head<BLK_M, EPI, FULL, 1>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, BLK_N, EPI, FULL, 1>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else
-          qkv_head<BLK_M, EPI, FULL, 2>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
+          qkv_head<BLK_M, BLK_N, EPI, FULL, 2>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
     } else {
@@ -639,10 +648,11 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
   }
 }
 
-template <int BLK_M, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
-  using TL = Tile<BLK_M>;
+template <int BLK_M, int BLK_N, int EPI>
+__global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
+  using TL = Tile<BLK_M, BLK_N>;
   constexpr int BM = TL::BM, kPer = TL::kPer, kStage = TL::kStage, kRopeTPitch = TL::kRopeTPitch;
+  constexpr int kThreads = TL::kThreads, WAVES_N = TL::WAVES_N;
   __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
   __shared__ float s_as[BM], s_ws[BN], s_bs[BN];
   __shared__ int s_pos[BM];
@@ -734,13 +744,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   };
   // Order the reads issued during a sub-step's MFMAs: read, MFMA, read,
   // MFMA ... then the remaining MFMAs.
+  // Short tiles (BLK_M 1) issue more reads than MFMAs per sub-step; the
+  // reads left over go last.
+  constexpr int kReads = BLK_M + BLK_N, kMfmas = BLK_M * BLK_N;
+  constexpr int kPairs = kReads < kMfmas ? kReads : kMfmas;
   auto interleave = [&]() {
 #pragma unroll
-    for (int u = 0; u < BLK_M + BLK_N; ++u) {
+    for (int u = 0; u < kPairs; ++u) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, BLK_M * BLK_N - (BLK_M + BLK_N), 0);
+    if constexpr (kMfmas > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPairs, 0);
+    if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
   };
   i32x4 fa0[BLK_M], fb0[BLK_N], fa1[BLK_M], fb1[BLK_N];
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -814,14 +829,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_i8_v3_kernel(const GemmI8Arg
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
-      epilogue32<BLK_M, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
     else
-      epilogue32<BLK_M, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
   } else {
     if (full)
-      epilogue32<BLK_M, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
     else
-      epilogue32<BLK_M, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
   }
 }
 
@@ -846,29 +861,31 @@ hipError_t launch_v1(const GemmI8Args& p, int epi, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BLK_M>
+template <int BLK_M, int BLK_N = 2>
 hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
   using namespace v3;
-  constexpr int BM = Tile<BLK_M>::BM;
+  constexpr int BM = Tile<BLK_M, BLK_N>::BM;
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const dim3 grid(tiles), block(kThreads);
+  const dim3 grid(tiles), block(Tile<BLK_M, BLK_N>::kThreads);
   switch (epi) {
-    case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiI32>), grid, block, 0, s, p); break;
-    case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32>), grid, block, 0, s, p); break;
-    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32Gelu>), grid, block, 0, s, p); break;
-    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32Resid>), grid, block, 0, s, p); break;
-    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvRope>), grid, block, 0, s, p); break;
-    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiI32>), grid, block, 0, s, p); break;
+    case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32>), grid, block, 0, s, p); break;
+    case kEpiF32Gelu: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32Gelu>), grid, block, 0, s, p); break;
+    case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32Resid>), grid, block, 0, s, p); break;
+    case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRope>), grid, block, 0, s, p); break;
+    case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluQ>), grid, block, 0, s, p); break;
     case kEpiQkvRopeF32:
-      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvRopeF32>), grid, block, 0, s, p);
+      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRopeF32>), grid, block, 0, s, p);
       break;
-    case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, kEpiQkvSplit>), grid, block, 0, s, p); break;
+    case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvSplit>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 std::atomic<int> g_tile_rows{0};
+
+}  // namespace
 
 // CUs of the current device (queried once per device).
 int device_cus() {
@@ -882,27 +899,62 @@ int device_cus() {
   return n;
 }
 
-// Workgroup rounds times tile height: the rows' worth of tile time the grid
-// needs when every round costs one tile's time.
-long tile_cost(int M, int N, int BM, int cus) {
-  const long tiles = static_cast<long>((M + BM - 1) / BM) * ((N + v3::BN - 1) / v3::BN);
-  return (tiles + cus - 1) / cus * BM;
+namespace {
+
+long tiles_of(int M, int N, int BM) {
+  return static_cast<long>((M + BM - 1) / BM) * ((N + v3::BN - 1) / v3::BN);
 }
 
-hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
-  int rows = g_tile_rows.load(std::memory_order_relaxed);
-  if (rows == 0) {
-    // Ties go to 320 rows: at equal rounds the taller tile re-reads less of
-    // A and W (fc1 at config 4: 270 vs 282 us). The GELU and bf16/fp32 RoPE
-    // epilogues stay at 256 rows: at BLK_M = 5 they exceed 256 VGPRs. The
-    // split-word QKV epilogue spills 72 bytes there too, but runs faster at
-    // 320 rows all the same (216 vs 224 us at config 4).
-    const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit;
-    const int cus = device_cus();
-    rows = tall_ok && tile_cost(p.M, p.N, v3::Tile<5>::BM, cus) <= tile_cost(p.M, p.N, v3::Tile<4>::BM, cus) ? 320
-                                                                                                           : 256;
+// Workgroup rounds times tile height: the rows' worth of tile time the grid
+// needs when every round costs one tile's time.
+long tile_cost(int M, int N, int BM, int cus) { return (tiles_of(M, N, BM) + cus - 1) / cus * BM; }
+
+}  // namespace
+
+int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus) {
+  const int forced = g_tile_rows.load(std::memory_order_relaxed);
+  if (forced != 0) return forced;
+  const int all = device_cus();
+  if (cus <= 0) cus = all;
+  // Ties go to 320 rows: at equal rounds the taller tile re-reads less of
+  // A and W (fc1 at config 4: 270 vs 282 us). The GELU and bf16/fp32 RoPE
+  // epilogues stay at 256 rows: at BLK_M = 5 they exceed 256 VGPRs. The
+  // split-word QKV epilogue spills 72 bytes there too, but runs faster at
+  // 320 rows all the same (216 vs 224 us at config 4). Rounds are counted
+  // over the whole device: concurrent launches fill each other's last round.
+  const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit;
+  if (tiles_of(M, N, 256) >= cus)
+    return tall_ok && tile_cost(M, N, 320, all) <= tile_cost(M, N, 256, all) ? 320 : 256;
+  // The 256-row grid leaves CUs idle (one workgroup per CU): shorter tiles
+  // spread the rows over more CUs. Estimated time of a grid = rounds x
+  // (stages + fixed cost) x the per-stage time of the tile height, the
+  // per-stage times relative to the 256-row tile's.
+  static constexpr int kRows[3] = {64, 128, 256};
+  static constexpr double kStage[3] = {0.45, 0.62, 1.0};
+  constexpr double kFixed = 3.0;  // prologue + epilogue, in stages
+  const double stages = K / v3::BK + kFixed;
+  int best = 256;
+  double best_t = 0.0;
+  for (int i = 2; i >= 0; --i) {
+    const long rounds = (tiles_of(M, N, kRows[i]) + cus - 1) / cus;
+    const double t = static_cast<double>(rounds) * stages * kStage[i];
+    if (i == 2 || t < best_t * 0.97) {
+      best = kRows[i];
+      best_t = t;
+    }
   }
-  return rows == 320 ? launch_v3_tile<5>(p, epi, s) : launch_v3_tile<4>(p, epi, s);
+  return best;
+}
+
+namespace {
+
+hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
+  switch (gemm_i8_tile_rows(p.M, p.N, p.K, epi, p.cus)) {
+    case 64: return launch_v3_tile<1>(p, epi, s);
+    case 128: return launch_v3_tile<2>(p, epi, s);
+    case 320: return launch_v3_tile<5>(p, epi, s);
+    default: return launch_v3_tile<4>(p, epi, s);
+  }
 }
 
 }  // namespace
@@ -930,7 +982,7 @@ hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
 }
 
 bool set_gemm_tile_rows(int rows) {
-  if (rows != 0 && rows != 256 && rows != 320) return false;
+  if (rows != 0 && rows != 64 && rows != 128 && rows != 256 && rows != 320) return false;
   g_tile_rows.store(rows, std::memory_order_relaxed);
   return true;
 }

@@ -53,6 +53,7 @@ struct GemmI8Args {
   const float* rope_sin = nullptr;   // [max_len, 32]
   float q_scale = 1.0f;
   float q_prescale = 1.0f;  // kEpiQkvSplit: power of two applied to Q before the split
+  int cus = 0;              // CUs the launch can expect to have to itself (0: the device's)
 };
 
 // Picks the pipelined 256- or 320-row-tile kernel when gemm_i8_pipelined_ok(p) (K a
@@ -63,9 +64,18 @@ bool gemm_i8_pipelined_ok(const GemmI8Args& p);
 // variant 1: general kernel; 2: pipelined kernel (fails on shapes it cannot take).
 hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epilogue, int variant, hipStream_t s);
 // Row height of the pipelined kernel's tile for every later launch in the
-// process: 256, 320, or 0 to pick per launch (fewest rows' worth of
-// workgroup rounds over the device's CUs). False for other values.
+// process: 64, 128, 256, 320, or 0 to pick per launch (gemm_i8_tile_rows).
+// False for other values.
 bool set_gemm_tile_rows(int rows);
+// The pipelined kernel's tile height for an M x N x K launch with epilogue
+// epi on `cus` CUs (0: the current device's): grids of at least one 256-row
+// workgroup per CU take 256 or 320 rows, whichever needs the fewer rows'
+// worth of workgroup rounds (320 on a tie, for the epilogues that fit it);
+// smaller grids take 64, 128 or 256 rows by an estimate of their time.
+int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus);
+// Compute units of the current device (queried once per device; 256 if the
+// query fails).
+int device_cus();
 
 // ---------------------------------------------------------------- FP32 GEMM
 enum GemmF32Epilogue : int {

@@ -144,11 +144,12 @@ int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const 
                            int M, int32_t* C);
 
 /* Row height of the INT8 GEMM's workgroup tile for every later launch in the
- * process: 256, 320, or 0 (default) to pick per launch the height whose grid
- * needs the fewer rows' worth of workgroup rounds over the device's CUs
- * (320 only for the plain dequant / int32 outputs). Results do not depend on
- * it; it exists for tuning and tests. No reference counterpart.
- * INVALID_ARGUMENT for other values. */
+ * process: 64, 128, 256, 320, or 0 (default) to pick per launch. The default
+ * gives grids that fill the device's CUs the height whose grid needs the
+ * fewer rows' worth of workgroup rounds (320 only for the plain dequant,
+ * int32 and split-word outputs), and small-M grids 64, 128 or 256 rows by an
+ * estimate of their time. Results do not depend on it; it exists for tuning
+ * and tests. No reference counterpart. INVALID_ARGUMENT for other values. */
 int esm_gfx950_set_gemm_tile_rows(int rows);
 
 /* Quantised-activation linear: out = fma(float(acc), a_scale[m] * w_scale[n], bias[n]),

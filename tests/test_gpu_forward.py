@@ -104,20 +104,21 @@ def test_w8a8_lm_dense_split_matches_fp32_mfma(dev, w650_small, small_batch):
 
 @pytest.mark.parametrize("per_token", [False, True])
 def test_gemm_tile_rows_do_not_change_logits(dev, w650_small, small_batch, per_token):
-    """The INT8 GEMM's 256- and 320-row tiles (and the automatic choice) give
-    bit-identical logits: the same int32 sums and the same dequant
-    expressions, only the workgroup tiling differs."""
+    """The INT8 GEMM's 64-, 128-, 256- and 320-row tiles (and the automatic
+    choice) give bit-identical logits: the same int32 sums and the same
+    dequant expressions, only the workgroup tiling differs."""
     mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
     m = eg.Model(dev, w650_small, int8=True, act_mode=mode)
     outs = []
     try:
-        for rows in (256, 320, 0):
+        for rows in (256, 320, 64, 128, 0):
             eg.set_gemm_tile_rows(rows)
             outs.append(m.forward_packed(small_batch.ids, small_batch.cu))
     finally:
         eg.set_gemm_tile_rows(0)
         m.free()
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
 
 
 def test_packed_equals_serial(dev, w650_small, small_batch):

@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 import esm_gfx950 as eg
 
 
-@pytest.fixture(params=[0, 256, 320], ids=["rows-auto", "rows-256", "rows-320"])
+@pytest.fixture(params=[0, 64, 128, 256, 320], ids=["rows-auto", "rows-64", "rows-128", "rows-256", "rows-320"])
 def tile_rows(request):
     """INT8 GEMM tile height (0: the per-launch choice); reset afterwards."""
     eg.set_gemm_tile_rows(request.param)
