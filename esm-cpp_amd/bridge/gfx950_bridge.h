@@ -1,0 +1,71 @@
+// Reference-side bridge to the gfx950 backend: the code a maintainer of
+// esm.cpp adds as src/kernels/gfx950_bridge.{h,cpp} so that the facade's
+// `case Isa::Gfx950:` arms (src/kernels/dispatch.cpp:40-262) can forward to
+// libesm_gfx950.so. It is compiled against the reference's own headers
+// (include/esm_cpp/kernels.h, include/esm_cpp/quant.h), so the signatures
+// below are checked against the facade they stand in for.
+//
+// Every arm takes the facade's arguments in the facade's order, all host
+// pointers, stages them on the device, runs the gfx950 kernel and copies the
+// result back. It returns false when no gfx950 device is present or the
+// device call fails; the facade then takes its CPU arm, the convention
+// LinearProj follows for the Apple backends (src/model.cpp:877-905):
+//
+//   case Isa::Gfx950:
+//     if (gfx950::LinearInt8(A, W, bias, C, M, N, K)) return;
+//     return LinearInt8Ref(A, W, bias, C, M, N, K);
+//
+// Threading follows the reference's Model contract (model.h:176-181): one
+// process-wide context, one stream; calls from several threads serialise on
+// a mutex.
+#pragma once
+
+#include <cstddef>
+
+#include "esm_cpp/quant.h"
+#include "esm_gfx950.h"
+
+namespace esm::gfx950 {
+
+// The process-wide context on device 0, created on first use; null when no
+// gfx950 device is present (then every arm returns false).
+esm_gfx950_ctx* Ctx();
+
+// The last device error message ("" when none).
+const char* LastError();
+
+// esm::kernels::Linear (kernels.h:19-20).
+bool Linear(const float* A, const float* W, const float* bias, float* C, int M, int N, int K);
+
+// esm::kernels::LinearInt8 (kernels.h:56-57, dispatch.cpp:80-103) with the
+// reference's dynamic per-tensor activation scale. The weight's device copy
+// is built on first use (BuildKernelCache's role, pack.cpp:107-117) and kept
+// until ReleaseWeight or exit; a QuantizedTensor whose packed data changed is
+// uploaded again.
+bool LinearInt8(const float* A, const esm::quant::QuantizedTensor& W, const float* bias, float* C, int M, int N,
+                int K);
+void ReleaseWeight(const esm::quant::QuantizedTensor& W);
+
+// esm::kernels::LayerNorm (kernels.h:32-33).
+bool LayerNorm(const float* x, const float* gamma, const float* beta, float eps, float* out, int num_rows, int d);
+
+// esm::kernels::Gelu (kernels.h:35).
+bool Gelu(const float* x, float* out, std::size_t n);
+
+// esm::kernels::ResidualAddInplace (kernels.h:24) and ScaleInplace (:29).
+bool ResidualAddInplace(float* y, const float* x, std::size_t n);
+bool ScaleInplace(float* x, std::size_t n, float scale);
+
+// esm::kernels::RopeApplyVarlen (kernels.h:90-92): x [T, H, head_dim] in
+// place; cos/sin [max_seqlen, head_dim], of which the rows up to the longest
+// sequence of cu_seqlens are read.
+bool RopeApplyVarlen(float* x, const float* cos, const float* sin, const int* cu_seqlens, int batch_size,
+                     int num_heads, int head_dim);
+
+// esm::kernels::AttentionVarlen (kernels.h:119-121): the split-fp16 MFMA
+// kernel at head_dim 64 (fp32-level results), the scalar fp32 kernel for any
+// other head_dim <= 128.
+bool AttentionVarlen(const float* q, const float* k, const float* v, const int* cu_seqlens, int batch_size,
+                     int num_heads, int head_dim, float* out);
+
+}  // namespace esm::gfx950

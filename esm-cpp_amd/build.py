@@ -1,6 +1,6 @@
 """Builds libesm_gfx950.so (HIP kernels + C ABI) in-tree for gfx950.
 
-Usage: python esm-cpp_amd/build.py [--jobs N]
+Usage: python esm-cpp_amd/build.py [--jobs N] [--reference-include <esm.cpp>/include]
 
 Each translation unit is compiled with hipcc for --offload-arch=gfx950 and
 linked into esm-cpp_amd/lib/libesm_gfx950.so. Packed-fp32 instruction
@@ -61,9 +61,34 @@ def build(jobs: int = 4) -> str:
     return LIB
 
 
+BRIDGE_SOURCES = ["gfx950_bridge.cpp", "bridge_capi.cpp"]
+BRIDGE_LIB = os.path.join(LIBDIR, "libesm_gfx950_bridge.so")
+
+
+def build_bridge(reference_include: str) -> str:
+    """Builds lib/libesm_gfx950_bridge.so: the reference-side bridge
+    (bridge/), compiled with the host compiler against the reference's own
+    headers (reference_include = <esm.cpp>/include) and linked to
+    libesm_gfx950.so only. Needs build() first."""
+    cxx = os.environ.get("CXX", "g++")
+    srcs = [os.path.join(HERE, "bridge", f) for f in BRIDGE_SOURCES]
+    tmp = BRIDGE_LIB + ".tmp"
+    cmd = [cxx, "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{reference_include}", f"-I{INCLUDE}",
+           *srcs, f"-L{LIBDIR}", "-lesm_gfx950", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib", "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"bridge build failed:\n{res.stderr}")
+    os.replace(tmp, BRIDGE_LIB)
+    return BRIDGE_LIB
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--reference-include", default=None,
+                    help="also build the reference-side bridge against <esm.cpp>/include")
     args = ap.parse_args()
     print(build(args.jobs))
+    if args.reference_include:
+        print(build_bridge(args.reference_include))
     sys.exit(0)

@@ -16,6 +16,8 @@ acids, reference src/tokenizer.cpp:12-17), eos = 2; no masks, no pads.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
+import os
 import zlib
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
@@ -110,38 +112,51 @@ def make_weights(cfg: EsmConfig, seed: int, int8: bool = False, smooth: bool = T
     w = EsmWeights(cfg)
     F = w.f32
     F["embed"] = _normal(seed, "embed", (V, d))
-    for i in range(cfg.num_layers):
+
+    def layer(i):
+        """Layer i's tensors (fp32 dict, int8 dict); every tensor draws from
+        its own stream, so layers can be made in any order or concurrently."""
         p = f"layers.{i}."
+        f32, i8 = {}, {}
         for ln in ("attn_ln", "ffn_ln"):
-            F[p + ln + ".weight"] = _normal(seed, p + ln + ".weight", (d,), mean=1.0)
-            F[p + ln + ".bias"] = _normal(seed, p + ln + ".bias", (d,))
+            f32[p + ln + ".weight"] = _normal(seed, p + ln + ".weight", (d,), mean=1.0)
+            f32[p + ln + ".bias"] = _normal(seed, p + ln + ".bias", (d,))
         shapes = {"q": (d, d), "k": (d, d), "v": (d, d), "out": (d, d), "fc1": (f, d), "fc2": (d, f)}
         lin = {n: _normal(seed, p + n + ".weight", s) for n, s in shapes.items()}
         for n, s in shapes.items():
-            F[p + n + ".bias"] = _normal(seed, p + n + ".bias", (s[0],))
+            f32[p + n + ".bias"] = _normal(seed, p + n + ".bias", (s[0],))
         if int8 and smooth:
             # Site 1: attn_ln -> {q,k,v}
             s1 = _smooth_factors(seed, p + "smooth.attn_ln", d)
-            F[p + "attn_ln.weight"] = F[p + "attn_ln.weight"] / s1
-            F[p + "attn_ln.bias"] = F[p + "attn_ln.bias"] / s1
+            f32[p + "attn_ln.weight"] = f32[p + "attn_ln.weight"] / s1
+            f32[p + "attn_ln.bias"] = f32[p + "attn_ln.bias"] / s1
             for n in ("q", "k", "v"):
                 lin[n] = lin[n] * s1[None, :]
             # Site 2: v output channels -> out_proj input channels
             s2 = _smooth_factors(seed, p + "smooth.attn_out", d)
-            F[p + "v.bias"] = F[p + "v.bias"] / s2
+            f32[p + "v.bias"] = f32[p + "v.bias"] / s2
             lin["v"] = lin["v"] / s2[:, None]
             lin["out"] = lin["out"] * s2[None, :]
             # Site 3: ffn_ln -> fc1
             s3 = _smooth_factors(seed, p + "smooth.ffn_ln", d)
-            F[p + "ffn_ln.weight"] = F[p + "ffn_ln.weight"] / s3
-            F[p + "ffn_ln.bias"] = F[p + "ffn_ln.bias"] / s3
+            f32[p + "ffn_ln.weight"] = f32[p + "ffn_ln.weight"] / s3
+            f32[p + "ffn_ln.bias"] = f32[p + "ffn_ln.bias"] / s3
             lin["fc1"] = lin["fc1"] * s3[None, :]
         for n, W in lin.items():
             W = W.astype(np.float32, copy=False)
             if int8:
-                w.i8[p + n] = quantize_weight(W)
+                i8[p + n] = quantize_weight(W)
             if keep_f32_linears:
-                F[p + n + ".weight"] = W
+                f32[p + n + ".weight"] = W
+        return f32, i8
+
+    # numpy's generators and array arithmetic release the GIL on large
+    # arrays, so layers are made on a few threads (same values as in order).
+    workers = max(1, min(8, os.cpu_count() or 1, cfg.num_layers))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
+        for f32, i8 in ex.map(layer, range(cfg.num_layers)):
+            F.update(f32)
+            w.i8.update(i8)
     F["final_ln.weight"] = _normal(seed, "final_ln.weight", (d,), mean=1.0)
     F["final_ln.bias"] = _normal(seed, "final_ln.bias", (d,))
     F["lm_head.dense.weight"] = _normal(seed, "lm_head.dense.weight", (d, d))

@@ -1,0 +1,45 @@
+"""The reference-side bridge (esm-cpp_amd/bridge/): built against the
+reference's own headers (include/esm_cpp/kernels.h, quant.h), it loads,
+exports its C entry points, links only libesm_gfx950.so, and with no gfx950
+device every arm reports that the caller must take its CPU arm."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from bridge_lib import BRIDGE_LIB, SIGNATURES, Bridge
+
+pytestmark = pytest.mark.skipif(not os.path.exists(BRIDGE_LIB),
+                                reason="bridge not built (needs the reference headers at build time)")
+
+
+def test_bridge_exports_its_entry_points():
+    b = Bridge()
+    for name in SIGNATURES:
+        assert hasattr(b.lib, name), name
+
+
+def test_bridge_links_only_the_gfx950_library():
+    """Nothing of the reference is linked: the arms are header-only users of
+    its types (QuantizedTensor) and call the C ABI."""
+    out = subprocess.run(["ldd", BRIDGE_LIB], capture_output=True, text=True, check=True).stdout
+    assert "libesm_gfx950.so" in out
+    assert "esmref" not in out and "oracle" not in out
+    nm = subprocess.run(["nm", "-D", "--undefined-only", BRIDGE_LIB], capture_output=True, text=True,
+                        check=True).stdout
+    assert "esm_gfx950_linear_i8" in nm and "esm_gfx950_attention_varlen" in nm
+    assert "_ZN3esm7kernels" not in nm and "_ZN3esm5quant" not in nm  # no reference symbol is needed
+
+
+def test_arms_fall_back_without_a_device():
+    """On a host without a gfx950 device an arm returns 0 (take the CPU arm)
+    with a message; on a GPU host it runs (covered by test_gpu_bridge)."""
+    b = Bridge()
+    x = np.linspace(-3, 3, 64, dtype=np.float32)
+    out = np.zeros_like(x)
+    ran = b.lib.esm_gfx950_bridge_gelu(x.ctypes.data, out.ctypes.data, x.size)
+    if ran == 0:
+        assert b.error()
+    else:
+        assert np.all(np.isfinite(out))

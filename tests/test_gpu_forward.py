@@ -190,6 +190,66 @@ def test_config4_varlen_full_forward_properties(dev):
     m.free()
 
 
+def test_config4_uniform_full_forward(dev, oracle):
+    """650M W8A8, configuration 4's uniform 8 x 256 batch (T = 2,048, the
+    small-M GEMM tiles): all 33 layers give finite logits and packed ==
+    serial; two layers over the whole batch match the oracle's same-mode
+    forward at the W8A8 bar (corr >= 0.9999), per token and per tensor."""
+    batch = syn.config4_uniform_batch()
+    w = syn.make_weights(syn.ESM2_650M, seed=20261201 + 4, int8=True, keep_f32_linears=False)
+    m = eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    logits = m.forward_packed(batch.ids, batch.cu)
+    assert logits.shape == (2048, 33) and np.all(np.isfinite(logits))
+    for b in (0, 5, 7):
+        s0, s1 = int(batch.cu[b]), int(batch.cu[b + 1])
+        solo = m.forward_packed(batch.ids[s0:s1], np.array([0, s1 - s0], np.int32))
+        np.testing.assert_allclose(logits[s0:s1], solo, rtol=1e-4, atol=1e-4)
+    m.set_parts(2)
+    np.testing.assert_array_equal(m.forward_packed(batch.ids, batch.cu), logits)
+    m.free()
+    del w
+    w2 = syn.make_weights(syn.ESM2_650M.with_layers(2), seed=20261201 + 4, int8=True, keep_f32_linears=False)
+    for per_token in (True, False):
+        mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+        m = eg.Model(dev, w2, int8=True, act_mode=mode)
+        got = m.forward_packed(batch.ids, batch.cu)
+        m.free()
+        want = oracle.forward_packed(w2, batch, int8=True, per_token=per_token)
+        c = corr(got, want)
+        print(f"uniform 8x256, 2 layers, per_token={per_token}: corr {c:.6f}")
+        assert c >= 0.9999, c
+
+
+def test_config5_full_workload(dev, oracle):
+    """ESM-2 3B W8A8, configuration 5's workload (36 layers, 64 sequences of
+    log-uniform 50..1024 tokens, T = 20,321): finite logits and packed ==
+    serial for the longest, shortest and median sequences; one layer over
+    those three sequences (T = 1,265, the 963-token one among them) matches
+    the oracle's same-mode forward at the W8A8 bar."""
+    batch = syn.config5_batch()
+    w = syn.make_weights(syn.ESM2_3B, seed=20261201 + 5, int8=True, keep_f32_linears=False)
+    m = eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    logits = m.forward_packed(batch.ids, batch.cu)
+    assert logits.shape == (batch.total_tokens, 33) and np.all(np.isfinite(logits))
+    order = np.argsort(batch.lengths, kind="stable")
+    picks = [int(order[-1]), int(order[0]), int(order[len(order) // 2])]
+    for b in picks:
+        s0, s1 = int(batch.cu[b]), int(batch.cu[b + 1])
+        solo = m.forward_packed(batch.ids[s0:s1], np.array([0, s1 - s0], np.int32))
+        np.testing.assert_allclose(logits[s0:s1], solo, rtol=1e-4, atol=1e-4)
+    m.free()
+    del w
+    sub = batch.subset(picks)
+    w1 = syn.make_weights(syn.ESM2_3B.with_layers(1), seed=20261201 + 5, int8=True, keep_f32_linears=False)
+    m = eg.Model(dev, w1, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    got = m.forward_packed(sub.ids, sub.cu)
+    m.free()
+    want = oracle.forward_packed(w1, sub, int8=True, per_token=True)
+    c = corr(got, want)
+    print(f"config 5, 1 layer of 3B over lengths {sub.lengths.tolist()}: corr {c:.6f}")
+    assert c >= 0.9999, c
+
+
 @pytest.mark.parametrize("parts", [2, 3, 4])
 def test_parts_match_single_stream(dev, w650_small, small_batch, parts):
     """Concurrent sequence groups on separate streams: every row depends only
