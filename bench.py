@@ -47,6 +47,7 @@ from esm_gfx950 import synthetic as syn  # noqa: E402
 MI355X_PEAK_INT8_TOPS = 5000.0  # dense int8, 5.0 POP/s
 MI355X_PEAK_HBM_GBS = 8000.0
 GEMM_SITES = ("qkv", "out", "fc1", "fc2")
+ROW_SITES = ("ln_quant", "ln_quant_first", "attn_quant", "gelu_quant")
 FIXTURE = os.path.join(ROOT, "tests", "golden", "full_depth_650m.npz")
 
 
@@ -92,7 +93,7 @@ def measure(dev, model, batch, cfg, steps, warmup, parts):
         model.forward_device(logits)
     ms_events = dev.timer_stop() / steps
     sites = {}
-    for site in GEMM_SITES + ("attention", "lm_dense"):
+    for site in GEMM_SITES + ("attention", "lm_dense") + ROW_SITES:
         n, tot = dev.kernel_timing_query(site)
         if n:
             sites[site] = {"launches": n, "avg_us": round(tot / n * 1000, 2), "ms_per_step": round(tot / steps, 3)}
@@ -138,6 +139,25 @@ def roofline_of(sites, T, cfg, batch, workload):
                           "frac_of_2500": round(flop / t / 1e12 / 2500.0, 4), "min_bytes": bytes_min,
                           "gbs": round(bytes_min / t / 1e9, 1),
                           "frac_of_hbm": round(bytes_min / t / 1e9 / MI355X_PEAK_HBM_GBS, 4)}
+    # HBM-bound row kernels (per-token mode): algorithmic bytes per launch
+    # over the event-timed duration, against the 8 TB/s peak. RoPE has no
+    # kernel of its own: it runs in the QKV GEMM's epilogue.
+    d, f = cfg.hidden_size, cfg.intermediate_size
+    row_bytes = {
+        "ln_quant": T * d * (4 + 4 + 4 + 1) + 4 * T,   # hidden + residual in, hidden + int8 out, scales
+        "ln_quant_first": T * d * (4 + 1) + 4 * T,     # hidden in, int8 out, scales
+        "attn_quant": T * d * (4 + 1) + 4 * T,         # fp32 in, int8 out, scales
+        "gelu_quant": T * f * (4 + 1) + 4 * T,         # fc1 fp32 in, int8 out, scales
+    }
+    rows = {}
+    for site, b in row_bytes.items():
+        if site in sites:
+            t = sites[site]["avg_us"] * 1e-6
+            rows[site] = {"bytes_per_launch": b, "avg_us": sites[site]["avg_us"], "gbs": round(b / t / 1e9, 1),
+                          "frac_of_hbm": round(b / t / 1e9 / MI355X_PEAK_HBM_GBS, 4)}
+    if rows:
+        rows["rope"] = "fused into the QKV GEMM epilogue (no separate pass)"
+        r["row_kernels"] = rows
     return r
 
 

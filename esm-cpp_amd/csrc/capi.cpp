@@ -1450,8 +1450,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
 
   // (residual) + attn LN + activation quant
   if (tok) {
+    ESM_TRY(ctx->time_begin(resid_in ? "ln_quant" : "ln_quant_first", &slot));
     ESM_HIP(ctx, launch_layernorm_quant(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
                                         a.xs, s));
+    ESM_TRY(ctx->time_end(slot));
     if (ob) {
       // The fused kernel keeps the LN output in registers: recompute it
       // (hidden already holds the residual sum) for the observer.
@@ -1538,7 +1540,9 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   ESM_TRY(ctx->time_end(slot));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   if (tok) {
+    ESM_TRY(ctx->time_begin("attn_quant", &slot));
     ESM_HIP(ctx, launch_quant_rows(a.attn, 0, d, T, d, a.xq, ldq_d, a.xs, s));
+    ESM_TRY(ctx->time_end(slot));
   } else {
     ESM_HIP(ctx, launch_quant_tensor(a.attn, d, T, d, amax_attn, a.xq, ldq_d, a.xs, s));
   }
@@ -1565,8 +1569,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   // residual + ffn LN + quant. The observer sees the LN output before the
   // first-block fp16 rounding (reference src/model.cpp:1023-1033).
   if (tok) {
+    ESM_TRY(ctx->time_begin("ln_quant", &slot));
     ESM_HIP(ctx, launch_layernorm_quant(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
                                         a.xs, s, round16));
+    ESM_TRY(ctx->time_end(slot));
     if (ob) {
       ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
       ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
@@ -1606,7 +1612,9 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
     ESM_TRY(ctx->time_end(slot));
     if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 1));
+    ESM_TRY(ctx->time_begin("gelu_quant", &slot));
     ESM_HIP(ctx, launch_gelu_quant_rows(a.inter, f, T, f, a.xq, ldq_f, a.xs, s));
+    ESM_TRY(ctx->time_end(slot));
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 3, 1, 0.0f, s));
     g.tensor_absmax = a.absmax + 3;

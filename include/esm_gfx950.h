@@ -117,10 +117,13 @@ int esm_gfx950_timer_stop(esm_gfx950_ctx* ctx, float* elapsed_ms);
 
 /* Per-kernel timing: while enabled, every launch of a timed site inside the
  * forward -- "qkv", "attention", "out", "fc1", "fc2" (INT8 GEMMs and the
- * attention kernel), "lm_dense" -- and of esm_gfx950_attention_varlen_bf16
- * ("attention") is bracketed by HIP events on the context stream. Enabling
- * (or disabling) resets the record; the query returns the number of timed
- * launches of `site` and their summed duration. */
+ * attention kernel), "lm_dense", and in per-token W8A8 mode the row kernels
+ * "ln_quant" (residual + LayerNorm + quant), "ln_quant_first" (the first
+ * layer's, with no residual), "attn_quant", "gelu_quant" -- and of
+ * esm_gfx950_attention_varlen_bf16 ("attention") is bracketed by HIP events
+ * on the context stream. Enabling (or disabling) resets the record; the
+ * query returns the number of timed launches of `site` and their summed
+ * duration. */
 int esm_gfx950_kernel_timing(esm_gfx950_ctx* ctx, int enable);
 int esm_gfx950_kernel_timing_query(esm_gfx950_ctx* ctx, const char* site, int* launches, double* total_ms);
 
