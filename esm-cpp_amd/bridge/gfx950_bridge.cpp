@@ -67,17 +67,29 @@ bool download(void* host, const void* dev, std::size_t bytes) {
 // Device weights by QuantizedTensor. The reference-side integration keeps
 // the handle in a new QuantizedTensor member, freed by its destructor; this
 // bridge, which cannot change that struct, keeps it in a side table keyed by
-// the tensor's address and checked against its packed data.
+// the tensor's address and checked against its packed data pointer, shape and
+// a checksum of its scales, so that a tensor rebuilt in reused storage is
+// uploaded again.
 struct DevWeight {
   esm_gfx950_weight* w = nullptr;
   const std::int8_t* data = nullptr;
   int N = 0, K = 0;
+  std::uint64_t scale_sum = 0;
 };
+
+// FNV-1a over the scales' bytes: N floats, cheap next to any call's staging.
+std::uint64_t scale_checksum(const esm::quant::QuantizedTensor& W) {
+  std::uint64_t h = 1469598103934665603ull;
+  const auto* b = reinterpret_cast<const unsigned char*>(W.per_channel_scales.data());
+  for (std::size_t i = 0; i < W.per_channel_scales.size() * sizeof(float); ++i) h = (h ^ b[i]) * 1099511628211ull;
+  return h;
+}
 std::unordered_map<const esm::quant::QuantizedTensor*, DevWeight> g_weights;
 
 esm_gfx950_weight* device_weight(const esm::quant::QuantizedTensor& W) {
   DevWeight& e = g_weights[&W];
-  if (e.w && e.data == W.packed.data() && e.N == W.N && e.K == W.K) return e.w;
+  const std::uint64_t sum = scale_checksum(W);
+  if (e.w && e.data == W.packed.data() && e.N == W.N && e.K == W.K && e.scale_sum == sum) return e.w;
   if (e.w) esm_gfx950_weight_free(Ctx(), e.w);
   e = DevWeight();
   if (static_cast<std::size_t>(W.N) * W.K != W.packed.size() ||
@@ -94,6 +106,7 @@ esm_gfx950_weight* device_weight(const esm::quant::QuantizedTensor& W) {
   e.data = W.packed.data();
   e.N = W.N;
   e.K = W.K;
+  e.scale_sum = sum;
   return e.w;
 }
 
@@ -104,7 +117,12 @@ esm_gfx950_ctx* Ctx() {
   return ctx;
 }
 
-const char* LastError() { return g_error.c_str(); }
+const char* LastError() {
+  thread_local std::string copy;
+  std::lock_guard<std::mutex> lk(g_mu);
+  copy = g_error;
+  return copy.c_str();
+}
 
 bool Linear(const float* A, const float* W, const float* bias, float* C, int M, int N, int K) {
   std::lock_guard<std::mutex> lk(g_mu);

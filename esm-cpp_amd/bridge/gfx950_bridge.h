@@ -40,8 +40,11 @@ bool Linear(const float* A, const float* W, const float* bias, float* C, int M, 
 // esm::kernels::LinearInt8 (kernels.h:56-57, dispatch.cpp:80-103) with the
 // reference's dynamic per-tensor activation scale. The weight's device copy
 // is built on first use (BuildKernelCache's role, pack.cpp:107-117) and kept
-// until ReleaseWeight or exit; a QuantizedTensor whose packed data changed is
-// uploaded again.
+// until ReleaseWeight or exit. It is found again by the tensor's address and
+// checked against its packed data pointer, shape and scales; a tensor whose
+// int8 values change in place keeps its old device copy, so call
+// ReleaseWeight before changing or destroying a tensor (the integration that
+// owns QuantizedTensor frees the copy in its destructor).
 bool LinearInt8(const float* A, const esm::quant::QuantizedTensor& W, const float* bias, float* C, int M, int N,
                 int K);
 void ReleaseWeight(const esm::quant::QuantizedTensor& W);
