@@ -269,8 +269,16 @@ constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
 // banks.
 constexpr int kVPitchX = 160;
 static_assert(KCX == 64, "the V^T swizzle covers 16 key quads");
+// PAIRED: the long-sequence variant's swizzle, quad ^ ((dim / 4) & 11). It
+// leaves bit 2 of the quad index alone, so quads q and q + 4 (q < 4 mod 8:
+// the two key blocks a lane reads for one PV fragment) stay 32 bytes apart
+// and load as one ds_read2_b64 straight into the fragment's registers (no
+// register moves to assemble it); the staging writes meet 2-way bank
+// conflicts instead.
+template <bool PAIRED = false>
 __device__ __forceinline__ int vt_off(int dim, int key) {
-  return dim * kVPitchX + ((((key >> 2) ^ (dim >> 2)) & 15) << 3) + ((key & 3) << 1);
+  constexpr int mask = PAIRED ? 11 : 15;
+  return dim * kVPitchX + ((((key >> 2) ^ ((dim >> 2) & mask)) & 15) << 3) + ((key & 3) << 1);
 }
 
 // Low (sel_lo) or high (sel_hi) 16-bit halves of two words, packed: the hi
@@ -294,6 +302,12 @@ __device__ __forceinline__ void unpack8(const uint4& a, const uint4& b, f16x8* h
   *lo = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(l));
 }
 
+// a * b rounded on its own: the product is never fused into a later add.
+__device__ __forceinline__ float mul_unfused(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
 // Raw v_exp_f32: 2^x for results >= 2^-126 exactly as exp2f, 0 below (the
 // library's exp2f adds a rescale for subnormal results; probabilities under
 // 2^-126 of the row maximum do not change an fp32 softmax sum).
@@ -309,6 +323,16 @@ __device__ __forceinline__ void split8(const float (&p)[8], f16x8* hi, f16x8* lo
   *lo = __builtin_bit_cast(f16x8, *reinterpret_cast<const uint4*>(l));
 }
 
+// LONG: the variant for batches with sequences past 256 tokens, whose many
+// key chunks per work item make the chunk loop's VALU work count: the
+// PAIRED V^T swizzle (no register moves per PV fragment), and O and the
+// running sum rescaled only when some lane's running maximum moved (else
+// alpha = exp2(0) = 1 exactly, so skipping it changes no bit). Measured on
+// configuration 5 (3B, sequences up to 963 tokens): 418 vs 428 us per layer.
+// Short-sequence batches keep the other variant: there the leaner kernel ran
+// as fast in isolation, but beside the second sequence group's kernels the
+// configuration-4 forward got 1% slower.
+template <bool LONG>
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     const uint32_t* __restrict__ q, const uint32_t* __restrict__ k,
     const uint32_t* __restrict__ v, int ld, float s2, const int* __restrict__ cu,
@@ -412,7 +436,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int off = vt_off(dq * 4 + j, key0);
+        const int off = vt_off<LONG>(dq * 4 + j, key0);
         *reinterpret_cast<uint32_t*>(sVh + off) = halves(xa[j], xb[j], kSelLo);
         *reinterpret_cast<uint32_t*>(sVl + off) = halves(xa[j], xb[j], kSelHi);
       }
@@ -447,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     // running max and the rescale of O happen first; the probabilities are
     // then formed, summed and split per key-block pair inside the PV loop, so
     // only one pair's fp16 fragments are live at a time.
-    float mnew[2];
+    float mnew[2], al[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       float cmax = -INFINITY;
@@ -457,7 +481,11 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = kb * 16 + lg * 4 + i;
-            const float sv = (FULLC || key < nkeys) ? s[kb][qb][i] * s2 : -INFINITY;
+            // The scaled score is rounded once (no fused multiply-add with
+            // the exponent's subtraction, which the compiler would form only
+            // in some instantiations): the row's largest probability is then
+            // exp2(0) = 1 exactly, and every variant rounds alike.
+            const float sv = (FULLC || key < nkeys) ? mul_unfused(s[kb][qb][i], s2) : -INFINITY;
             s[kb][qb][i] = sv;
             cmax = fmaxf(cmax, sv);
           }
@@ -466,11 +494,18 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
       mnew[qb] = fmaxf(mrun[qb], cmax);
-      const float alpha = exp2_raw(mrun[qb] - mnew[qb]);
-      mrun[qb] = mnew[qb];
-      lrun[qb] *= alpha;
+      // The running sum takes its rescale in one fused step with the chunk's
+      // first probabilities, lrun = fma(lrun, alpha, psum), in both variants,
+      // so that skipping the rescale (alpha = 1: fma(lrun, 1, psum) is the
+      // rounded sum) changes no bit.
+      al[qb] = 1.0f;
+      if (!LONG || __builtin_amdgcn_ballot_w64(mnew[qb] != mrun[qb]) != 0) {
+        const float alpha = exp2_raw(mrun[qb] - mnew[qb]);
+        al[qb] = alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+        for (int db = 0; db < 4; ++db) o[qb][db] *= alpha;
+      }
+      mrun[qb] = mnew[qb];
     }
 
     // O^T += V^T P^T over key-block pairs, three MFMAs per product.
@@ -490,12 +525,13 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
             psum += pr[j];
           }
           split8(pr, &pfh[qb], &pfl[qb]);
-          lrun[qb] += psum;
+          lrun[qb] = kp == 0 ? __builtin_fmaf(lrun[qb], al[qb], psum) : lrun[qb] + psum;
         }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const int dim = db * 16 + lr;
-          const int ca = vt_off(dim, (2 * kp) * 16 + lg * 4), cb = vt_off(dim, (2 * kp + 1) * 16 + lg * 4);
+          const int ca = vt_off<LONG>(dim, (2 * kp) * 16 + lg * 4);
+          const int cb = LONG ? ca + 32 : vt_off<LONG>(dim, (2 * kp + 1) * 16 + lg * 4);
           const f16x4 vah = *reinterpret_cast<const f16x4*>(sVh + ca);
           const f16x4 vbh = *reinterpret_cast<const f16x4*>(sVh + cb);
           const f16x4 val = *reinterpret_cast<const f16x4*>(sVl + ca);
@@ -622,11 +658,15 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 
 hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v, int ld, float q_prescale,
                                const int* cu_seqlens, const AttnWork* work, int num_work, float* out, int ld_out,
-                               hipStream_t s) {
+                               int max_len, hipStream_t s) {
   if (num_work <= 0) return hipSuccess;
   const float s2 = kLog2e / q_prescale;
-  hipLaunchKernelGGL(attn_x3_kernel, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work, out,
-                     ld_out);
+  if (max_len > kAttnLongSeq)
+    hipLaunchKernelGGL(attn_x3_kernel<true>, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work,
+                       out, ld_out);
+  else
+    hipLaunchKernelGGL(attn_x3_kernel<false>, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work,
+                       out, ld_out);
   return hipGetLastError();
 }
 

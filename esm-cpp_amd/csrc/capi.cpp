@@ -739,9 +739,12 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
     ESM_HIP(ctx, launch_pack_split(q, ld, T, ld, kQPrescale, qw, ld, ctx->stream));
     ESM_HIP(ctx, launch_pack_split(k, ld, T, ld, 1.0f, kw, ld, ctx->stream));
     ESM_HIP(ctx, launch_pack_split(v, ld, T, ld, 1.0f, vw, ld, ctx->stream));
+    int max_len = 0;
+    for (int b = 0; b < batch_size; ++b) max_len = std::max(max_len, cu_seqlens[b + 1] - cu_seqlens[b]);
     int slot;
     ESM_TRY(ctx->time_begin("attention", &slot));
-    ESM_HIP(ctx, launch_attention_x3(qw, kw, vw, ld, kQPrescale, d_cu, d_work, nwork, out, ld, ctx->stream));
+    ESM_HIP(ctx, launch_attention_x3(qw, kw, vw, ld, kQPrescale, d_cu, d_work, nwork, out, ld, max_len,
+                                     ctx->stream));
     ESM_TRY(ctx->time_end(slot));
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
@@ -1437,7 +1440,7 @@ class ObsRun {
 // so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
 // fc2 output of the previous layer (null for the first layer).
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
-               const Meta& md, int T, int nwork, const float* resid_in, ObsRun* ob, int cus) {
+               const Meta& md, int T, int nwork, int max_len, const float* resid_in, ObsRun* ob, int cus) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
   const int ldq_d = pad16(d), ldq_f = pad16(f);
@@ -1527,7 +1530,8 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   if (f32qkv) {
     if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
       const auto* w = reinterpret_cast<const uint32_t*>(a.qkv);
-      ESM_HIP(ctx, launch_attention_x3(w, w + d, w + 2 * d, 3 * d, kQPrescale, md.cu, md.work, nwork, a.attn, d, s));
+      ESM_HIP(ctx, launch_attention_x3(w, w + d, w + 2 * d, 3 * d, kQPrescale, md.cu, md.work, nwork, a.attn, d,
+                                       max_len, s));
     } else {
       ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
                                         d, s));
@@ -1937,7 +1941,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     } else if (x86) {
       ESM_TRY(layer_f32_x86(ctx, m, L, round16, a, md, P, ob));
     } else if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, pending, ob, cus));
+      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, P.maxL, pending, ob, cus));
       pending = a.ybuf;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));

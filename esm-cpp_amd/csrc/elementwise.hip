@@ -269,6 +269,66 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
   if (lane == 0) scales[row] = scale;
 }
 
+// The same pass with a row split over the block's four waves, for rows
+// wider than 5120 (ESM-2 3B's d_ff of 10240): wave w holds columns
+// [w * NV * 256, (w + 1) * NV * 256), the waves' maxima meet in LDS, and each
+// wave quantises its own part. One wave per 10240-wide row needs 160
+// registers per lane for the row (three waves per SIMD); split four ways it
+// needs 40 (seven): configuration 5's forward measured 87.6 against 88.7 ms.
+// At 5120 columns the split measured 160 against 162 us and left the
+// configuration-4 forward unchanged, so that width keeps the one-wave kernel.
+// Bytes and scales are those of gelu_quant_rows_kernel (the maximum does not
+// depend on the order it is taken in).
+template <int NV>
+__global__ __launch_bounds__(256) void gelu_quant_rows_split_kernel(
+    const float* __restrict__ x, int ldx, int rows, int cols,
+    int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
+  __shared__ float s_max[kRowsPerBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = blockIdx.x;  // uniform: the whole block takes one row
+  const int c0 = wave * NV * 256;
+  const float* xr = x + static_cast<size_t>(row) * ldx;
+  // Every load is issued before the first use; chunks past the row re-read
+  // its start (in bounds) and are zeroed (gelu(0) == 0 keeps them zero).
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = c0 + (j * 64 + lane) * 4;
+    v[j] = *reinterpret_cast<const float4*>(xr + (c < cols ? c : 0));
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool ok = c0 + (j * 64 + lane) * 4 < cols;
+    v[j].x = ok ? v[j].x : 0.0f;
+    v[j].y = ok ? v[j].y : 0.0f;
+    v[j].z = ok ? v[j].z : 0.0f;
+    v[j].w = ok ? v[j].w : 0.0f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j].x = gelu2_as(v[j].x);
+    v[j].y = gelu2_as(v[j].y);
+    v[j].z = gelu2_as(v[j].z);
+    v[j].w = gelu2_as(v[j].w);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) s_max[wave] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  const float scale = act_scale_from_absmax(0.5f * amax);
+  const float inv = 0.5f * (1.0f / scale);
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = c0 + (j * 64 + lane) * 4;
+    if (c < cols) *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
+  }
+  for (int c = cols + threadIdx.x; c < ldq; c += 256) qr[c] = 0;
+  if (threadIdx.x == 0) scales[row] = scale;
+}
+
 // ---- Per-tensor quantisation with a device-resident absmax.
 __global__ __launch_bounds__(256) void quant_tensor_kernel(
     const float* __restrict__ x, int ldx, int rows, int cols,
@@ -449,7 +509,8 @@ hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols, i
   } else if (cols <= 5120) {
     hipLaunchKernelGGL((gelu_quant_rows_kernel<20, false>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   } else {
-    hipLaunchKernelGGL((gelu_quant_rows_kernel<40, false>), g, b, 0, s, x, ldx, rows, cols, q, ldq, scales);
+    // One block (four waves) per row, up to 2560 columns per wave.
+    hipLaunchKernelGGL((gelu_quant_rows_split_kernel<10>), dim3(rows), b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   }
   return hipGetLastError();
 }

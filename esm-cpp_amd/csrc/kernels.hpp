@@ -140,11 +140,14 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 // Split-fp16 MFMA path, head_dim 64: q/k/v as split-fp16 words (row stride
 // ld words; q already multiplied by q_prescale), three MFMAs per product
 // (fp32-level accuracy on the fp16 matrix cores). Same work list as the
-// MFMA path; softmax logits are (q.k) / q_prescale.
+// MFMA path; softmax logits are (q.k) / q_prescale. max_len: the batch's
+// longest sequence; past kAttnLongSeq tokens the long-sequence variant runs
+// (same results, bit for bit).
+constexpr int kAttnLongSeq = 256;
 hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v,
                                int ld, float q_prescale, const int* cu_seqlens,
                                const AttnWork* work, int num_work, float* out,
-                               int ld_out, hipStream_t s);
+                               int ld_out, int max_len, hipStream_t s);
 // fp32 [rows, cols] (row stride ld_x) -> split-fp16 words of x * scale.
 hipError_t launch_pack_split(const float* x, int ld_x, int rows, int cols, float scale,
                              uint32_t* out, int ld_out, hipStream_t s);

@@ -136,6 +136,27 @@ def test_x3_unscaled_q_stress(dev, oracle):
     _x3_vs_oracle(dev, oracle, [200, 90, 64], H=8, seed=12, scale_q=False, tol=1e-4)
 
 
+def test_x3_long_sequence_variant_is_bit_identical(dev):
+    """Batches whose longest sequence passes 256 tokens run the split-fp16
+    kernel's long-sequence variant (another V^T swizzle, rescales skipped
+    when no running maximum moved): the same bits as the other variant, so
+    sequences give identical rows packed beside a long one or on their own."""
+    H = 20
+    r = rng(77)
+    short = [200, 77, 129, 1]
+    lengths = short + [300]
+    cu = cu_from_lengths(lengths)
+    T = int(cu[-1])
+    q, k, v = _qkv(r, T, H, 64)
+    packed = dev.empty((T, H * 64), np.float32)
+    dev.attention_varlen(dev.array(q), dev.array(k), dev.array(v), cu, H, 64, packed, eg.ATTN_F16X3_MFMA)
+    Ts = int(cu[len(short)])
+    alone = dev.empty((Ts, H * 64), np.float32)
+    dev.attention_varlen(dev.array(q[:Ts]), dev.array(k[:Ts]), dev.array(v[:Ts]), cu_from_lengths(short), H, 64,
+                         alone, eg.ATTN_F16X3_MFMA)
+    assert np.array_equal(packed.numpy()[:Ts].view(np.uint32), alone.numpy().view(np.uint32))
+
+
 def test_fp32_mfma_input_equivalence(dev, oracle):
     """The fp32-input MFMA entry (device bf16/fp16 cast) matches the bf16 entry."""
     r = rng(12)

@@ -187,7 +187,8 @@ def test_quantize_act(dev, oracle, mode, M, K, ldq):
     assert np.array_equal(ds.numpy(), s)
 
 
-@pytest.mark.parametrize("M,K,ldq", [(333, 5120, 5120), (65, 1280, 1296), (40, 4000, 4000), (9, 10240, 10240)])
+@pytest.mark.parametrize("M,K,ldq", [(333, 5120, 5120), (65, 1280, 1296), (40, 4000, 4000), (9, 10240, 10240),
+                                     (17, 7000, 7008)])
 def test_gelu_quantize_act(dev, oracle, M, K, ldq):
     """Fused GELU + per-token quantisation against GeluRef then the oracle's
     per-row quantisation. The device erf is Abramowitz & Stegun 7.1.26
