@@ -391,6 +391,9 @@ struct Tile {
   static constexpr int kBlocks = (BM + BN) / 8;  // 1 KB blocks per stage
   static constexpr int kPer = kBlocks / kWaves;
   static constexpr int kStage = kBlocks * 1024;  // 64 KB (BM 256) / 72 KB (BM 320)
+  // Stage buffers: three for the short tiles (40 / 48 KB each), so the loads
+  // run two stages ahead of the MFMAs; the tall tiles' two fill the LDS.
+  static constexpr int kNStage = BLK_M <= 2 ? 3 : 2;
   // RoPE cos / sin rows of a tile staged in LDS, transposed: [32 dims][BM
   // rows + pad], so that a lane reads four consecutive rows of one dim at once.
   static constexpr int kRopeTPitch = BM + 4;
@@ -652,8 +655,9 @@ template <int BLK_M, int BLK_N, int EPI>
 __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_kernel(const GemmI8Args p) {
   using TL = Tile<BLK_M, BLK_N>;
   constexpr int BM = TL::BM, kPer = TL::kPer, kStage = TL::kStage, kRopeTPitch = TL::kRopeTPitch;
+  constexpr int kNStage = TL::kNStage;
   constexpr int kThreads = TL::kThreads, WAVES_N = TL::WAVES_N;
-  __shared__ __attribute__((aligned(1024))) int8_t smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kNStage * kStage];
   __shared__ float s_as[BM], s_ws[BN], s_bs[BN];
   __shared__ int s_pos[BM];
   constexpr bool kRope = EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit;
@@ -759,14 +763,21 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   };
   i32x4 fa0[BLK_M], fb0[BLK_N], fa1[BLK_M], fb1[BLK_N];
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  if (nk > 1) {
+  // Stages 1 .. kNStage - 1 go to the free buffers.
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + BK, goff[i], ldst + kStage + i * 1024);
+  for (int st = 1; st < kNStage; ++st) {
+    if (st < nk) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + st * BK, goff[i], ldst + st * kStage + i * 1024);
+    }
   }
   read_frags(smem, 0, fa0, fb0);
   static_assert(kSub == 4, "the sub-step rotation below assumes four 32-byte sub-steps per stage");
+  // Buffer of stage kt (kt mod kNStage), kept as a wave-uniform counter.
+  int bcur = 0;
   for (int kt = 0; kt < nk; ++kt) {
-    const int8_t* cur = smem + (kt & 1) * kStage;
+    const int8_t* cur = smem + bcur * kStage;
+    const int bnext = bcur + 1 == kNStage ? 0 : bcur + 1;
     read_frags(cur, 1, fa1, fb1);
     mfmas(fa0, fb0);
     interleave();
@@ -778,20 +789,27 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
     interleave();
     // Stage kt + 1 has landed (own loads, then the barrier for everyone
     // else's) and every wave has finished reading stage kt, whose buffer
-    // then receives stage kt + 2. The body has no other branch: the last
-    // iteration reads sub-step 0 of the other, stale buffer into fa0 / fb0
-    // and never uses it (a branch around those reads would split the
-    // last sub-step's MFMAs over two blocks, and the accumulators' copies at
-    // the join spill).
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + 2 < nk) {
-      const uint32_t dst = ldst + (kt & 1) * kStage;
+    // then receives stage kt + kNStage. With three buffers stage kt + 2's
+    // loads, issued one iteration earlier, may still be in flight: vector
+    // memory operations complete in order, so waiting until at most those
+    // kPer remain means stage kt + 1's have landed. The body has no other
+    // branch: the last iteration reads sub-step 0 of a stale buffer into
+    // fa0 / fb0 and never uses it (a branch around those reads would split
+    // the last sub-step's MFMAs over two blocks, and the accumulators'
+    // copies at the join spill).
+    if (kNStage == 3 && kt + 2 < nk)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kPer) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + kNStage < nk) {
+      const uint32_t dst = ldst + bcur * kStage;
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + 2) * BK, goff[i], dst + i * 1024);
+      for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i) + (kt + kNStage) * BK, goff[i], dst + i * 1024);
     }
-    read_frags(smem + ((kt + 1) & 1) * kStage, 0, fa0, fb0);
+    read_frags(smem + bnext * kStage, 0, fa0, fb0);
     mfmas(fa1, fb1);
     interleave();
+    bcur = bnext;
   }
 
   const float* s_cosT = nullptr;
@@ -801,7 +819,7 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
       // The tile holds Q or K columns: stage its rows' RoPE cos / sin,
       // transposed, in the now idle operand buffers. Item u copies half a
       // table row (cos for even u, sin for odd u) of tile row u / 2.
-      static_assert(2 * 32 * kRopeTPitch * 4 <= 2 * kStage, "RoPE staging fits in the operand buffers");
+      static_assert(2 * 32 * kRopeTPitch * 4 <= kNStage * kStage, "RoPE staging fits in the operand buffers");
       float* cosT = reinterpret_cast<float*>(smem);
       float* sinT = cosT + 32 * kRopeTPitch;
       __syncthreads();
