@@ -70,11 +70,14 @@ def corr(a, b):
 
 
 def measure(dev, model, batch, cfg, steps, warmup, parts):
-    """(ms per step with `parts` groups, per-site kernel times with one group)."""
+    """(ms per step with `parts` groups (0: the library's automatic count),
+    per-step ms with per-kernel events and one group, per-site kernel times,
+    groups the throughput pass used)."""
     T = batch.total_tokens
     logits = dev.empty((T, cfg.vocab_size), np.float32)
     model.set_parts(parts)
     model.upload_batch(batch.ids, batch.cu)
+    used = model.staged_parts()
     for _ in range(warmup):
         model.forward_device(logits)
     dev.sync()
@@ -82,7 +85,7 @@ def measure(dev, model, batch, cfg, steps, warmup, parts):
     for _ in range(steps):
         model.forward_device(logits)
     ms = dev.timer_stop() / steps
-    if parts != 1:
+    if used != 1:
         model.set_parts(1)
         model.upload_batch(batch.ids, batch.cu)
         model.forward_device(logits)
@@ -102,7 +105,7 @@ def measure(dev, model, batch, cfg, steps, warmup, parts):
     logits.free()
     if not np.all(np.isfinite(out)):
         raise SystemExit("bench: non-finite logits")
-    return ms, ms_events, sites
+    return ms, ms_events, sites, used
 
 
 def roofline_of(sites, T, cfg, batch, workload):
@@ -164,13 +167,13 @@ def roofline_of(sites, T, cfg, batch, workload):
 def extra_workload(dev, name, cfg, weights, batch, args):
     model = eg.Model(dev, weights, int8=True, act_mode=eg.ACT_PER_TOKEN)
     try:
-        ms, _, sites = measure(dev, model, batch, cfg, args.extra_steps, 2, args.parts)
+        ms, _, sites, used = measure(dev, model, batch, cfg, args.extra_steps, 2, args.parts)
     finally:
         model.free()
     T = batch.total_tokens
     return {"workload": name, "tokens": T, "residues": batch.residues, "sequences": int(len(batch.lengths)),
             "ms_per_step": round(ms, 3), "value": round(batch.residues / (ms * 1e-3), 1), "unit": "residues/s",
-            "tokens_per_s": round(T / (ms * 1e-3), 1), "kernel_sites": sites,
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "streams": used, "kernel_sites": sites,
             "roofline": roofline_of(sites, T, cfg, batch, name.split(":")[0])}
 
 
@@ -325,8 +328,9 @@ def main():
     ap.add_argument("--cpu-warmup", type=int, default=2)
     ap.add_argument("--cpu-iters", type=int, default=5)
     ap.add_argument("--cpu-threads", type=int, default=16)
-    ap.add_argument("--parts", type=int, default=2,
-                    help="concurrent sequence groups (streams) in the throughput pass")
+    ap.add_argument("--parts", type=int, default=0,
+                    help="concurrent sequence groups (streams) in the throughput pass; 0 = the library's "
+                         "automatic count (one group per 6e11 int8 ops of a layer's linears, 1..3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the packed forward "
@@ -344,7 +348,7 @@ def main():
     mode = eg.ACT_PER_TOKEN if args.act_mode == "token" else eg.ACT_PER_TENSOR
     model = eg.Model(dev, weights, int8=True, act_mode=mode)
     T = batch.total_tokens
-    ms_plain, ms_events, sites = measure(dev, model, batch, cfg, args.steps, args.warmup, args.parts)
+    ms_plain, ms_events, sites, used = measure(dev, model, batch, cfg, args.steps, args.warmup, args.parts)
     model.free()
     log(f"ms/step {ms_plain:.3f} (with per-kernel events {ms_events:.3f}); sites {sites}")
     roofline = roofline_of(sites, T, cfg, batch, args.workload)
@@ -388,7 +392,7 @@ def main():
                    "tokens": T, "residues": batch.residues, "sequences": int(len(batch.lengths)),
                    "act_quant": "per-token" if mode == eg.ACT_PER_TOKEN else "per-tensor",
                    "attention": "split-fp16 (hi+lo, 3 MFMAs per product) fp32-accurate MFMA", "parallelism": "single GPU",
-                   "streams": args.parts},
+                   "streams": used},
         "tokens_per_s": round(T / (ms_plain * 1e-3), 1),
         "ms_per_step_with_kernel_events": round(ms_events, 3),
         "kernel_sites": sites,

@@ -31,6 +31,8 @@ constexpr int kHeadDimMfma = 64;
 // Power of two applied to Q before its split-fp16 split: keeps the lo parts
 // of the pre-scaled (|q| ~ 0.1) values out of the fp16 subnormal range.
 constexpr float kQPrescale = 8.0f;
+// Most sequence groups the automatic group count uses.
+constexpr int kAutoMaxParts = 3;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int pad16(int k) { return (k + 15) & ~15; }
@@ -914,9 +916,10 @@ struct esm_gfx950_model {
   // ESM_GFX950_NUMERICS_X86_AMX: the same with LinearAmx's row split.
   int numerics = ESM_GFX950_NUMERICS_DEFAULT;
   // A staged batch is split into `parts` contiguous sequence groups; each
-  // part has its own arena, metadata and (with more than one part) its own
-  // HIP stream, so the parts' kernels can occupy different CUs at the same
-  // time. Part p's tokens are rows [t0, t0 + T) of the packed batch.
+  // part has its own arena and metadata. Part 0 runs on the context stream,
+  // every other part on a HIP stream of its own, so the parts' kernels can
+  // occupy different CUs at the same time. Part p's tokens are rows
+  // [t0, t0 + T) of the packed batch.
   struct Part {
     void* arena = nullptr;  // grown when the part exceeds every earlier batch
     size_t arena_bytes = 0;
@@ -932,6 +935,9 @@ struct esm_gfx950_model {
     int maxL = 0;                    // longest sequence of the staged part
   };
   std::vector<Part> parts = std::vector<Part>(1);
+  // Automatic group count (esm_gfx950_model_set_parts(0), the default): each
+  // staged batch takes as many of the parts as its size warrants.
+  bool auto_parts = true;
   int staged_T = 0;  // tokens of the staged batch (all parts)
   // esm_gfx950_forward_scheduled: device and pinned host logits, two of each
   // so one group's copy-out overlaps the next group's forward.
@@ -1138,7 +1144,11 @@ extern "C" int esm_gfx950_model_create(esm_gfx950_ctx* ctx, const esm_gfx950_mod
   step(upload_f(ctx, m, desc->lm_ln_w, d, &m->lm_ln_w));
   step(upload_f(ctx, m, desc->lm_ln_b, d, &m->lm_ln_b));
   step(upload_f(ctx, m, desc->lm_decoder_bias, V, &m->dec_bias));
-  if (rc == ESM_GFX950_OK) step(init_part(ctx, m->parts[0], false));
+  if (rc == ESM_GFX950_OK) {
+    // The automatic group count (the default) can use up to kAutoMaxParts.
+    m->parts.assign(kAutoMaxParts, esm_gfx950_model::Part());
+    for (int i = 0; i < kAutoMaxParts; ++i) step(init_part(ctx, m->parts[i], i > 0));
+  }
   if (rc != ESM_GFX950_OK) {
     hipStreamSynchronize(ctx->stream);
     free_model(m);
@@ -2020,9 +2030,20 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
 
 }  // namespace
 
+extern "C" int esm_gfx950_model_staged_parts(const esm_gfx950_model* m, int* parts) {
+  if (!m || !parts) return ESM_GFX950_INVALID_ARGUMENT;
+  int n = 0;
+  for (const auto& P : m->parts) n += P.T > 0 ? 1 : 0;
+  *parts = n;
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* m, int parts) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
-  ESM_REQUIRE(ctx, parts >= 1 && parts <= 4, "model_set_parts: parts must be 1..4");
+  ESM_REQUIRE(ctx, parts >= 0 && parts <= 4, "model_set_parts: parts must be 0 (automatic) or 1..4");
+  const bool automatic = parts == 0;
+  if (automatic) parts = kAutoMaxParts;
+  m->auto_parts = automatic;
   if (static_cast<int>(m->parts.size()) == parts) return ESM_GFX950_OK;
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   for (auto& p : m->parts) {
@@ -2030,12 +2051,25 @@ extern "C" int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model*
     free_part(p);
   }
   m->parts.assign(parts, esm_gfx950_model::Part());
-  for (int i = 0; i < parts; ++i) ESM_TRY(init_part(ctx, m->parts[i], parts > 1));
+  for (int i = 0; i < parts; ++i) ESM_TRY(init_part(ctx, m->parts[i], i > 0));
   m->staged_T = 0;
   return ESM_GFX950_OK;
 }
 
 namespace {
+
+// Sequence groups for a batch of T tokens under the automatic count: one per
+// 6e11 int8 operations of a layer's four linears (24 T d^2), at least one and
+// at most kAutoMaxParts. Measured one-box forwards (ms, 1 / 2 / 3 groups):
+// 650M uniform 8 x 256 (T = 2,048) 5.15 / 5.51 / 5.68; 650M config-4 varlen
+// (T = 31,107) 41.7 / 40.9 / 41.6; 3B config 5 (T = 20,321) 92.9 / 90.2 /
+// 89.4. Fewer tokens per group shrink every GEMM's grid; more groups let one
+// group's GEMMs run beside another's attention and row kernels.
+int auto_part_count(const esm_gfx950_model_config& c, int T) {
+  const double work = 24.0 * static_cast<double>(T) * c.hidden_size * c.hidden_size;
+  const int n = static_cast<int>(work / 6e11);
+  return std::max(1, std::min(n, kAutoMaxParts));
+}
 
 // Validates and stages a packed batch in at most max_parts sequence groups.
 int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, const int32_t* cu, int B, int T,
@@ -2054,7 +2088,8 @@ int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, co
   // the batch in one part.
   const bool whole = m->cfg.weights_int8 && (m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR ||
                                             m->numerics != ESM_GFX950_NUMERICS_DEFAULT);
-  const int np = whole ? 1 : std::min({static_cast<int>(m->parts.size()), B, max_parts});
+  int np = whole ? 1 : std::min({static_cast<int>(m->parts.size()), B, max_parts});
+  if (m->auto_parts) np = std::min(np, auto_part_count(m->cfg, T));
   int b0 = 0;
   for (int p = 0; p < np; ++p) {
     int b1 = b0 + 1;
@@ -2065,6 +2100,27 @@ int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, co
     b0 = b1;
   }
   m->staged_T = T;
+  return ESM_GFX950_OK;
+}
+
+// Part 0 runs on the context stream itself (no own stream); parts 1.. with
+// work wait for what is queued there so far ...
+int fork_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* m) {
+  esm_gfx950_model::Part& P0 = m->parts[0];
+  ESM_HIP(ctx, hipEventRecord(P0.done, ctx->stream));
+  for (size_t i = 1; i < m->parts.size(); ++i)
+    if (m->parts[i].T > 0) ESM_HIP(ctx, hipStreamWaitEvent(m->parts[i].stream, P0.done, 0));
+  return ESM_GFX950_OK;
+}
+
+// ... and the context stream waits for their last work.
+int join_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* m) {
+  for (size_t i = 1; i < m->parts.size(); ++i) {
+    esm_gfx950_model::Part& P = m->parts[i];
+    if (P.T == 0) continue;
+    ESM_HIP(ctx, hipEventRecord(P.done, P.stream));
+    ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
+  }
   return ESM_GFX950_OK;
 }
 
@@ -2081,27 +2137,22 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   if (m->staged_T == 0) return ESM_GFX950_OK;
   ESM_REQUIRE(ctx, logits, "forward_device: null logits");
   const int V = m->cfg.vocab_size;
-  if (m->parts.size() == 1) return forward_part(ctx, m, m->parts[0], logits);
+  if (m->parts.size() == 1 || m->parts[1].T == 0) return forward_part(ctx, m, m->parts[0], logits);
   ESM_REQUIRE(ctx,
               !(m->cfg.weights_int8 && (m->cfg.act_quant_mode == ESM_GFX950_ACT_PER_TENSOR ||
                                         m->numerics != ESM_GFX950_NUMERICS_DEFAULT)) ||
                   m->parts[1].T == 0,
               "forward_device: batch staged in several parts before the switch to per-tensor scales; upload it again");
-  // Fork: every part's stream waits for the work queued so far on the
-  // context stream, runs its forward, and the context stream joins them.
-  esm_gfx950_model::Part& P0 = m->parts[0];
-  ESM_HIP(ctx, hipEventRecord(P0.done, ctx->stream));
-  for (auto& P : m->parts)
-    if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(P.stream, P0.done, 0));
+  // Fork: part 0 runs on the context stream; every other part's stream
+  // waits for the work queued so far there, runs its forward, and the
+  // context stream joins them.
+  ESM_TRY(fork_parts(ctx, m));
   for (auto& P : m->parts) {
     if (P.T == 0) continue;
     StreamScope scope(ctx, P.stream);
     ESM_TRY(forward_part(ctx, m, P, logits + static_cast<size_t>(P.t0) * V));
-    ESM_HIP(ctx, hipEventRecord(P.done, P.stream));
   }
-  for (auto& P : m->parts)
-    if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
-  return ESM_GFX950_OK;
+  return join_parts(ctx, m);
 }
 
 extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
@@ -2114,27 +2165,22 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   // Host logits: each part writes its rows into its own arena, then one
   // device-to-host copy per part after the join.
   const int V = m->cfg.vocab_size;
-  if (m->parts.size() == 1) {
+  if (m->parts.size() == 1 || m->parts[1].T == 0) {
     const esm_gfx950_model::Part& P = m->parts[0];
     const Arena a = part_arena(m, P);
     ESM_TRY(forward_part(ctx, m, P, a.logits));
     ESM_HIP(ctx, hipMemcpyAsync(logits, a.logits, static_cast<size_t>(T) * V * 4, hipMemcpyDeviceToHost, ctx->stream));
   } else {
-    esm_gfx950_model::Part& P0 = m->parts[0];
-    ESM_HIP(ctx, hipEventRecord(P0.done, ctx->stream));
-    for (auto& P : m->parts)
-      if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(P.stream, P0.done, 0));
+    ESM_TRY(fork_parts(ctx, m));
     for (auto& P : m->parts) {
       if (P.T == 0) continue;
       StreamScope scope(ctx, P.stream);
       const Arena a = part_arena(m, P);
       ESM_TRY(forward_part(ctx, m, P, a.logits));
       ESM_HIP(ctx, hipMemcpyAsync(logits + static_cast<size_t>(P.t0) * V, a.logits, static_cast<size_t>(P.T) * V * 4,
-                                  hipMemcpyDeviceToHost, P.stream));
-      ESM_HIP(ctx, hipEventRecord(P.done, P.stream));
+                                  hipMemcpyDeviceToHost, ctx->stream));
     }
-    for (auto& P : m->parts)
-      if (P.T > 0) ESM_HIP(ctx, hipStreamWaitEvent(ctx->stream, P.done, 0));
+    ESM_TRY(join_parts(ctx, m));
   }
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;

@@ -46,7 +46,8 @@ EXPORTED = [
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
     "esm_gfx950_model_create", "esm_gfx950_model_free", "esm_gfx950_model_set_act_mode",
     "esm_gfx950_forward_packed", "esm_gfx950_batch_upload", "esm_gfx950_forward_device",
-    "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_plan_batches",
+    "esm_gfx950_model_arena_bytes", "esm_gfx950_model_set_parts", "esm_gfx950_model_staged_parts",
+    "esm_gfx950_plan_batches",
     "esm_gfx950_forward_scheduled", "esm_gfx950_model_create_from_gguf",
     "esm_gfx950_model_set_first_block_fc1_fp16", "esm_gfx950_observer_create", "esm_gfx950_observer_free",
     "esm_gfx950_observer_clear", "esm_gfx950_observer_observe", "esm_gfx950_observer_site_count",
@@ -125,6 +126,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_forward_device": (i32, [vp, vp, vp]),
         "esm_gfx950_model_arena_bytes": (i32, [vp, C.POINTER(sz)]),
         "esm_gfx950_model_set_parts": (i32, [vp, vp, i32]),
+        "esm_gfx950_model_staged_parts": (i32, [vp, C.POINTER(C.c_int)]),
         "esm_gfx950_plan_batches": (i32, [vp, i32, f32, i32, vp, vp, C.POINTER(C.c_int)]),
         "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
         "esm_gfx950_model_create_from_gguf": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(vp)]),
@@ -556,8 +558,15 @@ class Model:
         self.dev._check(self.dev.lib.esm_gfx950_model_set_lm_dense_split(self.dev.ctx, self.handle, int(enabled)))
 
     def set_parts(self, parts: int):
-        """Concurrent sequence groups per batch (esm_gfx950_model_set_parts)."""
+        """Concurrent sequence groups per batch (esm_gfx950_model_set_parts);
+        0 chooses per batch (the default)."""
         self.dev._check(self.dev.lib.esm_gfx950_model_set_parts(self.dev.ctx, self.handle, int(parts)))
+
+    def staged_parts(self) -> int:
+        """Groups the last staged batch was split into (esm_gfx950_model_staged_parts)."""
+        n = C.c_int(0)
+        self.dev._check(self.dev.lib.esm_gfx950_model_staged_parts(self.handle, C.byref(n)))
+        return int(n.value)
 
     def forward_packed(self, ids: np.ndarray, cu: np.ndarray, out: Optional[DeviceArray] = None):
         """Packed forward; returns host logits [T, vocab] or fills `out` on device."""

@@ -375,13 +375,22 @@ int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const 
  * logits fp32 [T, vocab] go to DEVICE memory. Stream-ordered, no host sync. */
 int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, float* logits);
 /* Splits every later staged batch into `parts` (1..4) contiguous groups of
- * whole sequences with about equal token counts; with parts > 1 each group
- * gets its own arena and HIP stream (default priority), and forward_device
- * forks from / joins back to the context stream, so the groups' kernels run
- * concurrently on different CUs. Results are identical to parts = 1 (every
- * row depends only on its own sequence). No reference counterpart: the
- * reference's ForwardPacked (model.cpp:1093-1255) runs one thread pool. */
+ * whole sequences with about equal token counts; each group gets its own
+ * arena, group 0 runs on the context stream and every other group on a HIP
+ * stream of its own (default priority) that forward_device forks from / joins
+ * back to the context stream, so the groups' kernels run concurrently on
+ * different CUs. parts = 0 (every new model's setting)
+ * chooses per batch: one group per 6e11 int8 operations of a layer's four
+ * linears (24 T d^2 for T tokens), between 1 and 3 -- small batches keep
+ * whole GEMM grids, large ones overlap one group's GEMMs with another's
+ * attention. Per-tensor activation scales and the x86 numerics always take
+ * one group. Results are identical for every count (every row depends only
+ * on its own sequence). No reference counterpart: the reference's
+ * ForwardPacked (model.cpp:1093-1255) runs one thread pool. */
 int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int parts);
+/* The number of groups the last staged batch was split into (0 when none is
+ * staged). No reference counterpart. */
+int esm_gfx950_model_staged_parts(const esm_gfx950_model* model, int* parts);
 /* PlanBatches (reference src/sched/scheduler.cpp:54-75, SchedulerConfig in
  * include/esm_cpp/scheduler.h:8-21), host only: splits n sequences of the
  * given lengths into caller-order chunks of at most max_batch_size (all when

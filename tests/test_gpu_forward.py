@@ -256,9 +256,12 @@ def test_parts_match_single_stream(dev, w650_small, small_batch, parts):
     on its own sequence in per-token mode, so logits are bit-identical to the
     one-stream forward, on the host-logits and the device-logits paths."""
     m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    m.set_parts(1)
     want = m.forward_packed(small_batch.ids, small_batch.cu)
+    assert m.staged_parts() == 1
     m.set_parts(parts)
     got = m.forward_packed(small_batch.ids, small_batch.cu)
+    assert m.staged_parts() == min(parts, len(small_batch.lengths))
     np.testing.assert_array_equal(got, want)
     out = dev.empty((small_batch.total_tokens, 33), np.float32)
     m.upload_batch(small_batch.ids, small_batch.cu)
@@ -272,6 +275,28 @@ def test_parts_match_single_stream(dev, w650_small, small_batch, parts):
     sub = small_batch.subset(idx)
     rows = np.concatenate([np.arange(small_batch.cu[b], small_batch.cu[b + 1]) for b in idx])
     np.testing.assert_allclose(m.forward_packed(sub.ids, sub.cu), want[rows], rtol=1e-4, atol=1e-4)
+    m.free()
+
+
+def test_parts_automatic_count(dev, w650_small, small_batch):
+    """The default (set_parts(0)) splits a batch into one group per 6e11 int8
+    operations of a layer's four linears (24 T d^2), between 1 and 3, with
+    logits identical to one group."""
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    d = w650_small.cfg.hidden_size
+    auto = m.forward_packed(small_batch.ids, small_batch.cu)
+    assert m.staged_parts() == 1  # a few hundred tokens: whole GEMM grids
+    m.set_parts(1)
+    np.testing.assert_array_equal(m.forward_packed(small_batch.ids, small_batch.cu), auto)
+    m.set_parts(0)
+    rng = np.random.default_rng(7)
+    for T, want in ((2048, 1), (int(2.1 * 6e11 / (24 * d * d)), 2), (int(5.3 * 6e11 / (24 * d * d)), 3)):
+        lengths = np.full(T // 512, 512, np.int32)
+        lengths[-1] += T - int(lengths.sum())
+        cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+        ids = rng.integers(4, 24, size=T, dtype=np.int32)
+        m.upload_batch(ids, cu)
+        assert m.staged_parts() == want, (T, m.staged_parts())
     m.free()
 
 
