@@ -35,6 +35,7 @@ def _i8(r, shape):
 @pytest.mark.parametrize("M,N,K", [
     (1, 16, 16), (37, 64, 64), (5, 9, 17), (130, 260, 48), (300, 1280, 1280), (257, 3840, 1280),
     (129, 1280, 5120), (64, 5120, 1280), (31, 2560, 10240),
+    (300, 200, 512), (513, 640, 768), (260, 384, 384), (777, 1000, 2560),
 ])
 def test_int32_bit_exact(dev, oracle, tile_rows, M, N, K):
     r = rng(1000 + M + N + K)
