@@ -471,6 +471,10 @@ extern "C" int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int 
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_set_gemm_split_k(int splits) {
+  return set_gemm_split_k(splits) ? ESM_GFX950_OK : ESM_GFX950_INVALID_ARGUMENT;
+}
+
 extern "C" int esm_gfx950_set_gemm_tile_rows(int rows) {
   return set_gemm_tile_rows(rows) ? ESM_GFX950_OK : ESM_GFX950_INVALID_ARGUMENT;
 }
@@ -1576,6 +1580,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.bias = L.out.bias;
   g.C_f32 = a.ybuf;
   g.ldc = d;
+  // The FFN intermediate is dead here (its last reader was the previous
+  // layer's GELU pass): small grids may split K into it.
+  g.splitk_ws = reinterpret_cast<int32_t*>(a.inter);
+  g.splitk_ws_elems = Tf;
   ESM_TRY(ctx->time_begin("out", &slot));
   ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
   ESM_TRY(ctx->time_end(slot));
@@ -1654,6 +1662,10 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.bias = L.fc2.bias;
   g.C_f32 = a.ybuf;
   g.ldc = d;
+  // fc2's input is already quantised from the FFN intermediate, which is
+  // therefore free to hold split-K partial sums.
+  g.splitk_ws = reinterpret_cast<int32_t*>(a.inter);
+  g.splitk_ws_elems = Tf;
   ESM_TRY(ctx->time_begin("fc2", &slot));
   ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
   ESM_TRY(ctx->time_end(slot));

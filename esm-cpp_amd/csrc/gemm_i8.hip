@@ -65,10 +65,10 @@ __device__ __forceinline__ int xcd_remap(int id, int num) {
 // (workgroup id mod 8) owns a contiguous range, then walked in groups of
 // kGroupM row tiles so consecutive tiles on one XCD share W columns and A rows
 // in that XCD's L2.
-__device__ __forceinline__ void tile_origin(int M, int N, int BM, int BN, int* m0, int* n0) {
+__device__ __forceinline__ void tile_origin_of(int id, int M, int N, int BM, int BN, int* m0, int* n0) {
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
-  const int pid = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int pid = xcd_remap(id, tiles_m * tiles_n);
   const int per_group = kGroupM * tiles_n;
   const int group = pid / per_group;
   const int first_m = group * kGroupM;
@@ -76,6 +76,10 @@ __device__ __forceinline__ void tile_origin(int M, int N, int BM, int BN, int* m
   const int in_group = pid - group * per_group;
   *m0 = (first_m + in_group % gsize) * BM;
   *n0 = (in_group / gsize) * BN;
+}
+
+__device__ __forceinline__ void tile_origin(int M, int N, int BM, int BN, int* m0, int* n0) {
+  tile_origin_of(blockIdx.x, M, N, BM, BN, m0, n0);
 }
 
 // Global -> registers for one stage of ROWS rows x C::BK bytes. Rows past
@@ -545,11 +549,13 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
 }
 
 // MAX: also reduce |out| into p.row_absmax / p.tensor_absmax (whichever is set).
+// c_i32: the int32 output (kEpiI32), p.C_i32 or, for a split-K launch, the
+// split's own plane of it.
 template <int BLK_M, int BLK_N, int EPI, bool FULL, bool MAX>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
                                            const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
-                                           int n0) {
+                                           int n0, int32_t* c_i32) {
   const int lr0 = wm * BLK_M * 32 + hi * 4;
   const int lc0 = wn * BLK_N * 32 + l32;
   const uint32_t ldc = p.ldc;
@@ -559,7 +565,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
   // per-lane byte offset.
   const int wr0 = wm * BLK_M * 32;
   if constexpr (EPI == kEpiI32) {
-    int32_t* tile = p.C_i32 + static_cast<size_t>(m0) * ldc + n0;
+    int32_t* tile = c_i32 + static_cast<size_t>(m0) * ldc + n0;
     const uint32_t lane_b = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(lc0)) * 4u;
 #pragma unroll
     for (int i = 0; i < BLK_M; ++i)
@@ -662,8 +668,25 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   __shared__ int s_pos[BM];
   constexpr bool kRope = EPI == kEpiQkvRopeF32 || EPI == kEpiQkvRope || EPI == kEpiQkvSplit;
 
-  int m0, n0;
-  tile_origin(p.M, p.N, BM, BN, &m0, &n0);
+  // Split-K (int32 output only): workgroup b takes tile b mod tiles and the
+  // (b / tiles)-th of p.splits contiguous ranges of K stages, and writes its
+  // partial sums to that split's [M, ldc] plane of C_i32.
+  int m0, n0, split = 0;
+  int32_t* c_i32 = p.C_i32;
+  if (EPI == kEpiI32 && p.splits > 1) {
+    const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+    split = blockIdx.x / tiles;
+    tile_origin_of(blockIdx.x - split * tiles, p.M, p.N, BM, BN, &m0, &n0);
+    c_i32 += static_cast<size_t>(split) * p.M * p.ldc;
+  } else {
+    tile_origin(p.M, p.N, BM, BN, &m0, &n0);
+  }
+  const int splits = EPI == kEpiI32 ? max(p.splits, 1) : 1;
+  const int nk_all = p.K / BK;
+  const int kb0 = nk_all * split / splits;
+  const int nk = nk_all * (split + 1) / splits - kb0;
+  const int8_t* const pA = p.A + kb0 * BK;
+  const int8_t* const pW = p.W + kb0 * BK;
   if constexpr (EPI != kEpiI32) {
     // Per-row activation scales and per-column weight scales / bias of the
     // tile, read once here instead of per element in the epilogue.
@@ -702,9 +725,8 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
     const int row = is_a ? min(m0 + b * 8 + r, p.M - 1) : min(n0 + (b - BM / 8) * 8 + r, p.N - 1);
     goff[i] = static_cast<uint32_t>(row) * static_cast<uint32_t>(is_a ? p.lda : p.ldw) + c * 16;
   }
-  auto gbase = [&](int i) { return wave * kPer + i < BM / 8 ? p.A : p.W; };
+  auto gbase = [&](int i) { return wave * kPer + i < BM / 8 ? pA : pW; };
   const uint32_t ldst = lds_addr(smem) + static_cast<uint32_t>(wave * kPer * 1024);
-  const int nk = p.K / BK;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i), goff[i], ldst + i * 1024);
 
@@ -847,15 +869,55 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
-      epilogue32<BLK_M, BLK_N, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
+          c_i32);
     else
-      epilogue32<BLK_M, BLK_N, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
+          c_i32);
   } else {
     if (full)
-      epilogue32<BLK_M, BLK_N, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
+          c_i32);
     else
-      epilogue32<BLK_M, BLK_N, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0);
+      epilogue32<BLK_M, BLK_N, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
+          c_i32);
   }
+}
+
+// Split-K dequant: C[m, n] = fma(float(sum over the S planes of P[m, n]),
+// a_scale[m] * w_scale[n], bias[n]), the kEpiF32 epilogue's expression on the
+// exact int32 sum. Four columns per thread (N and ldc multiples of 4).
+__global__ __launch_bounds__(256) void splitk_dequant_kernel(const int32_t* __restrict__ P, int S, int M, int N,
+                                                             const float* __restrict__ a_scale,
+                                                             const float* __restrict__ w_scale,
+                                                             const float* __restrict__ bias, float* __restrict__ C,
+                                                             int ldc) {
+  const int n4 = N / 4;
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<size_t>(M) * n4) return;
+  const int m = static_cast<int>(i / n4), c = static_cast<int>(i % n4) * 4;
+  const size_t plane = static_cast<size_t>(M) * N;
+  const int32_t* src = P + static_cast<size_t>(m) * N + c;
+  int4 acc = *reinterpret_cast<const int4*>(src);
+  for (int k = 1; k < S; ++k) {
+    const int4 v = *reinterpret_cast<const int4*>(src + k * plane);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  const float as = a_scale[m];
+  const float4 ws = *reinterpret_cast<const float4*>(w_scale + c);
+  const float4 b = bias ? *reinterpret_cast<const float4*>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 out;
+  out.x = __builtin_fmaf(static_cast<float>(acc.x), as * ws.x, b.x);
+  out.y = __builtin_fmaf(static_cast<float>(acc.y), as * ws.y, b.y);
+  out.z = __builtin_fmaf(static_cast<float>(acc.z), as * ws.z, b.z);
+  out.w = __builtin_fmaf(static_cast<float>(acc.w), as * ws.w, b.w);
+  __builtin_nontemporal_store(out.x, C + static_cast<size_t>(m) * ldc + c);
+  __builtin_nontemporal_store(out.y, C + static_cast<size_t>(m) * ldc + c + 1);
+  __builtin_nontemporal_store(out.z, C + static_cast<size_t>(m) * ldc + c + 2);
+  __builtin_nontemporal_store(out.w, C + static_cast<size_t>(m) * ldc + c + 3);
 }
 
 }  // namespace v3
@@ -884,7 +946,7 @@ hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
   using namespace v3;
   constexpr int BM = Tile<BLK_M, BLK_N>::BM;
   const int tiles = ((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
-  const dim3 grid(tiles), block(Tile<BLK_M, BLK_N>::kThreads);
+  const dim3 grid(tiles * (epi == kEpiI32 ? std::max(p.splits, 1) : 1)), block(Tile<BLK_M, BLK_N>::kThreads);
   switch (epi) {
     case kEpiI32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiI32>), grid, block, 0, s, p); break;
     case kEpiF32: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32>), grid, block, 0, s, p); break;
@@ -966,13 +1028,86 @@ int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus) {
 
 namespace {
 
-hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
-  switch (gemm_i8_tile_rows(p.M, p.N, p.K, epi, p.cus)) {
+std::atomic<int> g_split_k{0};
+
+// Estimated time, in units of one 256-row tile's K stage (about 2 us here),
+// of a grid of `tiles` workgroups on `cus` CUs running `stages` K stages each
+// at tile height rows (64, 128 or 256), as in gemm_i8_tile_rows.
+double grid_units(long tiles, int stages, int rows, int cus) {
+  const double per = rows == 64 ? 0.45 : rows == 128 ? 0.62 : 1.0;
+  const long rounds = (tiles + cus - 1) / cus;
+  return static_cast<double>(rounds) * (stages + 3.0) * per;
+}
+
+}  // namespace
+
+int gemm_i8_split_k(int M, int N, int K, int cus, int* rows) {
+  const int all = device_cus();
+  if (cus <= 0) cus = all;
+  *rows = gemm_i8_tile_rows(M, N, K, kEpiF32, cus);
+  const int forced = g_split_k.load(std::memory_order_relaxed);
+  if (forced == 1 || N % 4 != 0) return 1;
+  const int nk = K / v3::BK;
+  if (forced >= 2) return nk >= forced ? forced : 1;
+  if (*rows == 320 || tiles_of(M, N, *rows) >= cus) return 1;
+  // The dequant pass reads S int32 planes and writes the fp32 result: at
+  // about 4 TB/s plus a launch, in the same units.
+  constexpr double kUnitUs = 2.05;
+  auto pass_units = [&](int S) {
+    const double bytes = (S + 1.0) * static_cast<double>(M) * N * 4.0;
+    return (bytes / 4.0e6 + 4.0) / kUnitUs;
+  };
+  double best = grid_units(tiles_of(M, N, *rows), nk, *rows, cus);
+  int best_s = 1, best_rows = *rows;
+  static constexpr int kRows[3] = {64, 128, 256};
+  for (int r : kRows)
+    for (int S = 2; S <= 4 && nk / S >= 4; ++S) {
+      const double t = grid_units(tiles_of(M, N, r) * S, (nk + S - 1) / S, r, cus) + pass_units(S);
+      if (t < best * 0.9) {
+        best = t;
+        best_s = S;
+        best_rows = r;
+      }
+    }
+  *rows = best_rows;
+  return best_s;
+}
+
+bool set_gemm_split_k(int splits) {
+  if (splits < 0 || splits > 4) return false;
+  g_split_k.store(splits, std::memory_order_relaxed);
+  return true;
+}
+
+namespace {
+
+hipError_t launch_v3_rows(const GemmI8Args& p, int epi, int rows, hipStream_t s) {
+  switch (rows) {
     case 64: return launch_v3_tile<1>(p, epi, s);
     case 128: return launch_v3_tile<2>(p, epi, s);
     case 320: return launch_v3_tile<5>(p, epi, s);
     default: return launch_v3_tile<4>(p, epi, s);
   }
+}
+
+hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
+  if (epi == kEpiF32 && p.splitk_ws && !p.row_absmax && !p.tensor_absmax && p.ldc % 4 == 0) {
+    int rows = 0;
+    const int S = gemm_i8_split_k(p.M, p.N, p.K, p.cus, &rows);
+    if (S > 1 && static_cast<size_t>(S) * p.M * p.N <= p.splitk_ws_elems) {
+      GemmI8Args q = p;
+      q.C_i32 = p.splitk_ws;
+      q.ldc = p.N;
+      q.splits = S;
+      const hipError_t e = launch_v3_rows(q, kEpiI32, rows, s);
+      if (e != hipSuccess) return e;
+      const size_t quads = static_cast<size_t>(p.M) * (p.N / 4);
+      hipLaunchKernelGGL(v3::splitk_dequant_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
+                         s, p.splitk_ws, S, p.M, p.N, p.a_scale, p.w_scale, p.bias, p.C_f32, p.ldc);
+      return hipGetLastError();
+    }
+  }
+  return launch_v3_rows(p, epi, gemm_i8_tile_rows(p.M, p.N, p.K, epi, p.cus), s);
 }
 
 }  // namespace

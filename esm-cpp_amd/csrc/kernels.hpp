@@ -54,6 +54,15 @@ struct GemmI8Args {
   float q_scale = 1.0f;
   float q_prescale = 1.0f;  // kEpiQkvSplit: power of two applied to Q before the split
   int cus = 0;              // CUs the launch can expect to have to itself (0: the device's)
+  // Split-K, int32 output (kEpiI32): the grid holds splits x tiles
+  // workgroups, and C_i32 holds `splits` consecutive [M, ldc] planes of
+  // partial sums over contiguous ranges of K.
+  int splits = 1;
+  // kEpiF32 launches: int32 workspace of splitk_ws_elems elements that a grid
+  // too small for the device may split K into (partial planes, then one
+  // dequant pass); null: never split.
+  int32_t* splitk_ws = nullptr;
+  size_t splitk_ws_elems = 0;
 };
 
 // Picks the pipelined 256- or 320-row-tile kernel when gemm_i8_pipelined_ok(p) (K a
@@ -76,6 +85,14 @@ int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus);
 // Compute units of the current device (queried once per device; 256 if the
 // query fails).
 int device_cus();
+// K splits of a kEpiF32 launch with a workspace (1: none): grids that leave
+// CUs idle split K when the estimated time of the split grid plus its dequant
+// pass beats the unsplit one's. *rows receives the tile height to use.
+int gemm_i8_split_k(int M, int N, int K, int cus, int* rows);
+// Process-wide override of gemm_i8_split_k for later launches: 0 automatic,
+// 1 never, 2..4 that many splits wherever a launch qualifies (workspace large
+// enough, kEpiF32 without absmax outputs). False for other values.
+bool set_gemm_split_k(int splits);
 
 // ---------------------------------------------------------------- FP32 GEMM
 enum GemmF32Epilogue : int {

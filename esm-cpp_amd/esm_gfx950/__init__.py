@@ -40,7 +40,7 @@ EXPORTED = [
     "esm_gfx950_memcpy_d2h", "esm_gfx950_memcpy_d2d", "esm_gfx950_timer_start", "esm_gfx950_timer_stop",
     "esm_gfx950_kernel_timing", "esm_gfx950_kernel_timing_query", "esm_gfx950_weight_upload_i8",
     "esm_gfx950_weight_free", "esm_gfx950_gemm_i8_i32", "esm_gfx950_linear_i8_q", "esm_gfx950_quantize_act",
-    "esm_gfx950_gelu_quantize_act", "esm_gfx950_set_gemm_tile_rows", "esm_gfx950_model_set_lm_dense_split",
+    "esm_gfx950_gelu_quantize_act", "esm_gfx950_set_gemm_tile_rows", "esm_gfx950_set_gemm_split_k", "esm_gfx950_model_set_lm_dense_split",
     "esm_gfx950_linear_i8", "esm_gfx950_linear_f32", "esm_gfx950_layernorm", "esm_gfx950_gelu",
     "esm_gfx950_residual_add", "esm_gfx950_scale", "esm_gfx950_rope_build_tables",
     "esm_gfx950_rope_apply_varlen", "esm_gfx950_attention_varlen", "esm_gfx950_attention_varlen_bf16",
@@ -98,6 +98,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
         "esm_gfx950_gelu_quantize_act": (i32, [vp, vp, i32, i32, vp, i32, vp]),
         "esm_gfx950_set_gemm_tile_rows": (i32, [i32]),
+        "esm_gfx950_set_gemm_split_k": (i32, [i32]),
         "esm_gfx950_model_set_lm_dense_split": (i32, [vp, vp, i32]),
         "esm_gfx950_linear_i8": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
         "esm_gfx950_linear_i8_noalloc": (i32, [vp, vp, vp, vp, vp, i32, i32, i32, i32]),
@@ -153,10 +154,18 @@ def _ptr(a: np.ndarray) -> C.c_void_p:
 
 
 def set_gemm_tile_rows(rows: int):
-    """INT8 GEMM tile height for later launches: 256, 320 or 0 (automatic)."""
+    """INT8 GEMM tile height for later launches: 64, 128, 256, 320 or 0 (automatic)."""
     rc = load_library().esm_gfx950_set_gemm_tile_rows(int(rows))
     if rc != OK:
         raise Gfx950Error(rc, f"set_gemm_tile_rows({rows})")
+
+
+def set_gemm_split_k(splits: int):
+    """K splits of the model's out-proj / fc2 GEMMs for later launches: 0
+    automatic, 1 never, 2..4 forced."""
+    rc = load_library().esm_gfx950_set_gemm_split_k(int(splits))
+    if rc != OK:
+        raise Gfx950Error(rc, f"set_gemm_split_k({splits})")
 
 
 def rope_build_tables(seq_len: int, head_dim: int):

@@ -155,6 +155,17 @@ int esm_gfx950_gemm_i8_i32(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const 
  * and tests. No reference counterpart. INVALID_ARGUMENT for other values. */
 int esm_gfx950_set_gemm_tile_rows(int rows);
 
+/* K splits of the model's out-proj and fc2 INT8 GEMMs for every later launch
+ * in the process: 0 (default) chooses per launch, 1 never splits, 2..4 split
+ * that many ways. A split grid writes int32 partial sums over contiguous K
+ * ranges into the (then unused) FFN intermediate buffer and one pass sums
+ * them and applies the dequant epilogue. The automatic choice splits only
+ * grids that leave CUs idle (small batches), when the estimated time of the
+ * split grid plus that pass is lower. int32 sums are exact, so results are
+ * bit-identical for every setting; it exists for tuning and tests. No
+ * reference counterpart. INVALID_ARGUMENT for other values. */
+int esm_gfx950_set_gemm_split_k(int splits);
+
 /* Quantised-activation linear: out = fma(float(acc), a_scale[m] * w_scale[n], bias[n]),
  * optionally followed by GELU (gelu != 0). The dequant expression of
  * FinalizeStore16 (gemm_int8.cpp:109-126) with a per-row activation scale.

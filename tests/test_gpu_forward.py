@@ -121,6 +121,32 @@ def test_gemm_tile_rows_do_not_change_logits(dev, w650_small, small_batch, per_t
         assert np.array_equal(outs[0], o)
 
 
+@pytest.mark.parametrize("per_token", [False, True])
+def test_gemm_split_k_does_not_change_logits(dev, w650_small, small_batch, per_token):
+    """Split-K out-proj / fc2 (int32 partial sums over K ranges, summed and
+    dequantised in one pass) gives bit-identical logits for every split
+    count: the int32 sums are exact and the dequant expression is the same.
+    The automatic choice splits this small batch's grids."""
+    mode = eg.ACT_PER_TOKEN if per_token else eg.ACT_PER_TENSOR
+    m = eg.Model(dev, w650_small, int8=True, act_mode=mode)
+    outs = []
+    try:
+        for splits in (1, 2, 3, 4, 0):
+            eg.set_gemm_split_k(splits)
+            outs.append(m.forward_packed(small_batch.ids, small_batch.cu))
+    finally:
+        eg.set_gemm_split_k(0)
+        m.free()
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
+
+
+def test_gemm_split_k_rejects_other_counts():
+    for bad in (-1, 5):
+        with pytest.raises(eg.Gfx950Error):
+            eg.set_gemm_split_k(bad)
+
+
 def test_packed_equals_serial(dev, w650_small, small_batch):
     """Per-token mode keeps every row independent, so packing changes nothing."""
     m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
