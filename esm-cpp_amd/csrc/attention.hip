@@ -262,30 +262,31 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 // select, then the words are unpacked into hi/lo planes with v_perm.
 constexpr int KCX = 64;                 // keys per LDS chunk
 constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
-// V^T hi / lo planes: one 160-byte row per dim, keys in 4-key (8-byte) quads
-// stored at quad ^ (dim / 4). The staging writes (4 bytes per lane, four dims
-// apart) and the PV fragment reads (8 bytes per lane, 16 dims by 4 quads) then
-// touch distinct LDS banks; a plain 144-byte pitch put 16 writing lanes on 4
-// banks.
+// V hi / lo planes, row-major like K: one 160-byte row per key. The PV
+// product needs, per lane, four consecutive keys of one dim; gfx950's
+// transposing LDS read (ds_read_b64_tr_b16) delivers exactly that from
+// row-major rows: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8-byte rows read by lanes i / 4, i / 4 + 4, i / 4 + 8 and
+// i / 4 + 12 (layout checked on the device). With lane s of a group reading
+// key s / 4 of a 4-key quad at dims 4 (s % 4) .. + 4, lane i gets dim i of
+// keys 0..3. The 160-byte pitch keeps those reads on distinct banks (the
+// staging writes meet 2-way conflicts, and there are four times fewer).
 constexpr int kVPitchX = 160;
-static_assert(KCX == 64, "the V^T swizzle covers 16 key quads");
-// PAIRED: the long-sequence variant's swizzle, quad ^ ((dim / 4) & 11). It
-// leaves bit 2 of the quad index alone, so quads q and q + 4 (q < 4 mod 8:
-// the two key blocks a lane reads for one PV fragment) stay 32 bytes apart
-// and load as one ds_read2_b64 straight into the fragment's registers (no
-// register moves to assemble it); the staging writes meet 2-way bank
-// conflicts instead.
-template <bool PAIRED = false>
-__device__ __forceinline__ int vt_off(int dim, int key) {
-  constexpr int mask = PAIRED ? 11 : 15;
-  return dim * kVPitchX + ((((key >> 2) ^ ((dim >> 2) & mask)) & 15) << 3) + ((key & 3) << 1);
-}
+static_assert(KCX == 64, "the PV loop takes 32-key pairs of 16-key blocks");
 
 // Low (sel_lo) or high (sel_hi) 16-bit halves of two words, packed: the hi
 // or lo fp16 parts of two consecutive values.
 constexpr uint32_t kSelLo = 0x05040100u, kSelHi = 0x07060302u;
 __device__ __forceinline__ uint32_t halves(uint32_t first, uint32_t second, uint32_t sel) {
   return __builtin_amdgcn_perm(second, first, sel);
+}
+
+// ds_read_b64_tr_b16 of the 8 bytes at LDS address p (8-byte aligned).
+__device__ __forceinline__ f16x4 lds_read_tr16(const uint8_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((__attribute__((address_space(3))) uint8_t*)p));
+  return __builtin_bit_cast(f16x4, v);
 }
 
 __device__ __forceinline__ f32x4 mma16(f16x8 a, f16x8 b, f32x4 c) {
@@ -324,13 +325,11 @@ __device__ __forceinline__ void split8(const float (&p)[8], f16x8* hi, f16x8* lo
 }
 
 // LONG: the variant for batches with sequences past 256 tokens, whose many
-// key chunks per work item make the chunk loop's VALU work count: the
-// PAIRED V^T swizzle (no register moves per PV fragment), and O and the
-// running sum rescaled only when some lane's running maximum moved (else
-// alpha = exp2(0) = 1 exactly, so skipping it changes no bit). Measured on
-// configuration 5 (3B, sequences up to 963 tokens): 418 vs 428 us per layer.
-// Short-sequence batches keep the other variant: there the leaner kernel ran
-// as fast in isolation, but beside the second sequence group's kernels the
+// key chunks per work item make the chunk loop's VALU work count: O and the
+// running sum are rescaled only when some lane's running maximum moved (else
+// alpha = exp2(0) = 1 exactly, so skipping it changes no bit). Short-sequence
+// batches keep the unconditional rescale: there the leaner loop ran as fast
+// in isolation, but beside the second sequence group's kernels the
 // configuration-4 forward got 1% slower.
 template <bool LONG>
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
@@ -339,8 +338,8 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
   __shared__ __attribute__((aligned(16))) uint8_t sKh[KCX * kKPitchX];
   __shared__ __attribute__((aligned(16))) uint8_t sKl[KCX * kKPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sVh[64 * kVPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sVl[64 * kVPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sVh[KCX * kVPitchX];
+  __shared__ __attribute__((aligned(16))) uint8_t sVl[KCX * kVPitchX];
 
   const AttnWork w = work[blockIdx.x];
   const int start = cu[w.seq];
@@ -358,9 +357,9 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   // pairs x 16 dim quads), clamped to the sequence's last key; the chunk
   // after the current one is loaded while the current one is computed.
   // Addresses: a uniform chunk base plus 32-bit lane byte offsets.
-  constexpr int kKLoads = KCX * 16 / 256, kVLoads = KCX / 2 * 16 / 256;
+  constexpr int kKLoads = KCX * 16 / 256, kVLoads = KCX * 16 / 256;
   const uint32_t ldb = static_cast<uint32_t>(ld) * 4u;  // row pitch in bytes
-  uint4 kr[kKLoads], va[kVLoads], vb[kVLoads];
+  uint4 kr[kKLoads], vr[kVLoads];
   auto load_chunk = [&](int kc) {
     const int nk = min(KCX, L - kc);
     const char* kbase = reinterpret_cast<const char*>(k + static_cast<size_t>(start + kc) * ld + hoff);
@@ -374,9 +373,8 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
 #pragma unroll
     for (int i = 0; i < kVLoads; ++i) {
       const int idx = tid + 256 * i;
-      const int dq = idx & 15, key0 = 2 * (idx >> 4);
-      va[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key0, nk - 1)) * ldb + dq * 16);
-      vb[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key0 + 1, nk - 1)) * ldb + dq * 16);
+      const int key = idx >> 4, c4 = idx & 15;
+      vr[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key, nk - 1)) * ldb + c4 * 16);
     }
   };
 
@@ -426,20 +424,16 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
       *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) =
           make_uint2(halves(x.x, x.y, kSelHi), halves(x.z, x.w, kSelHi));
     }
-    // V^T[dim][key]: each item is a key pair x 4 dims.
+    // V rows, staged like K.
 #pragma unroll
     for (int i = 0; i < kVLoads; ++i) {
       const int idx = tid + 256 * i;
-      const int dq = idx & 15, key0 = 2 * (idx >> 4);
-      const uint4 a = (FULLC || key0 < nkeys) ? va[i] : make_uint4(0u, 0u, 0u, 0u);
-      const uint4 b = (FULLC || key0 + 1 < nkeys) ? vb[i] : make_uint4(0u, 0u, 0u, 0u);
-      const uint32_t xa[4] = {a.x, a.y, a.z, a.w}, xb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int off = vt_off<LONG>(dq * 4 + j, key0);
-        *reinterpret_cast<uint32_t*>(sVh + off) = halves(xa[j], xb[j], kSelLo);
-        *reinterpret_cast<uint32_t*>(sVl + off) = halves(xa[j], xb[j], kSelHi);
-      }
+      const int key = idx >> 4, c4 = idx & 15;
+      const uint4 x = (FULLC || key < nkeys) ? vr[i] : make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint2*>(sVh + key * kVPitchX + c4 * 8) =
+          make_uint2(halves(x.x, x.y, kSelLo), halves(x.z, x.w, kSelLo));
+      *reinterpret_cast<uint2*>(sVl + key * kVPitchX + c4 * 8) =
+          make_uint2(halves(x.x, x.y, kSelHi), halves(x.z, x.w, kSelHi));
     }
     if (kc0 + KCX < L) load_chunk(kc0 + KCX);  // in flight during this chunk's compute
     __syncthreads();
@@ -529,13 +523,14 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          const int dim = db * 16 + lr;
-          const int ca = vt_off<LONG>(dim, (2 * kp) * 16 + lg * 4);
-          const int cb = LONG ? ca + 32 : vt_off<LONG>(dim, (2 * kp + 1) * 16 + lg * 4);
-          const f16x4 vah = *reinterpret_cast<const f16x4*>(sVh + ca);
-          const f16x4 vbh = *reinterpret_cast<const f16x4*>(sVh + cb);
-          const f16x4 val = *reinterpret_cast<const f16x4*>(sVl + ca);
-          const f16x4 vbl = *reinterpret_cast<const f16x4*>(sVl + cb);
+          // Transposing reads: lane (lr, lg) gets dim db*16 + lr of keys
+          // (2kp)*16 + lg*4 .. +4 (ca) and (2kp+1)*16 + lg*4 .. +4 (cb).
+          const int ca = ((2 * kp) * 16 + lg * 4 + (lr >> 2)) * kVPitchX + (db * 16 + 4 * (lr & 3)) * 2;
+          const int cb = ca + 16 * kVPitchX;
+          const f16x4 vah = lds_read_tr16(sVh + ca);
+          const f16x4 vbh = lds_read_tr16(sVh + cb);
+          const f16x4 val = lds_read_tr16(sVl + ca);
+          const f16x4 vbl = lds_read_tr16(sVl + cb);
           const f16x8 vfh = f16x8{vah[0], vah[1], vah[2], vah[3], vbh[0], vbh[1], vbh[2], vbh[3]};
           const f16x8 vfl = f16x8{val[0], val[1], val[2], val[3], vbl[0], vbl[1], vbl[2], vbl[3]};
 #pragma unroll
