@@ -247,32 +247,50 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 
 // ---- Split-fp16 MFMA path (head_dim 64): fp32 accuracy on fp16 MFMA.
 //
-// Every operand arrives as split-fp16 words (low half fp16(x), high half
-// fp16(x - fp16(x)): 22 significant bits together), written by the QKV
-// GEMM epilogue after RoPE (or by launch_pack_split for the op-level entry),
-// and each product uses three MFMAs: hi*hi + lo*hi + hi*lo (the dropped
-// lo*lo term is below 2^-22 relative). Q comes multiplied by a power of two
-// (q_prescale) so the lo parts of the small pre-scaled Q stay normal fp16;
-// the factor is divided back out in the exp2 argument. Layout and wave roles
-// are those of the single-fp16 kernel above: S^T = K Q^T puts each lane's
+// Every operand is split into hi + lo fp16 parts (hi = fp16(x), lo =
+// fp16(x - hi): 22 significant bits together), written by the QKV GEMM
+// epilogue after RoPE (or by launch_pack_x3 for the op-level entry), and each
+// product uses three MFMAs: hi*hi + lo*hi + hi*lo (the dropped lo*lo term is
+// below 2^-22 relative). Q comes multiplied by a power of two (q_prescale) so
+// the lo parts of the small pre-scaled Q stay normal fp16; the factor is
+// divided back out in the exp2 argument. Q arrives as split words (low half
+// hi, high half lo), K and V as separate hi and lo fp16 planes. Within each
+// head the 64 positions hold dims in the order 0, 32, 1, 33, ..., 31, 63 (the
+// epilogue's rotary pairs side by side); the dot products run over positions,
+// and O is written back in natural dim order. S^T = K Q^T puts each lane's
 // probabilities in the B-operand layout of O^T = V^T P^T. The running sum
 // uses the fp32 probabilities, so the normalisation is that of the
-// reference's fp32/double softmax (attention.cpp:118-139). Staging is
-// branch-free: rows past the sequence are loaded clamped and zeroed by
-// select, then the words are unpacked into hi/lo planes with v_perm.
-constexpr int KCX = 64;                 // keys per LDS chunk
-constexpr int kKPitchX = 64 * 2 + 16;   // bytes per key row of K hi / lo
-// V hi / lo planes, row-major like K: one 160-byte row per key. The PV
-// product needs, per lane, four consecutive keys of one dim; gfx950's
-// transposing LDS read (ds_read_b64_tr_b16) delivers exactly that from
-// row-major rows: within each group of 16 lanes, lane i receives element
-// i % 4 of the 8-byte rows read by lanes i / 4, i / 4 + 4, i / 4 + 8 and
-// i / 4 + 12 (layout checked on the device). With lane s of a group reading
-// key s / 4 of a 4-key quad at dims 4 (s % 4) .. + 4, lane i gets dim i of
-// keys 0..3. The 160-byte pitch keeps those reads on distinct banks (the
-// staging writes meet 2-way conflicts, and there are four times fewer).
-constexpr int kVPitchX = 160;
+// reference's fp32/double softmax (attention.cpp:118-139).
+//
+// K and V chunks go straight from global memory into LDS
+// (global_load_lds_dwordx4, no registers): each of the four waves loads one
+// plane (K hi, K lo, V hi, V lo) of the next 64-key chunk while the current
+// one is computed, into the other of two 32 KB buffers. Plane rows are 128
+// bytes, their 16-byte chunks stored at chunk ^ swizzle(row): (row / 2) % 8
+// for K, whose fragment reads take one chunk of 16 consecutive rows, and
+// 2 ((row / 2) % 4) for V, whose transposing reads (below) take two chunks of
+// 8 consecutive rows; both read patterns then touch distinct LDS banks.
+constexpr int KCX = 64;  // keys per LDS chunk
 static_assert(KCX == 64, "the PV loop takes 32-key pairs of 16-key blocks");
+constexpr int kPlaneBytes = KCX * 128;     // one plane of a chunk
+constexpr int kChunkBytes = 4 * kPlaneBytes;
+
+__device__ __forceinline__ int swz_k(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int swz_v(int row) { return 2 * ((row >> 1) & 3); }
+
+// One 16-byte-per-lane global -> LDS load: a wave-uniform global base plus a
+// 32-bit lane offset, into the wave-uniform LDS byte address lds (M0).
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t off, uint32_t lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0v)
+               : "memory", "m0");
+#endif
+}
+
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
 
 // Low (sel_lo) or high (sel_hi) 16-bit halves of two words, packed: the hi
 // or lo fp16 parts of two consecutive values.
@@ -282,6 +300,11 @@ __device__ __forceinline__ uint32_t halves(uint32_t first, uint32_t second, uint
 }
 
 // ds_read_b64_tr_b16 of the 8 bytes at LDS address p (8-byte aligned).
+// Within each group of 16 lanes, lane i receives element i % 4 of the 8-byte
+// rows read by lanes i / 4, i / 4 + 4, i / 4 + 8 and i / 4 + 12 (layout
+// checked on the device). So when lane s of a group reads key s / 4 of a
+// 4-key quad at positions 4 (s % 4) .. + 4 of a row-major V tile, lane i gets
+// position i of the quad's four keys: the PV operand, read from rows.
 __device__ __forceinline__ f16x4 lds_read_tr16(const uint8_t* p) {
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -333,13 +356,12 @@ __device__ __forceinline__ void split8(const float (&p)[8], f16x8* hi, f16x8* lo
 // configuration-4 forward got 1% slower.
 template <bool LONG>
 __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
-    const uint32_t* __restrict__ q, const uint32_t* __restrict__ k,
-    const uint32_t* __restrict__ v, int ld, float s2, const int* __restrict__ cu,
+    const uint32_t* __restrict__ q, int ldq, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
+    const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int ldp, float s2, const int* __restrict__ cu,
     const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
-  __shared__ __attribute__((aligned(16))) uint8_t sKh[KCX * kKPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sKl[KCX * kKPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sVh[KCX * kVPitchX];
-  __shared__ __attribute__((aligned(16))) uint8_t sVl[KCX * kVPitchX];
+  // Two chunk buffers, each [K hi | K lo | V hi | V lo] planes of 64 rows x
+  // 128 bytes.
+  __shared__ __attribute__((aligned(1024))) uint8_t sbuf[2 * kChunkBytes];
 
   const AttnWork w = work[blockIdx.x];
   const int start = cu[w.seq];
@@ -353,47 +375,43 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   const int qbase = w.q0 + wave * 32;
   const bool active = qbase < L;  // wave-uniform
 
-  // K / V chunk loads into registers (K: KCX keys x 16 uint4; V: KCX/2 key
-  // pairs x 16 dim quads), clamped to the sequence's last key; the chunk
-  // after the current one is loaded while the current one is computed.
-  // Addresses: a uniform chunk base plus 32-bit lane byte offsets.
-  constexpr int kKLoads = KCX * 16 / 256, kVLoads = KCX * 16 / 256;
-  const uint32_t ldb = static_cast<uint32_t>(ld) * 4u;  // row pitch in bytes
-  uint4 kr[kKLoads], vr[kVLoads];
-  auto load_chunk = [&](int kc) {
+  // Chunk loads: wave p moves plane p (K hi, K lo, V hi, V lo) as eight 1 KB
+  // blocks of 8 rows; lane j of block rg fills row 8 rg + j / 8 at slot j % 8
+  // with that row's chunk slot ^ swizzle(row). Rows past the sequence repeat
+  // its last key (their scores are masked to -inf, so their probabilities are
+  // exactly 0).
+  const uint16_t* const plane = wave == 0 ? kh : wave == 1 ? kl : wave == 2 ? vh : vl;
+  const uint32_t ldpb = static_cast<uint32_t>(ldp) * 2u;  // plane row pitch in bytes
+  const int drow = lane >> 3, dslot = lane & 7;
+  const uint32_t lds0 = lds_byte_addr(sbuf) + static_cast<uint32_t>(wave * kPlaneBytes);
+  auto load_chunk = [&](int kc, int buf) {
     const int nk = min(KCX, L - kc);
-    const char* kbase = reinterpret_cast<const char*>(k + static_cast<size_t>(start + kc) * ld + hoff);
-    const char* vbase = reinterpret_cast<const char*>(v + static_cast<size_t>(start + kc) * ld + hoff);
+    const char* base = reinterpret_cast<const char*>(plane + static_cast<size_t>(start + kc) * ldp + hoff);
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c4 = idx & 15;
-      kr[i] = *reinterpret_cast<const uint4*>(kbase + static_cast<uint32_t>(min(key, nk - 1)) * ldb + c4 * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < kVLoads; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c4 = idx & 15;
-      vr[i] = *reinterpret_cast<const uint4*>(vbase + static_cast<uint32_t>(min(key, nk - 1)) * ldb + c4 * 16);
+    for (int rg = 0; rg < 8; ++rg) {
+      const int row = rg * 8 + drow;
+      const int c = dslot ^ (wave < 2 ? swz_k(row) : swz_v(row));
+      lds_dma16(base, static_cast<uint32_t>(min(row, nk - 1)) * ldpb + static_cast<uint32_t>(c * 16),
+                lds0 + static_cast<uint32_t>(buf * kChunkBytes + rg * 1024));
     }
   };
 
   // Q fragments (B operand of S^T = K Q^T): lane (lr, lg) holds query lr of
-  // block qb, dims [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8). The Q words are
-  // loaded first and chunk 0's K / V right behind them, so both round trips
+  // block qb, positions [lg*8, lg*8+8) and [32+lg*8, 32+lg*8+8). The Q words
+  // are loaded first and chunk 0 right behind them, so both round trips
   // overlap.
   uint4 qw[2][2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qi = min(qbase + qb * 16 + lr, L - 1);
-    const uint32_t* qp = q + static_cast<size_t>(start + qi) * ld + hoff;
+    const uint32_t* qp = q + static_cast<size_t>(start + qi) * ldq + hoff;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       qw[qb][half][0] = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8);
       qw[qb][half][1] = *reinterpret_cast<const uint4*>(qp + half * 32 + lg * 8 + 4);
     }
   }
-  load_chunk(0);
+  load_chunk(0, 0);
   f16x8 qh[2][2], ql[2][2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
@@ -408,47 +426,42 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   float mrun[2] = {-INFINITY, -INFINITY};
   float lrun[2] = {0.f, 0.f};
 
-  // One chunk of keys; FULLC: all KCX keys are valid (every chunk but the
-  // last of a sequence whose length is not a multiple of KCX), so no key
-  // needs masking.
-  auto chunk = [&](int kc0, int nkeys, auto fullc_tag) {
+  // Fragment offsets inside a plane. K: row kb*16 + lr, chunks lg and 4 + lg
+  // (kb*16 leaves the swizzle unchanged). V (transposing reads): row
+  // (2kp)*16 + lg*4 + lr/4 (+16 for the pair's second block, same swizzle),
+  // positions db*16 + 4 (lr % 4): chunk 2 db + (lr % 4) / 2, half lr % 2.
+  const int koff0 = lr * 128 + ((lg ^ swz_k(lr)) << 4);
+  const int koff1 = lr * 128 + (((4 + lg) ^ swz_k(lr)) << 4);
+  const int vrow = lg * 4 + (lr >> 2);
+  const int vsw = swz_v(vrow);
+  const int vbase = vrow * 128 + ((lr & 1) << 3);
+  const int vc = (lr & 3) >> 1;
+
+  // One chunk of keys from buffer buf; FULLC: all KCX keys are valid (every
+  // chunk but the last of a sequence whose length is not a multiple of KCX),
+  // so no key needs masking.
+  auto chunk = [&](int kc0, int nkeys, int buf, auto fullc_tag) {
     constexpr bool FULLC = decltype(fullc_tag)::value;
-    __syncthreads();  // the previous chunk's LDS reads are done
-#pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c4 = idx & 15;
-      const uint4 x = (FULLC || key < nkeys) ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint2*>(sKh + key * kKPitchX + c4 * 8) =
-          make_uint2(halves(x.x, x.y, kSelLo), halves(x.z, x.w, kSelLo));
-      *reinterpret_cast<uint2*>(sKl + key * kKPitchX + c4 * 8) =
-          make_uint2(halves(x.x, x.y, kSelHi), halves(x.z, x.w, kSelHi));
-    }
-    // V rows, staged like K.
-#pragma unroll
-    for (int i = 0; i < kVLoads; ++i) {
-      const int idx = tid + 256 * i;
-      const int key = idx >> 4, c4 = idx & 15;
-      const uint4 x = (FULLC || key < nkeys) ? vr[i] : make_uint4(0u, 0u, 0u, 0u);
-      *reinterpret_cast<uint2*>(sVh + key * kVPitchX + c4 * 8) =
-          make_uint2(halves(x.x, x.y, kSelLo), halves(x.z, x.w, kSelLo));
-      *reinterpret_cast<uint2*>(sVl + key * kVPitchX + c4 * 8) =
-          make_uint2(halves(x.x, x.y, kSelHi), halves(x.z, x.w, kSelHi));
-    }
-    if (kc0 + KCX < L) load_chunk(kc0 + KCX);  // in flight during this chunk's compute
-    __syncthreads();
+    // This wave's loads of the chunk have landed; the barrier publishes
+    // everyone's and retires the previous chunk's reads of the other buffer,
+    // which then receives the next chunk, in flight during this one.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kc0 + KCX < L) load_chunk(kc0 + KCX, buf ^ 1);
     if (!active) return;
+    const uint8_t* sKh = sbuf + buf * kChunkBytes;
+    const uint8_t* sKl = sKh + kPlaneBytes;
+    const uint8_t* sVh = sKh + 2 * kPlaneBytes;
+    const uint8_t* sVl = sKh + 3 * kPlaneBytes;
 
     const int nkb = FULLC ? KCX / 16 : (nkeys + 15) >> 4;
     f32x4 s[KCX / 16][2];
 #pragma unroll
     for (int kb = 0; kb < KCX / 16; ++kb) {
       if (kb < nkb) {
-        const int off = (kb * 16 + lr) * kKPitchX + lg * 16;
-        const f16x8 kh0 = *reinterpret_cast<const f16x8*>(sKh + off);
-        const f16x8 kh1 = *reinterpret_cast<const f16x8*>(sKh + off + 64);
-        const f16x8 kl0 = *reinterpret_cast<const f16x8*>(sKl + off);
-        const f16x8 kl1 = *reinterpret_cast<const f16x8*>(sKl + off + 64);
+        const f16x8 kh0 = *reinterpret_cast<const f16x8*>(sKh + kb * 2048 + koff0);
+        const f16x8 kh1 = *reinterpret_cast<const f16x8*>(sKh + kb * 2048 + koff1);
+        const f16x8 kl0 = *reinterpret_cast<const f16x8*>(sKl + kb * 2048 + koff0);
+        const f16x8 kl1 = *reinterpret_cast<const f16x8*>(sKl + kb * 2048 + koff1);
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
           f32x4 acc = mma16(kh0, qh[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -523,10 +536,10 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
         }
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-          // Transposing reads: lane (lr, lg) gets dim db*16 + lr of keys
-          // (2kp)*16 + lg*4 .. +4 (ca) and (2kp+1)*16 + lg*4 .. +4 (cb).
-          const int ca = ((2 * kp) * 16 + lg * 4 + (lr >> 2)) * kVPitchX + (db * 16 + 4 * (lr & 3)) * 2;
-          const int cb = ca + 16 * kVPitchX;
+          // Lane (lr, lg) gets position db*16 + lr of keys (2kp)*16 + lg*4
+          // .. +4 (ca) and (2kp+1)*16 + lg*4 .. +4 (cb).
+          const int ca = kp * 4096 + vbase + (((2 * db + vc) ^ vsw) << 4);
+          const int cb = ca + 2048;
           const f16x4 vah = lds_read_tr16(sVh + ca);
           const f16x4 vbh = lds_read_tr16(sVh + cb);
           const f16x4 val = lds_read_tr16(sVl + ca);
@@ -545,35 +558,65 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
   };
 
   // Whole chunks, then the sequence's partial last chunk (if any).
-  int kc0 = 0;
-  for (; kc0 + KCX <= L; kc0 += KCX) chunk(kc0, KCX, std::true_type{});
-  if (kc0 < L) chunk(kc0, L - kc0, std::false_type{});
+  int kc0 = 0, buf = 0;
+  for (; kc0 + KCX <= L; kc0 += KCX, buf ^= 1) chunk(kc0, KCX, buf, std::true_type{});
+  if (kc0 < L) {
+    chunk(kc0, L - kc0, buf, std::false_type{});
+    buf ^= 1;
+  }
 
   if (!active) return;
+  // Output: rows of o[qb][db] are positions db*16 + 4 lg .. +4, i.e. dims i,
+  // i + 32, i + 1, i + 33 for i = 8 db + 2 lg. Each wave puts its 32 x 64
+  // tile in natural order into its own 8 KB of the chunk buffer the last
+  // chunk did not use (free: every wave has passed that chunk's barrier and
+  // no load targets it), 256-byte rows with 16-byte unit u at u ^ (row % 16),
+  // then stores whole rows: 16 lanes x 16 bytes per query.
+  uint8_t* stage = sbuf + buf * kChunkBytes + wave * 8192;
+  auto soff = [](int row, int dim) { return row * 256 + (((dim >> 2) ^ (row & 15)) << 4) + ((dim & 3) << 2); };
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     float lt = lrun[qb];
     lt += __shfl_xor(lt, 16, kWave);
     lt += __shfl_xor(lt, 32, kWave);
     const float inv = 1.0f / lt;
-    const int qi = qbase + qb * 16 + lr;
-    if (qi < L) {
-      float* orow = out + static_cast<size_t>(start + qi) * ld_out + hoff + lg * 4;
+    const int row = qb * 16 + lr;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-        *reinterpret_cast<float4*>(orow + db * 16) =
-            make_float4(o[qb][db][0] * inv, o[qb][db][1] * inv, o[qb][db][2] * inv, o[qb][db][3] * inv);
+    for (int db = 0; db < 4; ++db) {
+      const int i = 8 * db + 2 * lg;
+      *reinterpret_cast<float2*>(stage + soff(row, i)) = make_float2(o[qb][db][0] * inv, o[qb][db][2] * inv);
+      *reinterpret_cast<float2*>(stage + soff(row, i + 32)) = make_float2(o[qb][db][1] * inv, o[qb][db][3] * inv);
     }
+  }
+  const int unit = lane & 15;
+#pragma unroll
+  for (int r4 = 0; r4 < 8; ++r4) {
+    const int row = r4 * 4 + (lane >> 4);
+    const float4 val = *reinterpret_cast<const float4*>(stage + soff(row, unit * 4));
+    const int qi = qbase + row;
+    if (qi < L) *reinterpret_cast<float4*>(out + static_cast<size_t>(start + qi) * ld_out + hoff + unit * 4) = val;
   }
 }
 
-__global__ void pack_split_kernel(const float* __restrict__ x, int ld_x, int rows, int cols, float scale,
-                                  uint32_t* __restrict__ out, int ld_out) {
-  const size_t total = static_cast<size_t>(rows) * cols;
+// fp32 rows -> the split-fp16 kernel's operand layout (head_dim 64, positions
+// 0, 32, 1, 33, ... within each head): planes == 0, split words (x * scale)
+// at out_w[r * ld_out + c]; planes != 0, fp16 hi parts at out_h[r * ld_out +
+// c] and lo parts d elements further.
+__global__ void pack_x3_kernel(const float* __restrict__ x, int ld_x, int rows, int d, float scale, int planes,
+                               uint32_t* __restrict__ out_w, uint16_t* __restrict__ out_h, int ld_out) {
+  const size_t total = static_cast<size_t>(rows) * d;
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-    const size_t r = i / cols, c = i % cols;
-    out[r * ld_out + c] = split_f16_word(x[r * ld_x + c] * scale);
+    const size_t r = i / d;
+    const int c = static_cast<int>(i % d);
+    const int pos = c & 63, dim = (c & ~63) + (pos >> 1) + ((pos & 1) << 5);
+    const uint32_t wv = split_f16_word(x[r * ld_x + dim] * scale);
+    if (planes) {
+      out_h[r * ld_out + c] = static_cast<uint16_t>(wv & 0xffffu);
+      out_h[r * ld_out + d + c] = static_cast<uint16_t>(wv >> 16);
+    } else {
+      out_w[r * ld_out + c] = wv;
+    }
   }
 }
 
@@ -651,28 +694,30 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
   return hipGetLastError();
 }
 
-hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v, int ld, float q_prescale,
-                               const int* cu_seqlens, const AttnWork* work, int num_work, float* out, int ld_out,
-                               int max_len, hipStream_t s) {
+hipError_t launch_attention_x3(const uint32_t* q, int ldq, const uint16_t* kh, const uint16_t* kl, const uint16_t* vh,
+                               const uint16_t* vl, int ldp, float q_prescale, const int* cu_seqlens,
+                               const AttnWork* work, int num_work, float* out, int ld_out, int max_len,
+                               hipStream_t s) {
   if (num_work <= 0) return hipSuccess;
   const float s2 = kLog2e / q_prescale;
   if (max_len > kAttnLongSeq)
-    hipLaunchKernelGGL(attn_x3_kernel<true>, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work,
-                       out, ld_out);
+    hipLaunchKernelGGL(attn_x3_kernel<true>, dim3(num_work), dim3(256), 0, s, q, ldq, kh, kl, vh, vl, ldp, s2,
+                       cu_seqlens, work, out, ld_out);
   else
-    hipLaunchKernelGGL(attn_x3_kernel<false>, dim3(num_work), dim3(256), 0, s, q, k, v, ld, s2, cu_seqlens, work,
-                       out, ld_out);
+    hipLaunchKernelGGL(attn_x3_kernel<false>, dim3(num_work), dim3(256), 0, s, q, ldq, kh, kl, vh, vl, ldp, s2,
+                       cu_seqlens, work, out, ld_out);
   return hipGetLastError();
 }
 
-hipError_t launch_pack_split(const float* x, int ld_x, int rows, int cols, float scale, uint32_t* out, int ld_out,
-                             hipStream_t s) {
-  const size_t n = static_cast<size_t>(rows) * cols;
+hipError_t launch_pack_x3(const float* x, int ld_x, int rows, int d, float scale, uint32_t* words, uint16_t* planes,
+                          int ld_out, hipStream_t s) {
+  const size_t n = static_cast<size_t>(rows) * d;
   if (n == 0) return hipSuccess;
+  if (d % 64 != 0 || (words == nullptr) == (planes == nullptr)) return hipErrorInvalidValue;
   size_t g = (n + 255) / 256;
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL(pack_split_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, ld_x, rows, cols, scale,
-                     out, ld_out);
+  hipLaunchKernelGGL(pack_x3_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, ld_x, rows, d, scale,
+                     planes ? 1 : 0, words, planes, ld_out);
   return hipGetLastError();
 }
 

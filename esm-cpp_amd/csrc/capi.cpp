@@ -740,17 +740,17 @@ extern "C" int esm_gfx950_attention_varlen(esm_gfx950_ctx* ctx, const float* q, 
                                  &nwork, true));
     char* base = static_cast<char*>(ctx->scratch);
     auto* qw = reinterpret_cast<uint32_t*>(base);
-    auto* kw = reinterpret_cast<uint32_t*>(base + wbytes);
-    auto* vw = reinterpret_cast<uint32_t*>(base + 2 * wbytes);
-    ESM_HIP(ctx, launch_pack_split(q, ld, T, ld, kQPrescale, qw, ld, ctx->stream));
-    ESM_HIP(ctx, launch_pack_split(k, ld, T, ld, 1.0f, kw, ld, ctx->stream));
-    ESM_HIP(ctx, launch_pack_split(v, ld, T, ld, 1.0f, vw, ld, ctx->stream));
+    auto* kp = reinterpret_cast<uint16_t*>(base + wbytes);      // [T, 2 ld]: hi | lo
+    auto* vp = reinterpret_cast<uint16_t*>(base + 2 * wbytes);
+    ESM_HIP(ctx, launch_pack_x3(q, ld, T, ld, kQPrescale, qw, nullptr, ld, ctx->stream));
+    ESM_HIP(ctx, launch_pack_x3(k, ld, T, ld, 1.0f, nullptr, kp, 2 * ld, ctx->stream));
+    ESM_HIP(ctx, launch_pack_x3(v, ld, T, ld, 1.0f, nullptr, vp, 2 * ld, ctx->stream));
     int max_len = 0;
     for (int b = 0; b < batch_size; ++b) max_len = std::max(max_len, cu_seqlens[b + 1] - cu_seqlens[b]);
     int slot;
     ESM_TRY(ctx->time_begin("attention", &slot));
-    ESM_HIP(ctx, launch_attention_x3(qw, kw, vw, ld, kQPrescale, d_cu, d_work, nwork, out, ld, max_len,
-                                     ctx->stream));
+    ESM_HIP(ctx, launch_attention_x3(qw, ld, kp, kp + ld, vp, vp + ld, 2 * ld, kQPrescale, d_cu, d_work, nwork, out,
+                                     ld, max_len, ctx->stream));
     ESM_TRY(ctx->time_end(slot));
     ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return ESM_GFX950_OK;
@@ -1543,9 +1543,12 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   ESM_TRY(ctx->time_begin("attention", &slot));
   if (f32qkv) {
     if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
+      // The QKV epilogue's layout: per [3 d]-word row, Q words, then K's
+      // and V's hi and lo fp16 planes (d elements each).
       const auto* w = reinterpret_cast<const uint32_t*>(a.qkv);
-      ESM_HIP(ctx, launch_attention_x3(w, w + d, w + 2 * d, 3 * d, kQPrescale, md.cu, md.work, nwork, a.attn, d,
-                                       max_len, s));
+      const auto* h16 = reinterpret_cast<const uint16_t*>(a.qkv);
+      ESM_HIP(ctx, launch_attention_x3(w, 3 * d, h16 + 2 * d, h16 + 3 * d, h16 + 4 * d, h16 + 5 * d, 6 * d, kQPrescale,
+                                       md.cu, md.work, nwork, a.attn, d, max_len, s));
     } else {
       ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
                                         d, s));

@@ -482,6 +482,14 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
   const uint32_t lane_b =
       (static_cast<uint32_t>(lr0 - wr0) * ldc + static_cast<uint32_t>(hc + l32)) * 4u;  // 4-byte outputs
   const uint32_t lane_d = static_cast<uint32_t>(lr0) * dm + static_cast<uint32_t>(n0 + hc - WHICH * p.d_model + l32);
+  // kEpiQkvSplit layout of a [M, 3 d] word row: Q words [0, d), K hi / lo
+  // fp16 planes in words [d, 2d), V's in [2d, 3d). Every head keeps 64
+  // positions per part in the order (dim 0, dim 32, dim 1, dim 33, ...): the
+  // lane's rotary pair (l32, 32 + l32) lands at positions 2 l32, 2 l32 + 1.
+  // lane_s: the lane's byte offset from the tile's first row at column 0.
+  const uint32_t head_dim0 = static_cast<uint32_t>(n0 + hc - WHICH * p.d_model);  // head's first dim
+  const uint32_t col_s = WHICH == 0 ? head_dim0 + 2u * l32 : WHICH * dm + head_dim0 / 2u + l32;
+  const uint32_t lane_s = (static_cast<uint32_t>(lr0 - wr0) * ldc + col_s) * 4u;
 #pragma unroll
   for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
@@ -527,10 +535,18 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
             x1 *= p.q_prescale;
             x2 *= p.q_prescale;
           }
-          uint32_t* tile = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc + n0;
-          uint32_t* dst = row_at(tile, ldc, wr0 + static_cast<int>(dr), lane_b);
-          __builtin_nontemporal_store(split_f16_word(x1), dst);
-          __builtin_nontemporal_store(split_f16_word(x2), dst + 32);
+          const uint32_t w1 = split_f16_word(x1), w2 = split_f16_word(x2);
+          uint32_t* row0 = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc;
+          uint32_t* dst = row_at(row0, ldc, wr0 + static_cast<int>(dr), lane_s);
+          if constexpr (WHICH == 0) {
+            // Q words, the rotary pair adjacent: one 8-byte store per lane.
+            __builtin_nontemporal_store(u32x2{w1, w2}, reinterpret_cast<u32x2*>(dst));
+          } else {
+            // K / V: the pair's fp16 hi parts in the hi plane, lo parts in
+            // the lo plane (d / 2 words further).
+            __builtin_nontemporal_store(__builtin_amdgcn_perm(w2, w1, 0x05040100u), dst);
+            __builtin_nontemporal_store(__builtin_amdgcn_perm(w2, w1, 0x07060302u), dst + dm / 2);
+          }
         } else {
           // [M, d_model] outputs; column of the head inside its Q / K / V part.
           const uint32_t o = lane_d + dr * dm;

@@ -154,20 +154,25 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
                                  const AttnWork* work, int num_work, float* out,
                                  int ld_out, float* tensor_absmax,
                                  hipStream_t s);
-// Split-fp16 MFMA path, head_dim 64: q/k/v as split-fp16 words (row stride
-// ld words; q already multiplied by q_prescale), three MFMAs per product
-// (fp32-level accuracy on the fp16 matrix cores). Same work list as the
-// MFMA path; softmax logits are (q.k) / q_prescale. max_len: the batch's
-// longest sequence; past kAttnLongSeq tokens the long-sequence variant runs
-// (same results, bit for bit).
+// Split-fp16 MFMA path, head_dim 64, three MFMAs per product (fp32-level
+// accuracy on the fp16 matrix cores). Operands in the layout the QKV
+// epilogue (kEpiQkvSplit) writes: within each 64-wide head, positions hold
+// dims 0, 32, 1, 33, ..., 31, 63; q as split-fp16 words (row stride ldq
+// words, already multiplied by q_prescale); K and V as fp16 hi planes (kh,
+// vh) and lo planes (kl, vl), row stride ldp elements, 16-byte aligned rows.
+// out is written in natural dim order. Softmax logits are (q.k) / q_prescale.
+// max_len: the batch's longest sequence; past kAttnLongSeq tokens the
+// long-sequence variant runs (same results, bit for bit).
 constexpr int kAttnLongSeq = 256;
-hipError_t launch_attention_x3(const uint32_t* q, const uint32_t* k, const uint32_t* v,
-                               int ld, float q_prescale, const int* cu_seqlens,
-                               const AttnWork* work, int num_work, float* out,
-                               int ld_out, int max_len, hipStream_t s);
-// fp32 [rows, cols] (row stride ld_x) -> split-fp16 words of x * scale.
-hipError_t launch_pack_split(const float* x, int ld_x, int rows, int cols, float scale,
-                             uint32_t* out, int ld_out, hipStream_t s);
+hipError_t launch_attention_x3(const uint32_t* q, int ldq, const uint16_t* kh, const uint16_t* kl, const uint16_t* vh,
+                               const uint16_t* vl, int ldp, float q_prescale, const int* cu_seqlens,
+                               const AttnWork* work, int num_work, float* out, int ld_out, int max_len,
+                               hipStream_t s);
+// fp32 [rows, d] (row stride ld_x, d % 64 == 0) -> that layout: split words
+// of x * scale (words != null, row stride ld_out words) or hi / lo planes
+// (planes != null: hi at [r * ld_out + c], lo d elements further).
+hipError_t launch_pack_x3(const float* x, int ld_x, int rows, int d, float scale, uint32_t* words, uint16_t* planes,
+                          int ld_out, hipStream_t s);
 // Exact fp32 path for any head_dim <= 128 (one thread per query).
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v,
                                 int ld, int head_dim, const int* cu_seqlens,
