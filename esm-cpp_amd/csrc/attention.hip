@@ -264,16 +264,19 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 //
 // K and V chunks go straight from global memory into LDS
 // (global_load_lds_dwordx4, no registers): each of the four waves loads one
-// plane (K hi, K lo, V hi, V lo) of the next 64-key chunk while the current
-// one is computed, into the other of two 32 KB buffers. Plane rows are 128
+// plane (K hi, K lo, V hi, V lo) of the next 32-key chunk while the current
+// one is computed, into the other of two 16 KB buffers. 32 KB of LDS and
+// about 125 VGPRs per workgroup let four workgroups share a CU (64-key
+// chunks: two, and 8% / 12% slower at configurations 4 / 5). Plane rows are 128
 // bytes, their 16-byte chunks stored at chunk ^ swizzle(row): (row / 2) % 8
 // for K, whose fragment reads take one chunk of 16 consecutive rows, and
 // 2 ((row / 2) % 4) for V, whose transposing reads (below) take two chunks of
 // 8 consecutive rows; both read patterns then touch distinct LDS banks.
-constexpr int KCX = 64;  // keys per LDS chunk
-static_assert(KCX == 64, "the PV loop takes 32-key pairs of 16-key blocks");
+constexpr int KCX = 32;  // keys per LDS chunk
+static_assert(KCX % 32 == 0, "the PV loop takes 32-key pairs of 16-key blocks");
 constexpr int kPlaneBytes = KCX * 128;     // one plane of a chunk
 constexpr int kChunkBytes = 4 * kPlaneBytes;
+static_assert(2 * kChunkBytes >= 4 * 8192, "each wave's 32 x 64 fp32 output tile fits in the chunk buffers");
 
 __device__ __forceinline__ int swz_k(int row) { return (row >> 1) & 7; }
 __device__ __forceinline__ int swz_v(int row) { return 2 * ((row >> 1) & 3); }
@@ -355,7 +358,7 @@ __device__ __forceinline__ void split8(const float (&p)[8], f16x8* hi, f16x8* lo
 // in isolation, but beside the second sequence group's kernels the
 // configuration-4 forward got 1% slower.
 template <bool LONG>
-__global__ __launch_bounds__(256, 2) void attn_x3_kernel(
+__global__ __launch_bounds__(256, 4) void attn_x3_kernel(
     const uint32_t* __restrict__ q, int ldq, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
     const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int ldp, float s2, const int* __restrict__ cu,
     const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
@@ -388,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     const int nk = min(KCX, L - kc);
     const char* base = reinterpret_cast<const char*>(plane + static_cast<size_t>(start + kc) * ldp + hoff);
 #pragma unroll
-    for (int rg = 0; rg < 8; ++rg) {
+    for (int rg = 0; rg < KCX / 8; ++rg) {
       const int row = rg * 8 + drow;
       const int c = dslot ^ (wave < 2 ? swz_k(row) : swz_v(row));
       lds_dma16(base, static_cast<uint32_t>(min(row, nk - 1)) * ldpb + static_cast<uint32_t>(c * 16),
@@ -565,14 +568,14 @@ __global__ __launch_bounds__(256, 2) void attn_x3_kernel(
     buf ^= 1;
   }
 
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the chunks
   if (!active) return;
   // Output: rows of o[qb][db] are positions db*16 + 4 lg .. +4, i.e. dims i,
   // i + 32, i + 1, i + 33 for i = 8 db + 2 lg. Each wave puts its 32 x 64
-  // tile in natural order into its own 8 KB of the chunk buffer the last
-  // chunk did not use (free: every wave has passed that chunk's barrier and
-  // no load targets it), 256-byte rows with 16-byte unit u at u ^ (row % 16),
+  // tile in natural order into its own 8 KB of the chunk buffers (free after
+  // the barrier above), 256-byte rows with 16-byte unit u at u ^ (row % 16),
   // then stores whole rows: 16 lanes x 16 bytes per query.
-  uint8_t* stage = sbuf + buf * kChunkBytes + wave * 8192;
+  uint8_t* stage = sbuf + wave * 8192;
   auto soff = [](int row, int dim) { return row * 256 + (((dim >> 2) ^ (row & 15)) << 4) + ((dim & 3) << 2); };
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
