@@ -1452,9 +1452,15 @@ class ObsRun {
 // (hidden += ybuf) is performed by the LayerNorm kernel that reads hidden
 // next -- this layer's ffn LN, the next layer's attn LN, or the final LN --
 // so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
-// fc2 output of the previous layer (null for the first layer).
+// fc2 output of the previous layer (null for the first layer), or, when
+// split_in->splits > 0, that output left as split-K int32 partial sums in
+// the FFN intermediate buffer (summed and dequantised by this layer's first
+// LayerNorm kernel). With split_out set (per-token mode, not the last
+// layer), this layer's fc2 may leave its output that way too: split_out
+// says whether it did.
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
-               const Meta& md, int T, int nwork, int max_len, const float* resid_in, ObsRun* ob, int cus) {
+               const Meta& md, int T, int nwork, int max_len, const float* resid_in, ObsRun* ob, int cus,
+               const SplitResid* split_in = nullptr, SplitResid* split_out = nullptr) {
   const auto& c = m->cfg;
   const int d = c.hidden_size, f = c.intermediate_size, H = c.num_heads, dh = c.head_dim;
   const int ldq_d = pad16(d), ldq_f = pad16(f);
@@ -1467,9 +1473,14 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
 
   // (residual) + attn LN + activation quant
   if (tok) {
-    ESM_TRY(ctx->time_begin(resid_in ? "ln_quant" : "ln_quant_first", &slot));
-    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
-                                        a.xs, s));
+    const bool split = split_in && split_in->splits > 0;
+    ESM_TRY(ctx->time_begin(resid_in || split ? "ln_quant" : "ln_quant_first", &slot));
+    if (split)
+      ESM_HIP(ctx, launch_layernorm_quant_split(a.hidden, *split_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq,
+                                                ldq_d, a.xs, s));
+    else
+      ESM_HIP(ctx, launch_layernorm_quant(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.xq,
+                                          ldq_d, a.xs, s));
     ESM_TRY(ctx->time_end(slot));
     if (ob) {
       // The fused kernel keeps the LN output in registers: recompute it
@@ -1670,7 +1681,18 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.splitk_ws = reinterpret_cast<int32_t*>(a.inter);
   g.splitk_ws_elems = Tf;
   ESM_TRY(ctx->time_begin("fc2", &slot));
-  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+  if (split_out) split_out->splits = 0;
+  int rows = 0;
+  const int S = split_out && tok && !ob && gemm_i8_pipelined_ok(g) ? gemm_i8_split_k(T, d, g.K, cus, true, &rows) : 1;
+  if (S > 1 && static_cast<size_t>(S) * Td <= Tf) {
+    // The next layer's first LayerNorm sums the partial planes.
+    g.C_i32 = g.splitk_ws;
+    g.ldc = d;
+    ESM_HIP(ctx, launch_gemm_i8_partials(g, S, rows, s));
+    *split_out = SplitResid{g.splitk_ws, S, a.xs, L.fc2.ws, L.fc2.bias};
+  } else {
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+  }
   ESM_TRY(ctx->time_end(slot));
   return ESM_GFX950_OK;
 }
@@ -1957,6 +1979,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   const int cus = active > 1 ? std::max(1, device_cus() / active) : 0;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
   const float* pending = nullptr;  // fc2 output awaiting its residual add
+  SplitResid pending_split;         // ... or its split-K partial sums
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const DevLayer& L = m->layers[li];
     const int round16 = (li == 0 && m->first_block_fc1_fp16) ? 1 : 0;
@@ -1966,8 +1989,12 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     } else if (x86) {
       ESM_TRY(layer_f32_x86(ctx, m, L, round16, a, md, P, ob));
     } else if (c.weights_int8) {
-      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, P.maxL, pending, ob, cus));
+      SplitResid split_out;
+      const bool last = li + 1 == m->layers.size();
+      ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, P.maxL, pending, ob, cus, &pending_split,
+                         last ? nullptr : &split_out));
       pending = a.ybuf;
+      pending_split = split_out;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));
     }

@@ -58,21 +58,51 @@ __device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int c
 // With resid != null the row is first updated in place, x += resid (the
 // residual add that precedes the next LayerNorm, reference src/model.cpp:1013
 // and :1063), and the LayerNorm runs on the sum.
-template <int NV, bool QUANT>
+// SPLIT: the residual arrives as split-K partial sums (SplitResid).
+template <int NV, bool QUANT, bool SPLIT = false>
 __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ out,
     int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
-    float* __restrict__ scales, int round16) {
+    float* scales, int round16, SplitResid split = SplitResid()) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   float* xr = x + static_cast<size_t>(row) * d;
   float4 v[NV];
   load_row_vec<NV>(xr, d, lane, v);
-  if (resid) {
+  if (SPLIT || resid) {
     float4 r[NV];
-    load_row_vec<NV>(resid + static_cast<size_t>(row) * d, d, lane, r);
+    if constexpr (SPLIT) {
+      // The residual's GEMM epilogue on its summed split-K partial sums:
+      // fma(float(acc), a_scale * w_scale, bias), the same expression and
+      // operands. The row's a_scale is read here, before `scales` (which it
+      // may be) receives this row's new scale below.
+      const float as = split.a_scale[row];
+      const size_t plane = static_cast<size_t>(rows) * d;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 4;
+        const int cc = c < d ? c : 0;
+        const int32_t* src = split.planes + static_cast<size_t>(row) * d + cc;
+        int4 acc = *reinterpret_cast<const int4*>(src);
+        for (int k = 1; k < split.splits; ++k) {
+          const int4 t = *reinterpret_cast<const int4*>(src + k * plane);
+          acc.x += t.x;
+          acc.y += t.y;
+          acc.z += t.z;
+          acc.w += t.w;
+        }
+        const float4 ws = *reinterpret_cast<const float4*>(split.w_scale + cc);
+        const float4 bs = split.bias ? *reinterpret_cast<const float4*>(split.bias + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        r[j].x = c < d ? __builtin_fmaf(static_cast<float>(acc.x), as * ws.x, bs.x) : 0.0f;
+        r[j].y = c < d ? __builtin_fmaf(static_cast<float>(acc.y), as * ws.y, bs.y) : 0.0f;
+        r[j].z = c < d ? __builtin_fmaf(static_cast<float>(acc.z), as * ws.z, bs.z) : 0.0f;
+        r[j].w = c < d ? __builtin_fmaf(static_cast<float>(acc.w), as * ws.w, bs.w) : 0.0f;
+      }
+    } else {
+      load_row_vec<NV>(resid + static_cast<size_t>(row) * d, d, lane, r);
+    }
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       v[j].x += r[j].x;
@@ -493,6 +523,22 @@ hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gam
   } else {
     hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
                        nullptr, q, ldq, scales, round16);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_layernorm_quant_split(float* x, const SplitResid& r, const float* gamma, const float* beta,
+                                        float eps, int rows, int d, int8_t* q, int ldq, float* scales,
+                                        hipStream_t s, int round16) {
+  if (rows <= 0 || d <= 0) return hipSuccess;
+  if (d % 4 != 0 || d > 2560 || r.splits < 1 || !r.planes || !r.a_scale || !r.w_scale) return hipErrorInvalidValue;
+  const dim3 g = rows_grid(rows), b(256);
+  if (d <= 1280) {
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, true, true>), g, b, 0, s, x, nullptr, gamma, beta, eps, nullptr, rows,
+                       d, nullptr, q, ldq, scales, round16, r);
+  } else {
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, true, true>), g, b, 0, s, x, nullptr, gamma, beta, eps, nullptr,
+                       rows, d, nullptr, q, ldq, scales, round16, r);
   }
   return hipGetLastError();
 }

@@ -1057,7 +1057,7 @@ double grid_units(long tiles, int stages, int rows, int cus) {
 
 }  // namespace
 
-int gemm_i8_split_k(int M, int N, int K, int cus, int* rows) {
+int gemm_i8_split_k(int M, int N, int K, int cus, bool fused, int* rows) {
   const int all = device_cus();
   if (cus <= 0) cus = all;
   *rows = gemm_i8_tile_rows(M, N, K, kEpiF32, cus);
@@ -1067,9 +1067,11 @@ int gemm_i8_split_k(int M, int N, int K, int cus, int* rows) {
   if (forced >= 2) return nk >= forced ? forced : 1;
   if (*rows == 320 || tiles_of(M, N, *rows) >= cus) return 1;
   // The dequant pass reads S int32 planes and writes the fp32 result: at
-  // about 4 TB/s plus a launch, in the same units.
+  // about 4 TB/s plus a launch, in the same units. Fused into the reader, it
+  // costs the S - 1 planes read beyond the fp32 result it replaces.
   constexpr double kUnitUs = 2.05;
   auto pass_units = [&](int S) {
+    if (fused) return (S - 1.0) * static_cast<double>(M) * N * 4.0 / 4.0e6 / kUnitUs;
     const double bytes = (S + 1.0) * static_cast<double>(M) * N * 4.0;
     return (bytes / 4.0e6 + 4.0) / kUnitUs;
   };
@@ -1109,7 +1111,7 @@ hipError_t launch_v3_rows(const GemmI8Args& p, int epi, int rows, hipStream_t s)
 hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
   if (epi == kEpiF32 && p.splitk_ws && !p.row_absmax && !p.tensor_absmax && p.ldc % 4 == 0) {
     int rows = 0;
-    const int S = gemm_i8_split_k(p.M, p.N, p.K, p.cus, &rows);
+    const int S = gemm_i8_split_k(p.M, p.N, p.K, p.cus, false, &rows);
     if (S > 1 && static_cast<size_t>(S) * p.M * p.N <= p.splitk_ws_elems) {
       GemmI8Args q = p;
       q.C_i32 = p.splitk_ws;
@@ -1148,6 +1150,14 @@ hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epi, int variant, hip
 
 hipError_t launch_gemm_i8(const GemmI8Args& p, int epi, hipStream_t s) {
   return launch_gemm_i8_variant(p, epi, gemm_i8_pipelined_ok(p) ? 2 : 1, s);
+}
+
+hipError_t launch_gemm_i8_partials(const GemmI8Args& p, int splits, int rows, hipStream_t s) {
+  if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  if (!gemm_i8_pipelined_ok(p) || splits < 1 || splits > p.K / v3::BK || !p.C_i32) return hipErrorInvalidValue;
+  GemmI8Args q = p;
+  q.splits = splits;
+  return launch_v3_rows(q, kEpiI32, rows, s);
 }
 
 bool set_gemm_tile_rows(int rows) {

@@ -88,7 +88,13 @@ int device_cus();
 // K splits of a kEpiF32 launch with a workspace (1: none): grids that leave
 // CUs idle split K when the estimated time of the split grid plus its dequant
 // pass beats the unsplit one's. *rows receives the tile height to use.
-int gemm_i8_split_k(int M, int N, int K, int cus, int* rows);
+// fused: the partial planes are summed by the kernel that reads the result
+// (launch_layernorm_quant_split) instead of a pass of their own, which then
+// costs only that kernel's extra reads.
+int gemm_i8_split_k(int M, int N, int K, int cus, bool fused, int* rows);
+// The kEpiI32 split-K grid alone: p.C_i32 receives `splits` [M, p.ldc] planes
+// of partial sums (p.ldc >= N), at tile height rows.
+hipError_t launch_gemm_i8_partials(const GemmI8Args& p, int splits, int rows, hipStream_t s);
 // Process-wide override of gemm_i8_split_k for later launches: 0 automatic,
 // 1 never, 2..4 that many splits wherever a launch qualifies (workspace large
 // enough, kEpiF32 without absmax outputs). False for other values.
@@ -196,6 +202,23 @@ hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gam
                                   const float* beta, float eps, int rows,
                                   int d, int8_t* q, int ldq, float* scales,
                                   hipStream_t s, int round16 = 0);
+// A residual left as split-K int32 partial sums: planes [splits][rows][d]
+// of a GEMM whose dequant epilogue is fma(float(sum), a_scale[row] *
+// w_scale[col], bias[col]) (bias may be null).
+struct SplitResid {
+  const int32_t* planes = nullptr;
+  int splits = 0;
+  const float* a_scale = nullptr;
+  const float* w_scale = nullptr;
+  const float* bias = nullptr;
+};
+// launch_layernorm_quant with its residual given as split-K partial sums:
+// the planes are summed and dequantised by that expression, bit for bit the
+// GEMM epilogue's value, before the add. r.a_scale may be `scales` itself
+// (each row's scale is read before it is written). d % 4 == 0, d <= 2560.
+hipError_t launch_layernorm_quant_split(float* x, const SplitResid& r, const float* gamma, const float* beta,
+                                        float eps, int rows, int d, int8_t* q, int ldq, float* scales,
+                                        hipStream_t s, int round16 = 0);
 // GELU (erf of Abramowitz & Stegun 7.1.26) fused with per-token int8
 // quantisation of fp32 rows (cols % 4 == 0, cols <= 10240).
 hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols,
