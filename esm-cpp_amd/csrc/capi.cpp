@@ -1448,14 +1448,13 @@ class ObsRun {
 // One pre-LN encoder layer on the device (reference TransformerBlock,
 // src/model.cpp:932-1066): LN -> QKV -> Q-scale -> RoPE -> attention ->
 // out-proj -> residual -> LN -> fc1 -> GELU -> fc2 -> residual.
-// The out-proj and fc2 GEMMs store their outputs to a.ybuf; each residual add
-// (hidden += ybuf) is performed by the LayerNorm kernel that reads hidden
-// next -- this layer's ffn LN, the next layer's attn LN, or the final LN --
-// so the GEMM epilogue is a plain streaming store. `resid_in` is the pending
-// fc2 output of the previous layer (null for the first layer), or, when
-// split_in->splits > 0, that output left as split-K int32 partial sums in
-// the FFN intermediate buffer (summed and dequantised by this layer's first
-// LayerNorm kernel). With split_out set (per-token mode, not the last
+// The out-proj and fc2 GEMMs add their outputs into hidden in their
+// epilogues (the residual adds, hidden + out), so the LayerNorm kernels that
+// follow read hidden alone. `resid_in`, when not null, is a pending [T, d]
+// residual for this layer's first LayerNorm to add; when split_in->splits >
+// 0, the previous layer's fc2 output is instead still split-K int32 partial
+// sums in the FFN intermediate buffer, which that LayerNorm kernel sums,
+// dequantises and adds. With split_out set (per-token mode, not the last
 // layer), this layer's fc2 may leave its output that way too: split_out
 // says whether it did.
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
@@ -1579,7 +1578,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_quant_tensor(a.attn, d, T, d, amax_attn, a.xq, ldq_d, a.xs, s));
   }
 
-  // out-proj (its residual add happens in the ffn LN below)
+  // out-proj, added into hidden (the residual add)
   g = GemmI8Args();
   g.A = a.xq;
   g.lda = ldq_d;
@@ -1592,21 +1591,21 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.a_scale = a.xs;
   g.w_scale = L.out.ws;
   g.bias = L.out.bias;
-  g.C_f32 = a.ybuf;
+  g.C_f32 = a.hidden;
   g.ldc = d;
   // The FFN intermediate is dead here (its last reader was the previous
   // layer's GELU pass): small grids may split K into it.
   g.splitk_ws = reinterpret_cast<int32_t*>(a.inter);
   g.splitk_ws_elems = Tf;
   ESM_TRY(ctx->time_begin("out", &slot));
-  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+  ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
   ESM_TRY(ctx->time_end(slot));
 
-  // residual + ffn LN + quant. The observer sees the LN output before the
-  // first-block fp16 rounding (reference src/model.cpp:1023-1033).
+  // ffn LN + quant. The observer sees the LN output before the first-block
+  // fp16 rounding (reference src/model.cpp:1023-1033).
   if (tok) {
     ESM_TRY(ctx->time_begin("ln_quant", &slot));
-    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
+    ESM_HIP(ctx, launch_layernorm_quant(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.xq, ldq_d,
                                         a.xs, s, round16));
     ESM_TRY(ctx->time_end(slot));
     if (ob) {
@@ -1615,7 +1614,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     }
   } else {
     ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
-    ESM_HIP(ctx, launch_layernorm(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
+    ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
                                   s, round16));
     if (ob && round16) {
       ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
@@ -1661,7 +1660,8 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_quant_tensor(a.inter, f, T, f, a.absmax + 3, a.xq, ldq_f, a.xs, s));
   }
 
-  // fc2 (its residual add happens in the next LN that reads hidden)
+  // fc2, added into hidden (the residual add) or left as split-K partial sums
+  // for the next layer's first LayerNorm
   g = GemmI8Args();
   g.A = a.xq;
   g.lda = ldq_f;
@@ -1674,7 +1674,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.a_scale = a.xs;
   g.w_scale = L.fc2.ws;
   g.bias = L.fc2.bias;
-  g.C_f32 = a.ybuf;
+  g.C_f32 = a.hidden;
   g.ldc = d;
   // fc2's input is already quantised from the FFN intermediate, which is
   // therefore free to hold split-K partial sums.
@@ -1691,7 +1691,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_gemm_i8_partials(g, S, rows, s));
     *split_out = SplitResid{g.splitk_ws, S, a.xs, L.fc2.ws, L.fc2.bias};
   } else {
-    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Resid, s));
   }
   ESM_TRY(ctx->time_end(slot));
   return ESM_GFX950_OK;
@@ -1978,8 +1978,10 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   for (const auto& q : m->parts) active += q.T > 0 ? 1 : 0;
   const int cus = active > 1 ? std::max(1, device_cus() / active) : 0;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
-  const float* pending = nullptr;  // fc2 output awaiting its residual add
-  SplitResid pending_split;         // ... or its split-K partial sums
+  // x86 numerics: fc2 output awaiting its residual add (in the next
+  // LayerNorm); default numerics: fc2's split-K partial sums awaiting theirs.
+  const float* pending = nullptr;
+  SplitResid pending_split;
   for (size_t li = 0; li < m->layers.size(); ++li) {
     const DevLayer& L = m->layers[li];
     const int round16 = (li == 0 && m->first_block_fc1_fp16) ? 1 : 0;
@@ -1993,7 +1995,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
       const bool last = li + 1 == m->layers.size();
       ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, P.maxL, pending, ob, cus, &pending_split,
                          last ? nullptr : &split_out));
-      pending = a.ybuf;
+      pending = nullptr;  // fc2 added its output into hidden (or left split partials)
       pending_split = split_out;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));

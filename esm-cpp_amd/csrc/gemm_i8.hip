@@ -617,6 +617,50 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
           qkv_head<BLK_M, BLK_N, EPI, FULL, 2>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
+    } else if constexpr (EPI == kEpiF32Resid) {
+      // C += result, in groups of four rows x BLK_N columns (8 values per
+      // lane): the C values of group g + kDist are loaded while group g is
+      // formed and stored, so the reads stay in flight behind the work
+      // (scheduling barriers keep the compiler from hoisting them all, which
+      // would need 160 more registers). The sum is C + v, the residual add's
+      // operands and rounding.
+      constexpr int kGroups = BLK_M * 4, kDist = BLK_M >= 5 ? 3 : 4;
+      float* tile = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+      const uint32_t lane_b = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(lc0)) * 4u;
+      float res[kDist + 1][4][BLK_N];
+      auto load_group = [&](int g, float(&r)[4][BLK_N]) {
+        const int dr0 = (g >> 2) * 32 + (g & 3) * 8;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool rok = FULL || m0 + lr0 + dr0 + u < p.M;
+          const float* src = row_at(tile, ldc, wr0 + dr0 + u, lane_b);
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j) r[u][j] = (rok && col_ok(lc0 + j * 32)) ? src[j * 32] : 0.0f;
+        }
+      };
+#pragma unroll
+      for (int g = 0; g < kDist && g < kGroups; ++g) load_group(g, res[g]);
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g) {
+        if (g + kDist < kGroups) load_group(g + kDist, res[(g + kDist) % (kDist + 1)]);
+        const int i = g >> 2, q = g & 3;
+        const int lr = lr0 + i * 32 + q * 8;
+        const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
+        const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool rok = FULL || m0 + lr + u < p.M;
+          float* dst = row_at(tile, ldc, wr0 + i * 32 + q * 8 + u, lane_b);
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j) {
+            const float v = __builtin_fmaf(static_cast<float>(acc[i][j][4 * q + u]), asv[u] * ws[j], bs[j]);
+            if (rok && col_ok(lc0 + j * 32))
+              __builtin_nontemporal_store(res[g % (kDist + 1)][u][j] + v, dst + j * 32);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
     } else {
       float tmax = 0.0f;
       const uint32_t lane_c = static_cast<uint32_t>(lr0) * ldc + static_cast<uint32_t>(lc0);
@@ -639,10 +683,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
               if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
               if (rok && col_ok(lc0 + j * 32)) {
                 const uint32_t off = lane_c + static_cast<uint32_t>(i * 32 + q * 8 + u) * ldc + j * 32;
-                if constexpr (EPI == kEpiF32Resid) {
-                  float* base = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
-                  *at(base, off) += v;
-                } else if constexpr (EPI == kEpiF32GeluQ) {
+                if constexpr (EPI == kEpiF32GeluQ) {
                   uint16_t* base = p.C_f16 + static_cast<size_t>(m0) * ldc + n0;
                   *at(base, off) = f32_to_f16_bits(v);
                 } else {
@@ -903,6 +944,8 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
 // Split-K dequant: C[m, n] = fma(float(sum over the S planes of P[m, n]),
 // a_scale[m] * w_scale[n], bias[n]), the kEpiF32 epilogue's expression on the
 // exact int32 sum. Four columns per thread (N and ldc multiples of 4).
+// ACCUM: C[m, n] += that value instead (the kEpiF32Resid epilogue's C + v).
+template <bool ACCUM>
 __global__ __launch_bounds__(256) void splitk_dequant_kernel(const int32_t* __restrict__ P, int S, int M, int N,
                                                              const float* __restrict__ a_scale,
                                                              const float* __restrict__ w_scale,
@@ -930,6 +973,13 @@ __global__ __launch_bounds__(256) void splitk_dequant_kernel(const int32_t* __re
   out.y = __builtin_fmaf(static_cast<float>(acc.y), as * ws.y, b.y);
   out.z = __builtin_fmaf(static_cast<float>(acc.z), as * ws.z, b.z);
   out.w = __builtin_fmaf(static_cast<float>(acc.w), as * ws.w, b.w);
+  if constexpr (ACCUM) {
+    const float4 r = *reinterpret_cast<const float4*>(C + static_cast<size_t>(m) * ldc + c);
+    out.x = r.x + out.x;
+    out.y = r.y + out.y;
+    out.z = r.z + out.z;
+    out.w = r.w + out.w;
+  }
   __builtin_nontemporal_store(out.x, C + static_cast<size_t>(m) * ldc + c);
   __builtin_nontemporal_store(out.y, C + static_cast<size_t>(m) * ldc + c + 1);
   __builtin_nontemporal_store(out.z, C + static_cast<size_t>(m) * ldc + c + 2);
@@ -1109,7 +1159,8 @@ hipError_t launch_v3_rows(const GemmI8Args& p, int epi, int rows, hipStream_t s)
 }
 
 hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
-  if (epi == kEpiF32 && p.splitk_ws && !p.row_absmax && !p.tensor_absmax && p.ldc % 4 == 0) {
+  const bool accum = epi == kEpiF32Resid;
+  if ((epi == kEpiF32 || accum) && p.splitk_ws && !p.row_absmax && !p.tensor_absmax && p.ldc % 4 == 0) {
     int rows = 0;
     const int S = gemm_i8_split_k(p.M, p.N, p.K, p.cus, false, &rows);
     if (S > 1 && static_cast<size_t>(S) * p.M * p.N <= p.splitk_ws_elems) {
@@ -1120,8 +1171,13 @@ hipError_t launch_v3(const GemmI8Args& p, int epi, hipStream_t s) {
       const hipError_t e = launch_v3_rows(q, kEpiI32, rows, s);
       if (e != hipSuccess) return e;
       const size_t quads = static_cast<size_t>(p.M) * (p.N / 4);
-      hipLaunchKernelGGL(v3::splitk_dequant_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256), 0,
-                         s, p.splitk_ws, S, p.M, p.N, p.a_scale, p.w_scale, p.bias, p.C_f32, p.ldc);
+      const dim3 grid(static_cast<unsigned>((quads + 255) / 256)), block(256);
+      if (accum)
+        hipLaunchKernelGGL(v3::splitk_dequant_kernel<true>, grid, block, 0, s, p.splitk_ws, S, p.M, p.N, p.a_scale,
+                           p.w_scale, p.bias, p.C_f32, p.ldc);
+      else
+        hipLaunchKernelGGL(v3::splitk_dequant_kernel<false>, grid, block, 0, s, p.splitk_ws, S, p.M, p.N, p.a_scale,
+                           p.w_scale, p.bias, p.C_f32, p.ldc);
       return hipGetLastError();
     }
   }
