@@ -942,6 +942,10 @@ struct esm_gfx950_model {
   // Automatic group count (esm_gfx950_model_set_parts(0), the default): each
   // staged batch takes as many of the parts as its size warrants.
   bool auto_parts = true;
+  // Per-token W8A8: fc1's output goes to the GELU + quant pass as 24-bit
+  // values (esm_gfx950_model_set_ffn_intermediate_bits(24), the default) or
+  // as fp32 (32).
+  bool ffn_r24 = true;
   int staged_T = 0;  // tokens of the staged batch (all parts)
   // esm_gfx950_forward_scheduled: device and pinned host logits, two of each
   // so one group's copy-out overlaps the next group's forward.
@@ -1184,6 +1188,13 @@ extern "C" int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_mod
 extern "C" int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled) {
   if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
   model->first_block_fc1_fp16 = enabled != 0;
+  return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_model_set_ffn_intermediate_bits(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int bits) {
+  if (!ctx || !model) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, bits == 24 || bits == 32, "model_set_ffn_intermediate_bits: bits must be 24 or 32");
+  model->ffn_r24 = bits == 24;
   return ESM_GFX950_OK;
 }
 
@@ -1640,7 +1651,20 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.bias = L.fc1.bias;
   g.C_f32 = a.inter;
   g.ldc = f;
-  if (tok) {
+  if (tok && m->ffn_r24 && !ob && f % 64 == 0 && f <= 10240 && gemm_i8_pipelined_ok(g)) {
+    // Dequant + bias rounded to 24 bits (a high 16-bit plane, then a low
+    // byte plane, in the FFN buffer): 3 bytes per value instead of 4 for the
+    // GEMM to write and the GELU + quant pass to read.
+    g.C_f32 = nullptr;
+    g.C_f16 = reinterpret_cast<uint16_t*>(a.inter);
+    g.C_u8 = reinterpret_cast<uint8_t*>(a.inter) + Tf * 2;
+    ESM_TRY(ctx->time_begin("fc1", &slot));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32R24, s));
+    ESM_TRY(ctx->time_end(slot));
+    ESM_TRY(ctx->time_begin("gelu_quant", &slot));
+    ESM_HIP(ctx, launch_gelu_quant_rows_r24(g.C_f16, g.C_u8, f, T, f, a.xq, ldq_f, a.xs, s));
+    ESM_TRY(ctx->time_end(slot));
+  } else if (tok) {
     // Dequant + bias only; GELU runs in the per-token quantisation pass that
     // reads these rows anyway.
     ESM_TRY(ctx->time_begin("fc1", &slot));

@@ -299,6 +299,77 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
   if (lane == 0) scales[row] = scale;
 }
 
+// The same pass over the INT8 GEMM's 24-bit fc1 output (kEpiF32R24): a
+// high plane xh of bits 31..16 and a low plane xl of bits 15..8, in which
+// stored position 2 i + j of each aligned 64-column group holds column
+// 32 j + i. WAVES waves share a row (1: four rows per block; 4: one row,
+// their maxima meeting in LDS), each wave NV * 512 stored positions, eight
+// consecutive ones per lane per step: one 16-byte high and one 8-byte low
+// load give columns 4 k .. 4 k + 3 and 32 + 4 k .. (k = position / 8 within
+// the group), whose int8 values go out as two 4-byte words. cols % 64 == 0.
+template <int NV, int WAVES>
+__global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
+    const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl, int ldx, int rows, int cols,
+    int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
+  static_assert(WAVES == 1 || WAVES == 4, "one or four waves per row");
+  __shared__ float s_max[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = WAVES == 1 ? blockIdx.x * kRowsPerBlock + wave : blockIdx.x;
+  if (WAVES == 1 && row >= rows) return;
+  const int part = WAVES == 1 ? 0 : wave;
+  const uint16_t* hr = xh + static_cast<size_t>(row) * ldx;
+  const uint8_t* lr = xl + static_cast<size_t>(row) * ldx;
+  uint4 hv[NV];
+  uint2 lv[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int p0 = (part * NV + j) * 512 + lane * 8;
+    const int pc = p0 < cols ? p0 : 0;  // in bounds; zeroed below
+    hv[j] = *reinterpret_cast<const uint4*>(hr + pc);
+    lv[j] = *reinterpret_cast<const uint2*>(lr + pc);
+  }
+  float v[NV][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const bool ok = (part * NV + j) * 512 + lane * 8 < cols;
+    const uint32_t hw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+    const uint32_t lw[2] = {lv[j].x, lv[j].y};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // bytes: 0, the low plane's byte e % 4, the high plane's 16 bits of e
+      const uint32_t sel = 0x0cu | (static_cast<uint32_t>(e & 3) << 8) | ((4u + 2u * (e & 1)) << 16) |
+                           ((5u + 2u * (e & 1)) << 24);
+      const float x = __uint_as_float(__builtin_amdgcn_perm(hw[e >> 1], lw[e >> 2], sel));
+      v[j][e] = ok ? gelu2_as(x) : 0.0f;
+      amax = fmaxf(amax, fabsf(v[j][e]));
+    }
+  }
+  amax = wave_max(amax);
+  if constexpr (WAVES > 1) {
+    if (lane == 0) s_max[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  }
+  const float scale = act_scale_from_absmax(0.5f * amax);
+  const float inv = 0.5f * (1.0f / scale);
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int p0 = (part * NV + j) * 512 + lane * 8;
+    if (p0 < cols) {
+      const int c = (p0 & ~63) + ((p0 & 63) >> 1);  // column of position p0: group start + 4 k
+      *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(make_float4(v[j][0], v[j][2], v[j][4], v[j][6]), inv);
+      *reinterpret_cast<uint32_t*>(qr + c + 32) =
+          quant_pack4(make_float4(v[j][1], v[j][3], v[j][5], v[j][7]), inv);
+    }
+  }
+  if (part == 0) {
+    for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
+    if (lane == 0) scales[row] = scale;
+  }
+}
+
 // The same pass with a row split over the block's four waves, for rows
 // wider than 5120 (ESM-2 3B's d_ff of 10240): wave w holds columns
 // [w * NV * 256, (w + 1) * NV * 256), the waves' maxima meet in LDS, and each
@@ -558,6 +629,20 @@ hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols, i
     // One block (four waves) per row, up to 2560 columns per wave.
     hipLaunchKernelGGL((gelu_quant_rows_split_kernel<10>), dim3(rows), b, 0, s, x, ldx, rows, cols, q, ldq, scales);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu_quant_rows_r24(const uint16_t* xh, const uint8_t* xl, int ldx, int rows, int cols, int8_t* q,
+                                      int ldq, float* scales, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (cols % 64 != 0 || ldx % 8 != 0 || ldq % 4 != 0 || cols > 10240) return hipErrorInvalidValue;
+  const dim3 b(256);
+  if (cols <= 5120)
+    hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<10, 1>), rows_grid(rows), b, 0, s, xh, xl, ldx, rows, cols, q, ldq,
+                       scales);
+  else
+    hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<5, 4>), dim3(rows), b, 0, s, xh, xl, ldx, rows, cols, q, ldq,
+                       scales);
   return hipGetLastError();
 }
 

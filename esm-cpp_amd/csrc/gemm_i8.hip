@@ -617,6 +617,41 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
           qkv_head<BLK_M, BLK_N, EPI, FULL, 2>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
       }
       return;
+    } else if constexpr (EPI == kEpiF32R24) {
+      // The lane's two columns (l32 and 32 + l32 of the wave's 64) round to
+      // 24 bits (+0x80, then the top three bytes) and go out as one 4-byte
+      // word of their high halves and one 2-byte word of their low bytes, at
+      // stored positions 2 l32 and 2 l32 + 1 of the group: whole 128-byte
+      // rows of the high plane per half-wave.
+      static_assert(BLK_N == 2, "the 24-bit layout pairs a lane's two 32-column blocks");
+      const int gc = wn * 64;  // the wave's column group inside the tile
+      if (!FULL && n0 + gc >= p.N) return;
+      uint16_t* htile = p.C_f16 + static_cast<size_t>(m0) * ldc + n0 + gc;
+      uint8_t* ltile = p.C_u8 + static_cast<size_t>(m0) * ldc + n0 + gc;
+      const uint32_t lane_h = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32)) * 2u;
+      const uint32_t lane_l = static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32);
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int lr = lr0 + i * 32 + q * 8;
+          const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
+          const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * q + u;
+            if (!FULL && m0 + lr + u >= p.M) continue;
+            const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
+            const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
+            const uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
+            const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
+            auto* hdst = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(htile) + static_cast<size_t>(R * ldc) * 2u + lane_h);
+            auto* ldst = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ltile) + static_cast<size_t>(R * ldc) + lane_l);
+            __builtin_nontemporal_store(__builtin_amdgcn_perm(b1, b0, 0x07060302u), hdst);
+            __builtin_nontemporal_store(static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u)), ldst);
+          }
+        }
+      return;
     } else if constexpr (EPI == kEpiF32Resid) {
       // C += result, in groups of four rows x BLK_N columns (8 values per
       // lane): the C values of group g + kDist are loaded while group g is
@@ -1024,6 +1059,10 @@ hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
       hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRopeF32>), grid, block, 0, s, p);
       break;
     case kEpiQkvSplit: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvSplit>), grid, block, 0, s, p); break;
+    case kEpiF32R24:
+      if (p.N % 64 != 0 || !p.C_f16 || !p.C_u8 || p.ldc % 2 != 0) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32R24>), grid, block, 0, s, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -1068,7 +1107,8 @@ int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus) {
   // split-word QKV epilogue spills 72 bytes there too, but runs faster at
   // 320 rows all the same (216 vs 224 us at config 4). Rounds are counted
   // over the whole device: concurrent launches fill each other's last round.
-  const bool tall_ok = epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit;
+  const bool tall_ok =
+      epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit || epi == kEpiF32R24;
   if (tiles_of(M, N, 256) >= cus)
     return tall_ok && tile_cost(M, N, 320, all) <= tile_cost(M, N, 256, all) ? 320 : 256;
   // The 256-row grid leaves CUs idle (one workgroup per CU): shorter tiles

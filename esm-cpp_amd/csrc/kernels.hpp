@@ -22,6 +22,12 @@ enum GemmEpilogue : int {
   kEpiQkvRopeF32 = 6, // fp32 [M, 3*d_model] (ldc): Q*q_scale and RoPE on Q, K
   kEpiQkvSplit = 7,   // as kEpiQkvRopeF32, then Q *= q_prescale and every value
                       // stored as a split-fp16 word (C_f32 reinterpreted)
+  kEpiF32R24 = 8,     // kEpiF32's value rounded to its top 24 bits (sign,
+                      // exponent, 15 mantissa bits; nearest, ties away):
+                      // bits 31..16 to C_f16 [M, ldc], bits 15..8 to C_u8
+                      // [M, ldc]; in each aligned group of 64 columns, stored
+                      // position 2 i + j holds column 32 j + i (i < 32, j < 2).
+                      // Pipelined kernel only; N % 64 == 0.
 };
 
 // Split-fp16 word of an fp32 value x: low half fp16(x), high half
@@ -36,6 +42,7 @@ struct GemmI8Args {
   int32_t* C_i32 = nullptr;
   float* C_f32 = nullptr;
   uint16_t* C_f16 = nullptr;
+  uint8_t* C_u8 = nullptr;  // kEpiF32R24: the low byte plane
   int ldc = 0;
   const float* a_scale = nullptr;  // [M]
   const float* w_scale = nullptr;  // [N]
@@ -224,6 +231,11 @@ hipError_t launch_layernorm_quant_split(float* x, const SplitResid& r, const flo
 hipError_t launch_gelu_quant_rows(const float* x, int ldx, int rows, int cols,
                                   int8_t* q, int ldq, float* scales,
                                   hipStream_t s);
+// The same pass over the INT8 GEMM's kEpiF32R24 output (high plane xh, low
+// plane xl, row pitch ldx elements): the 24-bit values are exact floats, so
+// this is the pass above on them; cols % 64 == 0, cols <= 10240.
+hipError_t launch_gelu_quant_rows_r24(const uint16_t* xh, const uint8_t* xl, int ldx, int rows, int cols, int8_t* q,
+                                      int ldq, float* scales, hipStream_t s);
 // Per-row (per-token) quantisation. src_kind: 0 fp32, 1 fp16, 2 bf16.
 hipError_t launch_quant_rows(const void* x, int src_kind, int ldx, int rows,
                              int cols, int8_t* q, int ldq, float* scales,

@@ -55,6 +55,7 @@ EXPORTED = [
     "esm_gfx950_attention_work_items", "esm_gfx950_layernorm_avx512", "esm_gfx950_gelu_avx512",
     "esm_gfx950_expf_glibc", "esm_gfx950_linear_f32_avx512", "esm_gfx950_rope_apply_varlen_avx512",
     "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics", "esm_gfx950_linear_i8_noalloc",
+    "esm_gfx950_model_set_ffn_intermediate_bits",
 ]
 
 
@@ -132,6 +133,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
         "esm_gfx950_model_create_from_gguf": (i32, [vp, C.c_char_p, i32, i32, C.POINTER(vp)]),
         "esm_gfx950_model_set_first_block_fc1_fp16": (i32, [vp, vp, i32]),
+        "esm_gfx950_model_set_ffn_intermediate_bits": (i32, [vp, vp, i32]),
         "esm_gfx950_observer_create": (i32, [vp, C.POINTER(vp)]),
         "esm_gfx950_observer_free": (i32, [vp, vp]),
         "esm_gfx950_observer_clear": (i32, [vp]),
@@ -553,6 +555,11 @@ class Model:
         """Round layer 0's fc1 input to fp16 (esm_gfx950_model_set_first_block_fc1_fp16)."""
         self.dev._check(self.dev.lib.esm_gfx950_model_set_first_block_fc1_fp16(self.dev.ctx, self.handle,
                                                                              int(bool(enabled))))
+
+    def set_ffn_intermediate_bits(self, bits: int):
+        """24 (default) or 32: width of the per-token W8A8 fc1 output that the
+        GELU + quantisation pass reads (esm_gfx950_model_set_ffn_intermediate_bits)."""
+        self.dev._check(self.dev.lib.esm_gfx950_model_set_ffn_intermediate_bits(self.dev.ctx, self.handle, int(bits)))
 
     def set_numerics(self, numerics: int):
         """NUMERICS_X86_AVX512: forward bit-equal to the reference's x86 AVX-512

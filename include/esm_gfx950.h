@@ -344,6 +344,16 @@ int esm_gfx950_model_free(esm_gfx950_ctx* ctx, esm_gfx950_model* model);
  * the nearest fp16 and back before it is quantised or multiplied
  * (src/model.cpp:1028-1033). Off by default. */
 int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int enabled);
+/* Width of the per-token W8A8 FFN intermediate, 24 (default) or 32 bits. No
+ * counterpart in the reference, whose fc1 output stays an fp32 array until
+ * Gelu and the next LinearInt8 quantise it (src/model.cpp:1036-1052). At 24
+ * fc1's GEMM stores each output rounded to its top 24 bits (sign, exponent,
+ * 15 mantissa bits; nearest, ties away from zero) and the GELU + per-token
+ * quantisation pass reads those: 3 bytes per value instead of 4 each way. An
+ * int8 code can then differ by one from the fp32 intermediate's only where
+ * the rounding (relative 2^-16 at most) crosses a quantisation midpoint.
+ * Observed forwards, per-tensor mode and the x86 numerics keep fp32. */
+int esm_gfx950_model_set_ffn_intermediate_bits(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int bits);
 /* Model::LoadFromGguf (reference src/model.cpp:229-298): creates a model
  * from an esm.cpp GGUF v3 file (src/io/gguf.cpp) -- esm.* metadata for the
  * shape; Q8_ESM layer linears ([N, K] int8 + [N] fp32 scales) when

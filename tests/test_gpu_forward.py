@@ -147,6 +147,55 @@ def test_gemm_split_k_rejects_other_counts():
             eg.set_gemm_split_k(bad)
 
 
+@pytest.mark.parametrize("shape", ["650M", "3B"])
+def test_ffn_intermediate_24_bits(dev, w650_small, small_batch, shape):
+    """The per-token forward's 24-bit fc1 output (the default,
+    esm_gfx950_model_set_ffn_intermediate_bits): the GELU + quant pass sees
+    each fp32 value rounded to 15 mantissa bits, so an int8 code moves by one
+    only where that rounding crosses a quantisation midpoint (about 4e-5 of
+    the codes, 0.2 per 5120-wide row). A row with one moved code then
+    re-quantises differently at every later site, so its logits drift at the
+    int8 noise level: the same mechanism that puts the reference's own two
+    CPU paths at 0.99992 on this batch. Bar, as for the oracle comparison:
+    correlation >= 0.9999 and argmax agreement >= 0.98 against the fp32
+    intermediate's logits (650M: two layers, 5120-wide rows, one wave per
+    row; 3B: one layer, 10240-wide rows over four waves). Per-tensor mode
+    keeps fp32 and ignores the setting."""
+    if shape == "3B":
+        w = syn.make_weights(syn.ESM2_3B.with_layers(1), seed=20261201 + 5, int8=True, keep_f32_linears=False)
+        batch = syn.batch_from_lengths([520, 90, 33], seed=11)
+    else:
+        w, batch = w650_small, small_batch
+    out = {}
+    for mode in (eg.ACT_PER_TOKEN, eg.ACT_PER_TENSOR):
+        m = eg.Model(dev, w, int8=True, act_mode=mode)
+        try:
+            for bits in (32, 24):
+                m.set_ffn_intermediate_bits(bits)
+                out[mode, bits] = m.forward_packed(batch.ids, batch.cu)
+        finally:
+            m.free()
+    a, b = out[eg.ACT_PER_TOKEN, 32], out[eg.ACT_PER_TOKEN, 24]
+    c = corr(a, b)
+    agree = float(np.mean(np.argmax(a, 1) == np.argmax(b, 1)))
+    print(f"{shape}: 24-bit vs fp32 intermediate corr={c:.8f} argmax_agree={agree:.4f} "
+          f"identical={np.array_equal(a, b)}")
+    assert np.all(np.isfinite(b))
+    assert c >= 0.9999, c
+    assert agree >= 0.98, agree
+    assert np.array_equal(out[eg.ACT_PER_TENSOR, 32], out[eg.ACT_PER_TENSOR, 24])
+
+
+def test_ffn_intermediate_bits_rejects_other_widths(dev, w650_small):
+    m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    try:
+        for bad in (16, 0, 33):
+            with pytest.raises(eg.Gfx950Error):
+                m.set_ffn_intermediate_bits(bad)
+    finally:
+        m.free()
+
+
 def test_packed_equals_serial(dev, w650_small, small_batch):
     """Per-token mode keeps every row independent, so packing changes nothing."""
     m = eg.Model(dev, w650_small, int8=True, act_mode=eg.ACT_PER_TOKEN)
