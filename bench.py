@@ -108,7 +108,15 @@ def measure(dev, model, batch, cfg, steps, warmup, parts):
     return ms, ms_events, sites, used
 
 
-def roofline_of(sites, T, cfg, batch, workload):
+# Bytes each GEMM moves per output value beyond its int8 operands: QKV
+# writes split-fp16 hi + lo parts; out-proj and fc2 read and write hidden
+# (the residual add); fc1 writes its 24-bit intermediate in per-token mode
+# and fp32 GELU output per tensor.
+def out_bytes(site, per_token):
+    return {"qkv": 4, "out": 8, "fc1": 3 if per_token else 4, "fc2": 8}[site]
+
+
+def roofline_of(sites, T, cfg, batch, workload, per_token=True):
     dom = max((s for s in GEMM_SITES if s in sites), key=lambda s: sites[s]["ms_per_step"])
     ops = gemm_ops(dom, T, cfg)
     achieved = ops / (sites[dom]["avg_us"] * 1e-6) / 1e12
@@ -126,7 +134,7 @@ def roofline_of(sites, T, cfg, batch, workload):
     r = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MI355X_PEAK_INT8_TOPS, "unit": "TFLOP/s",
          "frac": round(achieved / MI355X_PEAK_INT8_TOPS, 4), "traffic": traffic,
          "kernel": f"gemm_i8_v3_kernel, {dom} GEMM M={T} N={n_dom} K={k_dom} (int8 ops: 2MNK = {ops:.4g})",
-         "algorithmic_bytes": T * k_dom + n_dom * k_dom + 4 * T + 8 * n_dom + 4 * T * n_dom}
+         "algorithmic_bytes": T * k_dom + n_dom * k_dom + 4 * T + 8 * n_dom + out_bytes(dom, per_token) * T * n_dom}
     total_gemm_ms = sum(sites[s]["ms_per_step"] for s in GEMM_SITES if s in sites)
     all_ops = sum(gemm_ops(s, T, cfg) for s in GEMM_SITES) * cfg.num_layers
     r["all_i8_gemms_frac"] = round(all_ops / (total_gemm_ms * 1e-3) / 1e12 / MI355X_PEAK_INT8_TOPS, 4)
@@ -147,10 +155,10 @@ def roofline_of(sites, T, cfg, batch, workload):
     # kernel of its own: it runs in the QKV GEMM's epilogue.
     d, f = cfg.hidden_size, cfg.intermediate_size
     row_bytes = {
-        "ln_quant": T * d * (4 + 4 + 4 + 1) + 4 * T,   # hidden + residual in, hidden + int8 out, scales
+        "ln_quant": T * d * (4 + 1) + 4 * T,           # hidden in, int8 out, scales (residual added by the GEMM)
         "ln_quant_first": T * d * (4 + 1) + 4 * T,     # hidden in, int8 out, scales
         "attn_quant": T * d * (4 + 1) + 4 * T,         # fp32 in, int8 out, scales
-        "gelu_quant": T * f * (4 + 1) + 4 * T,         # fc1 fp32 in, int8 out, scales
+        "gelu_quant": T * f * (3 + 1) + 4 * T,         # fc1's 24-bit values in, int8 out, scales
     }
     rows = {}
     for site, b in row_bytes.items():
@@ -351,7 +359,7 @@ def main():
     ms_plain, ms_events, sites, used = measure(dev, model, batch, cfg, args.steps, args.warmup, args.parts)
     model.free()
     log(f"ms/step {ms_plain:.3f} (with per-kernel events {ms_events:.3f}); sites {sites}")
-    roofline = roofline_of(sites, T, cfg, batch, args.workload)
+    roofline = roofline_of(sites, T, cfg, batch, args.workload, per_token=mode == eg.ACT_PER_TOKEN)
     value = batch.residues / (ms_plain * 1e-3)
 
     workloads = []
