@@ -466,7 +466,9 @@ int esm_gfx950_observer_percentile(const esm_gfx950_observer* obs, const char* s
  * "layer{i}.ffn_ln_output" (before the first-block fp16 rounding) and
  * "layer{i}.inter_gelu" over the batch's [T, d] / [T, ffn] values in packed
  * row order (model.cpp:952-955,996-999,1023-1026,1047-1050). The batch runs as
- * one sequence group. T == 0 observes nothing. */
+ * one sequence group, and in per-token W8A8 with the fp32 FFN intermediate
+ * (the observer samples fc1's fp32 output), so its logits are those of
+ * esm_gfx950_model_set_ffn_intermediate_bits(32). T == 0 observes nothing. */
 int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                                      const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
                                      esm_gfx950_observer* obs);

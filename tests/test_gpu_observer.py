@@ -164,7 +164,9 @@ def test_forward_with_observer_fp32_vs_reference(dev, ref, fc1_fp16):
 def test_forward_with_observer_w8a8(dev, ref, per_token):
     """Per-tensor mode is the reference's own INT8 arithmetic: percentiles of
     the same positions within 1e-2. Per-token mode quantises activations
-    differently from the reference (per row), so it is held to 5e-2."""
+    differently from the reference (per row), so it is held to 5e-2. An
+    observed forward samples fc1's fp32 output, so it runs the fp32 FFN
+    intermediate: its logits equal the plain forward's at that width."""
     cfg = syn.ESM2_650M.with_layers(2)
     w = syn.make_weights(cfg, seed=20261201 + 4, int8=True, keep_f32_linears=False)
     b = syn.batch_from_lengths([130, 61, 250, 2, 97, 200], seed=7)
@@ -176,6 +178,7 @@ def test_forward_with_observer_w8a8(dev, ref, per_token):
     try:
         logits = m.forward_packed_with_observer(b.ids, b.cu, obs)
         m.set_parts(1)
+        m.set_ffn_intermediate_bits(32)
         assert np.array_equal(logits, m.forward_packed(b.ids, b.cu))
         rm.forward_packed(b, theirs)
         sites = _sites(cfg.num_layers)
