@@ -342,7 +342,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on exactly one GPU (got --gpus {args.gpus}); the packed forward "
-              "shards whole sequences across GPUs with no exchange -- see DESIGN.md.", file=sys.stderr)
+              "would shard whole sequences across GPUs with no exchange; only one GPU is measured here.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
 
