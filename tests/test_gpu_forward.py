@@ -147,7 +147,7 @@ def test_gemm_split_k_rejects_other_counts():
             eg.set_gemm_split_k(bad)
 
 
-@pytest.mark.parametrize("shape", ["650M", "3B"])
+@pytest.mark.parametrize("shape", ["650M", "3B", "narrow"])
 def test_ffn_intermediate_24_bits(dev, w650_small, small_batch, shape):
     """The per-token forward's 24-bit fc1 output (the default,
     esm_gfx950_model_set_ffn_intermediate_bits): the GELU + quant pass sees
@@ -159,9 +159,14 @@ def test_ffn_intermediate_24_bits(dev, w650_small, small_batch, shape):
     CPU paths at 0.99992 on this batch. Bar, as for the oracle comparison:
     correlation >= 0.9999 and argmax agreement >= 0.98 against the fp32
     intermediate's logits (650M: two layers, 5120-wide rows, one wave per
-    row; 3B: one layer, 10240-wide rows over four waves). Per-tensor mode
-    keeps fp32 and ignores the setting."""
-    if shape == "3B":
+    row; 3B: one layer, 10240-wide rows over four waves; narrow: d 256, ffn
+    1024, rows shorter than the pass's 5120-wide register tile, masked).
+    Per-tensor mode keeps fp32 and ignores the setting."""
+    if shape == "narrow":
+        cfg = syn.EsmConfig("narrow-w8a8", 2, 256, 4, 1024)
+        w = syn.make_weights(cfg, seed=20261201 + 7, int8=True, keep_f32_linears=False)
+        batch = small_batch
+    elif shape == "3B":
         w = syn.make_weights(syn.ESM2_3B.with_layers(1), seed=20261201 + 5, int8=True, keep_f32_linears=False)
         batch = syn.batch_from_lengths([520, 90, 33], seed=11)
     else:
