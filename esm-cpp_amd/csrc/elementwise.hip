@@ -302,8 +302,9 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
 // The same pass over the INT8 GEMM's 24-bit fc1 output (kEpiF32R24): a
 // high plane xh of bits 31..16 and a low plane xl of bits 15..8, in which
 // stored position 2 i + j of each aligned 64-column group holds column
-// 32 j + i. WAVES waves share a row (1: four rows per block; 4: one row,
-// their maxima meeting in LDS), each wave NV * 512 stored positions, eight
+// 32 j + i. WAVES waves share a row (1: four rows per block; 2: two rows;
+// 4: one row; several waves' maxima meet in LDS), each wave NV * 512 stored
+// positions, eight
 // consecutive ones per lane per step: one 16-byte high and one 8-byte low
 // load give columns 4 k .. 4 k + 3 and 32 + 4 k .. (k = position / 8 within
 // the group), whose int8 values go out as two 4-byte words. cols % 64 == 0.
@@ -311,14 +312,17 @@ template <int NV, int WAVES>
 __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
     const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl, int ldx, int rows, int cols,
     int8_t* __restrict__ q, int ldq, float* __restrict__ scales) {
-  static_assert(WAVES == 1 || WAVES == 4, "one or four waves per row");
+  static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "one, two or four waves per row");
   __shared__ float s_max[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = WAVES == 1 ? blockIdx.x * kRowsPerBlock + wave : blockIdx.x;
+  const int row = blockIdx.x * (kRowsPerBlock / WAVES) + wave / WAVES;
   if (WAVES == 1 && row >= rows) return;
-  const int part = WAVES == 1 ? 0 : wave;
-  const uint16_t* hr = xh + static_cast<size_t>(row) * ldx;
-  const uint8_t* lr = xl + static_cast<size_t>(row) * ldx;
+  // Several waves per row: every wave reaches the barrier below; a row past
+  // the end reads row 0 and stores nothing.
+  const bool live = row < rows;
+  const int part = wave % WAVES;
+  const uint16_t* hr = xh + static_cast<size_t>(live ? row : 0) * ldx;
+  const uint8_t* lr = xl + static_cast<size_t>(live ? row : 0) * ldx;
   uint4 hv[NV];
   uint2 lv[NV];
 #pragma unroll
@@ -349,7 +353,11 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
   if constexpr (WAVES > 1) {
     if (lane == 0) s_max[wave] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    const int w0 = wave - part;
+    amax = s_max[w0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) amax = fmaxf(amax, s_max[w0 + w]);
+    if (!live) return;
   }
   const float scale = act_scale_from_absmax(0.5f * amax);
   const float inv = 0.5f * (1.0f / scale);
@@ -637,7 +645,14 @@ hipError_t launch_gelu_quant_rows_r24(const uint16_t* xh, const uint8_t* xl, int
   if (rows <= 0) return hipSuccess;
   if (cols % 64 != 0 || ldx % 8 != 0 || ldq % 4 != 0 || cols > 10240) return hipErrorInvalidValue;
   const dim3 b(256);
-  if (cols <= 5120)
+  // Below kSplitRows rows a one-wave-per-row grid leaves most SIMDs with one
+  // or two waves, each waiting out its row's load latency alone: two waves
+  // per row double the waves in flight (same bytes, same codes).
+  constexpr int kSplitRows = 8192;
+  if (cols <= 5120 && rows < kSplitRows)
+    hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<5, 2>), dim3((rows + 1) / 2), b, 0, s, xh, xl, ldx, rows, cols, q,
+                       ldq, scales);
+  else if (cols <= 5120)
     hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<10, 1>), rows_grid(rows), b, 0, s, xh, xl, ldx, rows, cols, q, ldq,
                        scales);
   else
