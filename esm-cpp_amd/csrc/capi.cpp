@@ -502,6 +502,39 @@ extern "C" int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int 
   return ESM_GFX950_OK;
 }
 
+extern "C" int esm_gfx950_linear_i8_gelu_quant_r24(esm_gfx950_ctx* ctx, const int8_t* A, int lda,
+                                                   const float* a_scale, const esm_gfx950_weight* W, const float* bias,
+                                                   int M, uint16_t* inter_hi, uint8_t* inter_lo, int8_t* q, int ldq,
+                                                   float* q_scale) {
+  if (!ctx) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_REQUIRE(ctx, A && a_scale && W && inter_hi && inter_lo && q && q_scale && M >= 0,
+              "linear_i8_gelu_quant_r24: bad arguments");
+  ESM_REQUIRE(ctx, W->N % 64 == 0 && W->N <= 10240, "linear_i8_gelu_quant_r24: N must be a multiple of 64, <= 10240");
+  ESM_REQUIRE(ctx, ldq >= W->N && ldq % 4 == 0, "linear_i8_gelu_quant_r24: ldq must be >= N and a multiple of 4");
+  GemmI8Args p;
+  p.A = A;
+  p.lda = lda;
+  p.W = W->data;
+  p.ldw = W->ldk;
+  p.M = M;
+  p.N = W->N;
+  p.K = W->ldk;
+  p.a_scale = a_scale;
+  p.w_scale = W->scales;
+  p.bias = bias;
+  p.C_f16 = inter_hi;
+  p.C_u8 = inter_lo;
+  p.ldc = W->N;
+  ESM_REQUIRE(ctx, gemm_i8_pipelined_ok(p),
+              "linear_i8_gelu_quant_r24: needs K % 128 == 0, lda % 16 == 0 and 16-byte aligned operands");
+  if (M == 0) return ESM_GFX950_OK;
+  // The forward's sequence (layer_int8): the GEMM's 24-bit epilogue, then
+  // the GELU + per-row quantisation pass over the two planes.
+  ESM_HIP(ctx, launch_gemm_i8(p, kEpiF32R24, ctx->stream));
+  ESM_HIP(ctx, launch_gelu_quant_rows_r24(inter_hi, inter_lo, W->N, M, W->N, q, ldq, q_scale, ctx->stream));
+  return ESM_GFX950_OK;
+}
+
 namespace {
 int quantize_into(esm_gfx950_ctx* ctx, const float* x, int M, int K, int mode, int8_t* q, int ldq,
                   float* scales, float* absmax_slot) {
@@ -1407,7 +1440,10 @@ class ObsRun {
 
   // The next site's values: x [n] fp32 on the device (gelu: GELU applied on
   // the fly, for the per-token path whose fc1 output is stored pre-GELU).
-  int capture(esm_gfx950_ctx* ctx, const float* x, size_t n, int gelu) {
+  // r24_lo != null: x is kEpiF32R24's high plane (uint16) and r24_lo its low
+  // plane, rows of r24_cols values, GELU applied.
+  int capture(esm_gfx950_ctx* ctx, const void* x, size_t n, int gelu, const uint8_t* r24_lo = nullptr,
+              int r24_cols = 0) {
     if (next_ >= sites_.size() || sites_[next_].n != n)
       return ctx->fail(ESM_GFX950_INTERNAL, "forward_with_observer: site sequence mismatch");
     if (fail_site_ >= 0 && static_cast<size_t>(fail_site_) == next_)
@@ -1424,8 +1460,12 @@ class ObsRun {
     if (st.count == 0) return ESM_GFX950_OK;
     ESM_HIP(ctx, hipMemcpyAsync(obs_->d_pos + off, obs_->h_pos + off, st.count * 4, hipMemcpyHostToDevice,
                                 ctx->stream));
-    ESM_HIP(ctx, launch_observe_gather(x, obs_->d_pos + off, static_cast<int>(st.count), gelu, obs_->d_val + off,
-                                       ctx->stream));
+    if (r24_lo)
+      ESM_HIP(ctx, launch_observe_gather_r24(static_cast<const uint16_t*>(x), r24_lo, r24_cols, obs_->d_pos + off,
+                                             static_cast<int>(st.count), obs_->d_val + off, ctx->stream));
+    else
+      ESM_HIP(ctx, launch_observe_gather(static_cast<const float*>(x), obs_->d_pos + off, static_cast<int>(st.count),
+                                         gelu, obs_->d_val + off, ctx->stream));
     return ESM_GFX950_OK;
   }
 
@@ -1651,7 +1691,7 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
   g.bias = L.fc1.bias;
   g.C_f32 = a.inter;
   g.ldc = f;
-  if (tok && m->ffn_r24 && !ob && f % 64 == 0 && f <= 10240 && gemm_i8_pipelined_ok(g)) {
+  if (tok && m->ffn_r24 && f % 64 == 0 && f <= 10240 && gemm_i8_pipelined_ok(g)) {
     // Dequant + bias rounded to 24 bits (a high 16-bit plane, then a low
     // byte plane, in the FFN buffer): 3 bytes per value instead of 4 for the
     // GEMM to write and the GELU + quant pass to read.
@@ -1661,6 +1701,8 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_TRY(ctx->time_begin("fc1", &slot));
     ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32R24, s));
     ESM_TRY(ctx->time_end(slot));
+    // The observer sees GELU of the 24-bit values fc2's quantisation reads.
+    if (ob) ESM_TRY(ob->capture(ctx, g.C_f16, Tf, 1, g.C_u8, f));
     ESM_TRY(ctx->time_begin("gelu_quant", &slot));
     ESM_HIP(ctx, launch_gelu_quant_rows_r24(g.C_f16, g.C_u8, f, T, f, a.xq, ldq_f, a.xs, s));
     ESM_TRY(ctx->time_end(slot));
@@ -1985,8 +2027,16 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
 }
 
 // The whole forward of one part on ctx->stream; logits rows [0, T).
+// Hidden-state capture for esm_gfx950_forward_hidden_states: base points at
+// this part's first row of state 0 in a device buffer [layers + 1, T, d],
+// stride is T * d floats between states.
+struct HiddenCapture {
+  float* base = nullptr;
+  size_t stride = 0;
+};
+
 int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx950_model::Part& P, float* logits,
-                 ObsRun* ob = nullptr) {
+                 ObsRun* ob = nullptr, const HiddenCapture* cap = nullptr) {
   const auto& c = m->cfg;
   const int T = P.T;
   const int d = c.hidden_size, V = c.vocab_size, H = c.num_heads, dh = c.head_dim;
@@ -2002,6 +2052,12 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   for (const auto& q : m->parts) active += q.T > 0 ? 1 : 0;
   const int cus = active > 1 ? std::max(1, device_cus() / active) : 0;
   ESM_HIP(ctx, launch_embed(md.ids, md.tok_scale, m->embed, T, d, c.mask_token_id, a.hidden, s));
+  const size_t Td = static_cast<size_t>(T) * d;
+  auto capture = [&](size_t state, const float* src) -> int {
+    ESM_HIP(ctx, hipMemcpyAsync(cap->base + state * cap->stride, src, Td * 4, hipMemcpyDeviceToDevice, s));
+    return ESM_GFX950_OK;
+  };
+  if (cap) ESM_TRY(capture(0, a.hidden));
   // x86 numerics: fc2 output awaiting its residual add (in the next
   // LayerNorm); default numerics: fc2's split-K partial sums awaiting theirs.
   const float* pending = nullptr;
@@ -2017,12 +2073,22 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     } else if (c.weights_int8) {
       SplitResid split_out;
       const bool last = li + 1 == m->layers.size();
+      // A captured forward keeps every layer's hidden state whole: no split-K
+      // partial sums left for the next layer (int32 sums, same bits).
       ESM_TRY(layer_int8(ctx, m, L, round16, a, md, T, nwork, P.maxL, pending, ob, cus, &pending_split,
-                         last ? nullptr : &split_out));
+                         last || cap ? nullptr : &split_out));
       pending = nullptr;  // fc2 added its output into hidden (or left split partials)
       pending_split = split_out;
     } else {
       ESM_TRY(layer_f32(ctx, m, L, round16, a, md, T, nwork, ob));
+    }
+    if (cap && li + 1 < m->layers.size()) {
+      if (pending) {
+        // The residual add the next LayerNorm would fuse (the same fp32 add).
+        ESM_HIP(ctx, launch_residual_add(a.hidden, pending, Td, s));
+        pending = nullptr;
+      }
+      ESM_TRY(capture(li + 1, a.hidden));
     }
   }
   if (x86) {
@@ -2031,6 +2097,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
     // (reference src/model.cpp:1181-1239).
     ESM_HIP(ctx, launch_layernorm_x86(a.hidden, pending, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d,
                                       nullptr, 0, s));
+    if (cap) ESM_TRY(capture(m->layers.size(), a.ln));
     int slot;
     ESM_TRY(ctx->time_begin("lm_dense", &slot));
     ESM_HIP(ctx, launch_linear_x86(a.ln, d, m->lm_dense_w, d, m->lm_dense_b, a.lm_a, d, T, d, d, kF32Gelu, s));
@@ -2044,6 +2111,7 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
   // decoder + bias (reference src/model.cpp:1181-1239).
   ESM_HIP(ctx, launch_layernorm(a.hidden, pending, m->final_ln_w, m->final_ln_b, c.layer_norm_eps, a.ln, T, d,
                                 nullptr, s));
+  if (cap) ESM_TRY(capture(m->layers.size(), a.ln));
   DevLinear dense;
   dense.w32 = m->lm_dense_w;
   dense.bias = m->lm_dense_b;
@@ -2252,6 +2320,39 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
   }
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
+}
+
+extern "C" int esm_gfx950_forward_hidden_states(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                                const int32_t* cu, int B, int T, float* logits, float* hidden) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  ESM_TRY(esm_gfx950_batch_upload(ctx, m, ids, cu, B, T));
+  if (T == 0) return ESM_GFX950_OK;
+  ESM_REQUIRE(ctx, logits && hidden, "forward_hidden_states: null logits or hidden");
+  const int V = m->cfg.vocab_size, d = m->cfg.hidden_size;
+  const size_t states = m->layers.size() + 1, Td = static_cast<size_t>(T) * d;
+  float* dev_hidden = nullptr;
+  ESM_HIP(ctx, hipMalloc(&dev_hidden, states * Td * 4));
+  auto run = [&]() -> int {
+    const bool several = m->parts.size() > 1 && m->parts[1].T > 0;
+    if (several) ESM_TRY(fork_parts(ctx, m));
+    for (auto& P : m->parts) {
+      if (P.T == 0) continue;
+      StreamScope scope(ctx, several ? P.stream : ctx->stream);
+      const Arena a = part_arena(m, P);
+      HiddenCapture cap{dev_hidden + static_cast<size_t>(P.t0) * d, Td};
+      ESM_TRY(forward_part(ctx, m, P, a.logits, nullptr, &cap));
+      ESM_HIP(ctx, hipMemcpyAsync(logits + static_cast<size_t>(P.t0) * V, a.logits, static_cast<size_t>(P.T) * V * 4,
+                                  hipMemcpyDeviceToHost, ctx->stream));
+    }
+    if (several) ESM_TRY(join_parts(ctx, m));
+    ESM_HIP(ctx, hipMemcpyAsync(hidden, dev_hidden, states * Td * 4, hipMemcpyDeviceToHost, ctx->stream));
+    ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return ESM_GFX950_OK;
+  };
+  const int rc = run();
+  if (rc != ESM_GFX950_OK) hipStreamSynchronize(ctx->stream);
+  hipFree(dev_hidden);
+  return rc;
 }
 
 // ---------------------------------------------------------------- observer

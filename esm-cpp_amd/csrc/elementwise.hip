@@ -480,6 +480,19 @@ __global__ void observe_gather_kernel(const float* __restrict__ x, const uint32_
   out[w] = fabsf(v);
 }
 
+// The same over kEpiF32R24's planes (xh bits 31..16, xl bits 15..8, row
+// pitch cols; stored position 2 i + j of each 64-column group holds column
+// 32 j + i): |GELU(x)| of the 24-bit values the GELU + quantisation pass reads.
+__global__ void observe_gather_r24_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl, int cols,
+                                          const uint32_t* __restrict__ pos, int count, float* __restrict__ out) {
+  const int w = blockIdx.x * blockDim.x + threadIdx.x;
+  if (w >= count) return;
+  const uint32_t i = pos[w], r = i / static_cast<uint32_t>(cols), c = i - r * static_cast<uint32_t>(cols);
+  const size_t at = static_cast<size_t>(r) * cols + (c & ~63u) + 2u * (c & 31u) + ((c >> 5) & 1u);
+  const float v = __uint_as_float((static_cast<uint32_t>(xh[at]) << 16) | (static_cast<uint32_t>(xl[at]) << 8));
+  out[w] = fabsf(0.5f * gelu2_as(v));
+}
+
 __global__ void gelu_kernel(const float* __restrict__ x, float* __restrict__ out, size_t n) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
@@ -694,6 +707,15 @@ hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s)
   size_t g = (n + 255) / 256;
   if (g > 4096) g = 4096;
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_observe_gather_r24(const uint16_t* xh, const uint8_t* xl, int cols, const uint32_t* pos, int count,
+                                     float* out, hipStream_t s) {
+  if (count <= 0) return hipSuccess;
+  if (cols <= 0 || cols % 64 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(observe_gather_r24_kernel, dim3((count + 255) / 256), dim3(256), 0, s, xh, xl, cols, pos, count,
+                     out);
   return hipGetLastError();
 }
 

@@ -643,7 +643,14 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
             if (!FULL && m0 + lr + u >= p.M) continue;
             const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
             const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
-            const uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
+            uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
+            // A NaN's bit pattern must not take the rounding add (it could
+            // carry into the sign or leave an infinity); one unordered
+            // compare per pair finds NaNs, which become the quiet NaN.
+            if (__builtin_expect(__builtin_isunordered(v0, v1), 0)) {
+              if (__builtin_isnan(v0)) b0 = 0x7fc00000u;
+              if (__builtin_isnan(v1)) b1 = 0x7fc00000u;
+            }
             const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
             auto* hdst = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(htile) + static_cast<size_t>(R * ldc) * 2u + lane_h);
             auto* ldst = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ltile) + static_cast<size_t>(R * ldc) + lane_l);

@@ -23,7 +23,8 @@ enum GemmEpilogue : int {
   kEpiQkvSplit = 7,   // as kEpiQkvRopeF32, then Q *= q_prescale and every value
                       // stored as a split-fp16 word (C_f32 reinterpreted)
   kEpiF32R24 = 8,     // kEpiF32's value rounded to its top 24 bits (sign,
-                      // exponent, 15 mantissa bits; nearest, ties away):
+                      // exponent, 15 mantissa bits; nearest, ties away;
+                      // NaN -> the quiet NaN 0x7fc00000):
                       // bits 31..16 to C_f16 [M, ldc], bits 15..8 to C_u8
                       // [M, ldc]; in each aligned group of 64 columns, stored
                       // position 2 i + j holds column 32 j + i (i < 32, j < 2).
@@ -251,6 +252,10 @@ hipError_t launch_fill_f32(float* x, size_t n, float v, hipStream_t s);
 // with the Abramowitz & Stegun erf of the fused GELU + quantisation kernel).
 hipError_t launch_observe_gather(const float* x, const uint32_t* pos, int count, int gelu, float* out,
                                  hipStream_t s);
+// The same (with GELU) over kEpiF32R24's two planes, flat positions
+// row * cols + column; cols % 64 == 0.
+hipError_t launch_observe_gather_r24(const uint16_t* xh, const uint8_t* xl, int cols, const uint32_t* pos, int count,
+                                     float* out, hipStream_t s);
 hipError_t launch_gelu(const float* x, float* out, size_t n, hipStream_t s);
 hipError_t launch_residual_add(float* y, const float* x, size_t n,
                                hipStream_t s);

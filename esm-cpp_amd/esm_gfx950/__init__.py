@@ -55,7 +55,8 @@ EXPORTED = [
     "esm_gfx950_attention_work_items", "esm_gfx950_layernorm_avx512", "esm_gfx950_gelu_avx512",
     "esm_gfx950_expf_glibc", "esm_gfx950_linear_f32_avx512", "esm_gfx950_rope_apply_varlen_avx512",
     "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics", "esm_gfx950_linear_i8_noalloc",
-    "esm_gfx950_model_set_ffn_intermediate_bits",
+    "esm_gfx950_model_set_ffn_intermediate_bits", "esm_gfx950_linear_i8_gelu_quant_r24",
+    "esm_gfx950_forward_hidden_states",
 ]
 
 
@@ -98,6 +99,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_linear_i8_q": (i32, [vp, vp, i32, vp, vp, vp, vp, i32, i32]),
         "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
         "esm_gfx950_gelu_quantize_act": (i32, [vp, vp, i32, i32, vp, i32, vp]),
+        "esm_gfx950_linear_i8_gelu_quant_r24": (i32, [vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp]),
+        "esm_gfx950_forward_hidden_states": (i32, [vp, vp, vp, vp, i32, i32, vp, vp]),
         "esm_gfx950_set_gemm_tile_rows": (i32, [i32]),
         "esm_gfx950_set_gemm_split_k": (i32, [i32]),
         "esm_gfx950_model_set_lm_dense_split": (i32, [vp, vp, i32]),
@@ -334,6 +337,15 @@ class Device:
     def gelu_quantize_act(self, x: DeviceArray, M: int, K: int, q: DeviceArray, ldq: int, scales: DeviceArray):
         """GELU then per-token int8 quantisation, fused (fc2's input in the INT8 FFN)."""
         self._check(self.lib.esm_gfx950_gelu_quantize_act(self.ctx, x.ptr, M, K, q.ptr, ldq, scales.ptr))
+
+    def linear_i8_gelu_quant_r24(self, A: DeviceArray, lda: int, a_scale: DeviceArray, W: Weight,
+                                 bias: Optional[DeviceArray], M: int, inter_hi: DeviceArray, inter_lo: DeviceArray,
+                                 q: DeviceArray, ldq: int, q_scale: DeviceArray):
+        """fc1 with the 24-bit intermediate, then GELU + per-token quantisation
+        (the default forward's FFN up path, esm_gfx950_linear_i8_gelu_quant_r24)."""
+        self._check(self.lib.esm_gfx950_linear_i8_gelu_quant_r24(
+            self.ctx, A.ptr, lda, a_scale.ptr, W.handle, bias.ptr if bias is not None else None, M, inter_hi.ptr,
+            inter_lo.ptr, q.ptr, ldq, q_scale.ptr))
 
     def linear_i8(self, A: DeviceArray, W: Weight, bias: Optional[DeviceArray], C_out: DeviceArray, M: int, N: int,
                   K: int, mode: int):
@@ -597,6 +609,19 @@ class Model:
         self.dev._check(self.dev.lib.esm_gfx950_forward_packed(self.dev.ctx, self.handle, _ptr(ids), _ptr(cu),
                                                                len(cu) - 1, T, out.ptr, 1))
         return out
+
+    def forward_hidden_states(self, ids: np.ndarray, cu: np.ndarray):
+        """Packed forward returning (logits [T, vocab], hidden [layers + 1, T, d]):
+        post-embed, each layer's output, and the post-final-LN state last
+        (reference Model::ForwardWithHiddenStates, esm_gfx950_forward_hidden_states)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        cu = np.ascontiguousarray(cu, np.int32)
+        T = int(ids.shape[0])
+        logits = np.empty((T, self.cfg.vocab_size), np.float32)
+        hidden = np.empty((self.cfg.num_layers + 1, T, self.cfg.hidden_size), np.float32)
+        self.dev._check(self.dev.lib.esm_gfx950_forward_hidden_states(
+            self.dev.ctx, self.handle, _ptr(ids), _ptr(cu), len(cu) - 1, T, _ptr(logits), _ptr(hidden)))
+        return logits, hidden
 
     def forward_packed_with_observer(self, ids: np.ndarray, cu: np.ndarray, observer: "ActivationObserver"):
         """Packed forward that also feeds `observer` at the reference's four

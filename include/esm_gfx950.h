@@ -173,6 +173,23 @@ int esm_gfx950_set_gemm_split_k(int splits);
 int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const float* a_scale,
                            const esm_gfx950_weight* W, const float* bias, float* C, int M, int gelu);
 
+/* The per-token W8A8 FFN up-projection exactly as the default forward runs
+ * it: fc1 (LinearInt8, src/model.cpp:1039-1045), Gelu (:1046-1048,
+ * src/kernels/gelu.cpp:30-35) and the per-token quantisation of fc2's input
+ * (gemm_int8.cpp:391-508 with one scale per row). fc1's dequantised value
+ * fma(float(acc), a_scale[m] * w_scale[n], bias[n]) is rounded to its top 24
+ * bits (0x80 added to the bit pattern, the low byte cleared: nearest, ties
+ * away from zero; NaN becomes the quiet NaN 0x7fc00000) and stored as two
+ * planes, inter_hi uint16 [M, N] (bits 31..16) and inter_lo uint8 [M, N]
+ * (bits 15..8), in which stored position 64 g + 2 i + j holds column
+ * 64 g + 32 j + i; the GELU + quantisation pass reads them and writes q int8
+ * [M, ldq] (zero past N) and q_scale fp32 [M]. A int8 [M, lda], a_scale
+ * fp32 [M], bias fp32 [N] or NULL; all device pointers. Requires N % 64 == 0,
+ * N <= 10240, K % 128 == 0, lda % 16 == 0, ldq >= N, ldq % 4 == 0. */
+int esm_gfx950_linear_i8_gelu_quant_r24(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const float* a_scale,
+                                        const esm_gfx950_weight* W, const float* bias, int M, uint16_t* inter_hi,
+                                        uint8_t* inter_lo, int8_t* q, int ldq, float* q_scale);
+
 /* Activation quantisation: x fp32 [M, K] -> q int8 [M, ldq] (zero padded
  * past K) and scales fp32 [M] (all equal in PER_TENSOR mode). Reference
  * QuantizeActPrefixAvx512 (gemm_int8.cpp:391-508) / QuantizeActivation-
@@ -387,6 +404,18 @@ int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, 
 int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                               const int32_t* cu_seqlens, int batch_size, int total_tokens,
                               float* logits, int logits_on_device);
+/* Model::ForwardWithHiddenStates / ForwardPackedInto's hidden_packed_out
+ * (include/esm_cpp/model.h:184-191, src/model.cpp:1149-1189): the packed
+ * forward of esm_gfx950_forward_packed with HOST ids, cu_seqlens and logits
+ * [T, vocab], that also writes every hidden state to HOST hidden
+ * [num_layers + 1, T, hidden_size]: [0] after the embedding, [i] after layer
+ * i, and [num_layers] the post-final-LayerNorm state in place of the last
+ * layer's output. The logits equal esm_gfx950_forward_packed's (the layers
+ * add fc2's output into the hidden state in its GEMM; split-K partial sums
+ * are not carried across a layer boundary in this call). Synchronises. */
+int esm_gfx950_forward_hidden_states(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                                     const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
+                                     float* hidden);
 /* Stages a packed batch in the model's device buffers: ids, per-token
  * embedding scale, in-sequence positions, cu_seqlens, the attention work
  * list and the RoPE tables (one pinned host-to-device copy). */

@@ -289,7 +289,28 @@ static void linear_call(const or_model* m, int layer, int j, const float* A, flo
   or_dequant(accbuf, sbuf, m->w_scale[idx], m->bias[idx], M, N, 0, C);
 }
 
+float or_round24(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  if ((b & 0x7fffffffu) > 0x7f800000u)
+    b = 0x7fc00000u; /* NaN: the quiet NaN (an add could carry into the sign) */
+  else
+    b += 0x80u;
+  b &= 0xffffff00u;
+  memcpy(&x, &b, 4);
+  return x;
+}
+
+void or_round24_array(const float* x, float* out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = or_round24(x[i]);
+}
+
 int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits) {
+  return or_forward_packed_hidden(m, ids, cu, B, T, logits, NULL);
+}
+
+int or_forward_packed_hidden(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits,
+                             float* hidden_out) {
   const int d = m->hidden, H = m->heads, dh = m->head_dim, f = m->ffn, V = m->vocab;
   const size_t Td = (size_t)T * d, Tf = (size_t)T * f;
   int maxL = 0;
@@ -329,6 +350,8 @@ int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, 
     }
   }
 
+  if (hidden_out) memcpy(hidden_out, hidden, Td * 4);
+
   const float q_scale = 1.0f / sqrtf((float)dh);
   void (*layernorm)(const float*, const float*, const float*, float, float*, int, int) =
       m->x86 ? or_x86_layernorm : or_layernorm;
@@ -357,11 +380,14 @@ int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, 
     layernorm(hidden, m->ln2_w[l], m->ln2_b[l], m->eps, ln, T, d);
     if (m->fc1_fp16 && l == 0) or_round_fp16(ln, Td);
     linear_call(m, l, 4, ln, inter, T, f, d, qbuf, sbuf, acc);
+    if (m->ffn_round24 && m->weights_int8 && m->act_per_token && !m->x86) or_round24_array(inter, inter, Tf);
     gelu(inter, inter_g, Tf);
     linear_call(m, l, 5, inter_g, proj, T, d, f, qbuf, sbuf, acc);
     for (size_t i = 0; i < Td; ++i) hidden[i] += proj[i];
+    if (hidden_out) memcpy(hidden_out + (size_t)(l + 1) * Td, hidden, Td * 4);
   }
   layernorm(hidden, m->final_ln_w, m->final_ln_b, m->eps, ln, T, d);
+  if (hidden_out) memcpy(hidden_out + (size_t)m->num_layers * Td, ln, Td * 4);
   linear_f32(ln, m->lm_dense_w, m->lm_dense_b, proj, T, d, d);
   gelu(proj, attn, Td);
   layernorm(attn, m->lm_ln_w, m->lm_ln_b, m->eps, ln, T, d);

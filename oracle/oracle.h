@@ -111,12 +111,29 @@ typedef struct {
                           GELU, RoPE, attention, FP32 Linear and activation quantisation
                           (Isa::Avx512Vnni: LinearVnni); 2: the same with LinearAmx's row
                           split (Isa::Amx); requires weights_int8 == 0 or act_per_token == 0 */
+  int ffn_round24;     /* W8A8 per-token only: 1 rounds fc1's output to its top 24 bits
+                          (or_round24) before GELU, the FFN intermediate of the GPU's default
+                          per-token forward; not a reference mode (the reference keeps fp32) */
 } or_model;
 
 /* Embed (src/model.cpp:737-778) + TransformerBlock per layer (:932-1066) +
  * final LN and lm head (:1181-1239): packed logits [T, vocab]. Returns 0,
  * or -1 on allocation failure. */
 int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits);
+/* The same, also writing every hidden state to hidden [num_layers + 1, T,
+ * hidden] when it is not NULL: [0] post-embed, [i] after layer i, and [N]
+ * the post-final-LN state in place of the last layer's output
+ * (ForwardPackedInto's hidden_packed_out, model.cpp:1149-1189). */
+int or_forward_packed_hidden(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits,
+                             float* hidden_out);
+
+/* x rounded to its top 24 bits (sign, exponent, 15 mantissa bits): 0x80
+ * added to the bit pattern, then the low byte cleared, i.e. round to
+ * nearest with ties away from zero; values that round past the largest
+ * finite float become infinity; NaN becomes the quiet NaN 0x7fc00000.
+ * Not a reference function: the GPU's default FFN intermediate format. */
+float or_round24(float x);
+void or_round24_array(const float* x, float* out, size_t n);
 
 #ifdef __cplusplus
 }

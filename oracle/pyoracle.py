@@ -34,13 +34,15 @@ class _OrModel(C.Structure):
                 ("ln2_w", C.POINTER(vp)), ("ln2_b", C.POINTER(vp)), ("w_f32", C.POINTER(vp)),
                 ("w_i8", C.POINTER(vp)), ("w_scale", C.POINTER(vp)), ("bias", C.POINTER(vp)),
                 ("final_ln_w", vp), ("final_ln_b", vp), ("lm_dense_w", vp), ("lm_dense_b", vp),
-                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp), ("fc1_fp16", i32), ("x86", i32)]
+                ("lm_ln_w", vp), ("lm_ln_b", vp), ("lm_decoder_bias", vp), ("fc1_fp16", i32), ("x86", i32),
+                ("ffn_round24", i32)]
 
 
 LINEARS = ("q", "k", "v", "out", "fc1", "fc2")
 
 
-def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False, x86: bool = False):
+def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False, x86: bool = False,
+                  ffn_bits: int = 32):
     """Builds the or_model descriptor (and keeps its arrays alive)."""
     cfg = weights.cfg
     keep = []
@@ -82,6 +84,11 @@ def make_or_model(weights, int8: bool, per_token: bool, fc1_fp16: bool = False, 
     m.lm_decoder_bias = p(F["lm_head.decoder.bias"])
     m.fc1_fp16 = int(fc1_fp16)
     m.x86 = int(x86)  # 0 none, 1 avx512vnni, 2 amx
+    if ffn_bits not in (24, 32):
+        raise ValueError("ffn_bits must be 24 or 32")
+    if ffn_bits == 24 and not (int8 and per_token and not x86):
+        raise ValueError("the 24-bit FFN intermediate exists only in the per-token W8A8 forward")
+    m.ffn_round24 = int(ffn_bits == 24)
     keep.extend([ln1w, ln1b, ln2w, ln2b, wf, wi, ws, bs])
     return m, keep
 
@@ -108,6 +115,8 @@ class Oracle:
             "or_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
             "or_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
             "or_forward_packed": [C.POINTER(_OrModel), vp, vp, i32, i32, vp],
+            "or_forward_packed_hidden": [C.POINTER(_OrModel), vp, vp, i32, i32, vp, vp],
+            "or_round24_array": [vp, vp, sz],
             "or_x86_gelu": [vp, vp, sz],
             "or_x86_layernorm": [vp, vp, vp, f32, vp, i32, i32],
             "or_x86_rope_varlen": [vp, vp, vp, vp, i32, i32, i32],
@@ -119,7 +128,7 @@ class Oracle:
         for name, args in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
-            fn.restype = i32 if name == "or_forward_packed" else None
+            fn.restype = i32 if name.startswith("or_forward_packed") else None
         self.lib = lib
 
     def gemm_i8_i32(self, A, W):
@@ -265,21 +274,35 @@ class Oracle:
         self.lib.or_x86_quant_act(_p(x), x.size, _p(q), C.byref(s))
         return q, float(s.value)
 
+    def round24(self, x):
+        """or_round24 of every element (the 24-bit FFN intermediate)."""
+        x = _c(x, np.float32)
+        out = np.empty_like(x)
+        self.lib.or_round24_array(_p(x), _p(out), x.size)
+        return out
+
     def forward_packed(self, weights, batch, int8: bool, per_token: bool, fc1_fp16: bool = False,
-                       x86=False):
+                       x86=False, ffn_bits: int = 32, hidden: bool = False):
         """Restated packed forward. x86=True (or "avx512vnni") runs the
         reference's x86 AVX-512 kernels, per-tensor scales and LinearVnni in
-        W8A8; x86="amx" the same with LinearAmx's row split."""
+        W8A8; x86="amx" the same with LinearAmx's row split. ffn_bits=24
+        rounds fc1's output to 24 bits (per-token W8A8, the GPU's default).
+        hidden=True also returns the hidden states [N + 1, T, d]
+        (ForwardWithHiddenStates' layout)."""
         if x86 and int8 and per_token:
             raise ValueError("the x86 path quantises activations per tensor")
-        m, keep = make_or_model(weights, int8, per_token, fc1_fp16, 2 if x86 == "amx" else int(bool(x86)))
+        m, keep = make_or_model(weights, int8, per_token, fc1_fp16, 2 if x86 == "amx" else int(bool(x86)),
+                                ffn_bits)
         T = batch.total_tokens
-        logits = np.empty((T, weights.cfg.vocab_size), np.float32)
-        rc = self.lib.or_forward_packed(C.byref(m), _p(_c(batch.ids, np.int32)), _p(_c(batch.cu, np.int32)),
-                                        len(batch.cu) - 1, T, _p(logits))
+        cfg = weights.cfg
+        logits = np.empty((T, cfg.vocab_size), np.float32)
+        hs = np.empty((cfg.num_layers + 1, T, cfg.hidden_size), np.float32) if hidden else None
+        rc = self.lib.or_forward_packed_hidden(C.byref(m), _p(_c(batch.ids, np.int32)),
+                                               _p(_c(batch.cu, np.int32)), len(batch.cu) - 1, T, _p(logits),
+                                               _p(hs))
         if rc != 0:
             raise MemoryError("or_forward_packed")
-        return logits
+        return (logits, hs) if hidden else logits
 
 
 class RefLib:

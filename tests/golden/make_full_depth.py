@@ -19,6 +19,9 @@ Arrays (fp32 logits [T, 33] unless noted):
                           W8A16 LinearInt8Ref: several minutes)
   oracle_per_tensor       oracle.c's W8A8 forward (Ref-order kernels, per-tensor scales)
   oracle_per_token        oracle.c's W8A8 forward, per-token scales
+  oracle_per_token_ffn24  the same with fc1's output rounded to 24 bits
+                          (the GPU's default per-token FFN intermediate)
+Arrays already in an existing file are kept; only missing ones are computed.
 The reference's forward is oracle/ref_shim.cpp's ForwardPackedInto sequence
 over the reference's compiled kernels (oracle/_ref/libesmref.so).
 """
@@ -51,20 +54,30 @@ def main():
     from pyoracle import Oracle, RefLib, RefModel
     b = batch()
     w = weights()
-    ref = RefLib(threads=os.cpu_count() or 8)
-    rm = RefModel(ref, w, int8=True)
     out = {"ids": b.ids, "cu": b.cu}
+    if os.path.exists(OUT):
+        with np.load(OUT, allow_pickle=False) as z:
+            assert np.array_equal(z["ids"], b.ids) and np.array_equal(z["cu"], b.cu)
+            out.update({k: z[k] for k in z.files})
+    ref = RefLib(threads=os.cpu_count() or 8)
     isas = ["avx512vnni", "ref"] + (["amx"] if ref.host_isa() == "amx" else [])
-    for isa in isas:
-        os.environ["ESM_FORCE_ISA"] = isa
-        t = time.time()
-        out[f"ref_{'isa_ref' if isa == 'ref' else isa}"] = rm.forward_packed(b)
-        print(f"reference {isa}: {time.time() - t:.1f}s", flush=True)
-    os.environ.pop("ESM_FORCE_ISA", None)
-    rm.free()
+    todo = [isa for isa in isas if f"ref_{'isa_ref' if isa == 'ref' else isa}" not in out]
+    if todo:
+        rm = RefModel(ref, w, int8=True)
+        for isa in todo:
+            os.environ["ESM_FORCE_ISA"] = isa
+            t = time.time()
+            out[f"ref_{'isa_ref' if isa == 'ref' else isa}"] = rm.forward_packed(b)
+            print(f"reference {isa}: {time.time() - t:.1f}s", flush=True)
+        os.environ.pop("ESM_FORCE_ISA", None)
+        rm.free()
     o = Oracle()
-    out["oracle_per_tensor"] = o.forward_packed(w, b, int8=True, per_token=False)
-    out["oracle_per_token"] = o.forward_packed(w, b, int8=True, per_token=True)
+    if "oracle_per_tensor" not in out:
+        out["oracle_per_tensor"] = o.forward_packed(w, b, int8=True, per_token=False)
+    if "oracle_per_token" not in out:
+        out["oracle_per_token"] = o.forward_packed(w, b, int8=True, per_token=True)
+    if "oracle_per_token_ffn24" not in out:
+        out["oracle_per_token_ffn24"] = o.forward_packed(w, b, int8=True, per_token=True, ffn_bits=24)
     np.savez_compressed(OUT, **out)
     print(f"wrote {OUT}: T={b.total_tokens}")
 

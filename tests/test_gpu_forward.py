@@ -65,7 +65,8 @@ def test_w8a8_forward_vs_oracle(dev, oracle, w650_small, small_batch, per_token,
     m = eg.Model(dev, w650_small, int8=True, act_mode=mode, attention_mode=attn)
     got = m.forward_packed(small_batch.ids, small_batch.cu)
     m.free()
-    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token)
+    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token,
+                                  ffn_bits=24 if per_token else 32)
     assert np.all(np.isfinite(got))
     c = corr(got, want)
     agree = float(np.mean(np.argmax(got, 1) == np.argmax(want, 1)))
@@ -294,7 +295,7 @@ def test_config4_uniform_full_forward(dev, oracle):
         m = eg.Model(dev, w2, int8=True, act_mode=mode)
         got = m.forward_packed(batch.ids, batch.cu)
         m.free()
-        want = oracle.forward_packed(w2, batch, int8=True, per_token=per_token)
+        want = oracle.forward_packed(w2, batch, int8=True, per_token=per_token, ffn_bits=24 if per_token else 32)
         c = corr(got, want)
         print(f"uniform 8x256, 2 layers, per_token={per_token}: corr {c:.6f}")
         assert c >= 0.9999, c
@@ -324,7 +325,7 @@ def test_config5_full_workload(dev, oracle):
     m = eg.Model(dev, w1, int8=True, act_mode=eg.ACT_PER_TOKEN)
     got = m.forward_packed(sub.ids, sub.cu)
     m.free()
-    want = oracle.forward_packed(w1, sub, int8=True, per_token=True)
+    want = oracle.forward_packed(w1, sub, int8=True, per_token=True, ffn_bits=24)
     c = corr(got, want)
     print(f"config 5, 1 layer of 3B over lengths {sub.lengths.tolist()}: corr {c:.6f}")
     assert c >= 0.9999, c
@@ -413,7 +414,7 @@ def test_config5_3b_shapes_vs_oracle(dev, oracle, per_token):
     m = eg.Model(dev, w, int8=True, act_mode=mode)
     got = m.forward_packed(batch.ids, batch.cu)
     m.free()
-    want = oracle.forward_packed(w, batch, int8=True, per_token=per_token)
+    want = oracle.forward_packed(w, batch, int8=True, per_token=per_token, ffn_bits=24 if per_token else 32)
     assert np.all(np.isfinite(got))
     c = corr(got, want)
     agree = float(np.mean(np.argmax(got, 1) == np.argmax(want, 1)))
@@ -433,7 +434,8 @@ def test_first_block_fc1_fp16_vs_oracle(dev, oracle, w650_small, small_batch, pe
     m.set_first_block_fc1_fp16(True)
     got = m.forward_packed(small_batch.ids, small_batch.cu)
     m.free()
-    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token, fc1_fp16=True)
+    want = oracle.forward_packed(w650_small, small_batch, int8=True, per_token=per_token, fc1_fp16=True,
+                                  ffn_bits=24 if per_token else 32)
     c = corr(got, want)
     print(f"fc1 fp16 escape per_token={per_token}: corr={c:.6f}")
     assert c >= 0.9999, c
@@ -514,7 +516,7 @@ def test_w8a8_forward_full_depth(dev, full_depth, per_token, attn):
     got = m.forward_packed(data["ids"], data["cu"])
     m.free()
     assert np.all(np.isfinite(got))
-    keys = ["oracle_per_token"] if per_token else ["oracle_per_tensor", "ref_avx512vnni"]
+    keys = ["oracle_per_token_ffn24"] if per_token else ["oracle_per_tensor", "ref_avx512vnni"]
     for key in keys:
         c = corr(got, data[key])
         agree = float(np.mean(got.argmax(1) == data[key].argmax(1)))

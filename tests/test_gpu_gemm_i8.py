@@ -221,3 +221,80 @@ def test_gelu_quantize_act_rejects_bad_shapes(dev):
         dev.gelu_quantize_act(dx, 2, 6, dq, 16, ds)  # K % 4 != 0
     with pytest.raises(eg.Gfx950Error):
         dev.gelu_quantize_act(dx, 2, 8, dq, 4, ds)  # ldq < K
+
+
+def _planes_to_f32(hi, lo):
+    """The 24-bit intermediate's two planes back in column order: stored
+    position 64 g + 2 i + j holds column 64 g + 32 j + i."""
+    M, N = hi.shape
+    bits = (hi.astype(np.uint32) << 16) | (lo.astype(np.uint32) << 8)
+    g = bits.reshape(M, N // 64, 32, 2)           # [.., i, j] at position 2 i + j
+    cols = g.transpose(0, 1, 3, 2).reshape(M, N)  # column 32 j + i
+    return cols.view(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K,ldq", [
+    (8191, 5120, 256, 5120),    # rows < 8192, N <= 5120: two waves per row, odd row count
+    (8193, 5120, 256, 5136),    # rows >= 8192: one wave per row; padded ldq
+    (777, 10240, 256, 10240),   # N > 5120: four waves per row
+    (333, 1280, 1280, 1296),    # narrow rows (N < 5120), the 650M K
+    (65, 2560, 1280, 2560),
+])
+def test_linear_i8_gelu_quant_r24(dev, oracle, M, N, K, ldq):
+    """The default forward's fc1 -> 24-bit intermediate -> GELU + per-token
+    quantisation (esm_gfx950_linear_i8_gelu_quant_r24) against the oracle:
+    the two planes bit-exact against or_round24 of the oracle's dequant
+    (fma(acc, a_scale w_scale, bias), itself bit-exact), and the codes and
+    scales against GeluRef + per-row quantisation of those 24-bit values,
+    with test_gelu_quantize_act's allowance (the device GELU's erf is A&S
+    7.1.26: a byte may differ by one next to a rounding tie). Row 7's
+    activation scale is NaN: its values must stay NaN in the planes."""
+    r = rng(2400 + M + N)
+    A = _i8(r, (M, K))
+    W = _i8(r, (N, K))
+    a_s = r.uniform(0.005, 0.05, size=M).astype(np.float32)
+    w_s = r.uniform(0.005, 0.05, size=N).astype(np.float32)
+    bias = (r.standard_normal(N) * 0.02).astype(np.float32)
+    nan_row = 7
+    a_s_dev = a_s.copy()
+    a_s_dev[nan_row] = np.nan
+    w = dev.weight_i8(W, w_s)
+    dA, da, db = dev.array(A), dev.array(a_s_dev), dev.array(bias)
+    dh, dl = dev.empty((M, N), np.uint16), dev.empty((M, N), np.uint8)
+    dq, ds = dev.array(np.full((M, ldq), 99, np.int8)), dev.empty((M,), np.float32)
+    dev.linear_i8_gelu_quant_r24(dA, K, da, w, db, M, dh, dl, dq, ldq, ds)
+    inter = _planes_to_f32(dh.numpy(), dl.numpy())
+    got, s = dq.numpy(), ds.numpy()
+    w.free()
+
+    acc = _exact_i32(A, W.T.astype(np.float64))
+    want = oracle.round24(oracle.dequant(acc, a_s, w_s, bias))
+    assert np.all(np.isnan(inter[nan_row]))
+    ok = np.arange(M) != nan_row
+    assert np.array_equal(inter[ok].view(np.uint32), want[ok].view(np.uint32))
+
+    g = oracle.gelu(want[ok])
+    q_ref, s_ref = oracle.quant_act_rows(g)
+    np.testing.assert_allclose(s[ok], s_ref, rtol=2e-6)
+    d = got[ok, :N].astype(np.int32) - q_ref
+    assert np.abs(d).max() <= 1
+    prod = g.astype(np.float64) / s_ref.astype(np.float64)[:, None]
+    tie = np.abs(prod - np.floor(prod) - 0.5)
+    assert np.all(tie[d != 0] < 1e-3)
+    assert (d != 0).mean() < 1e-3
+    assert np.all(got[:, N:] == 0)
+
+
+def test_linear_i8_gelu_quant_r24_rejects_bad_shapes(dev):
+    r = rng(5)
+    w = dev.weight_i8(_i8(r, (96, 256)), np.ones(96, np.float32))  # N % 64 != 0
+    dA, da = dev.array(_i8(r, (4, 256))), dev.array(np.ones(4, np.float32))
+    dh, dl = dev.empty((4, 96), np.uint16), dev.empty((4, 96), np.uint8)
+    dq, ds = dev.empty((4, 96), np.int8), dev.empty((4,), np.float32)
+    with pytest.raises(eg.Gfx950Error):
+        dev.linear_i8_gelu_quant_r24(dA, 256, da, w, None, 4, dh, dl, dq, 96, ds)
+    w.free()
+    w = dev.weight_i8(_i8(r, (64, 200)), np.ones(64, np.float32))  # K % 128 != 0
+    with pytest.raises(eg.Gfx950Error):
+        dev.linear_i8_gelu_quant_r24(dA, 208, da, w, None, 4, dh, dl, dq, 64, ds)
+    w.free()

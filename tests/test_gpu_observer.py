@@ -165,8 +165,9 @@ def test_forward_with_observer_w8a8(dev, ref, per_token):
     """Per-tensor mode is the reference's own INT8 arithmetic: percentiles of
     the same positions within 1e-2. Per-token mode quantises activations
     differently from the reference (per row), so it is held to 5e-2. An
-    observed forward samples fc1's fp32 output, so it runs the fp32 FFN
-    intermediate: its logits equal the plain forward's at that width."""
+    observed forward keeps the model's FFN intermediate (per token: 24 bits
+    by default, the observer samples GELU of the values fc2's quantisation
+    reads), so its logits equal the plain forward's at either width."""
     cfg = syn.ESM2_650M.with_layers(2)
     w = syn.make_weights(cfg, seed=20261201 + 4, int8=True, keep_f32_linears=False)
     b = syn.batch_from_lengths([130, 61, 250, 2, 97, 200], seed=7)
@@ -178,8 +179,16 @@ def test_forward_with_observer_w8a8(dev, ref, per_token):
     try:
         logits = m.forward_packed_with_observer(b.ids, b.cu, obs)
         m.set_parts(1)
-        m.set_ffn_intermediate_bits(32)
         assert np.array_equal(logits, m.forward_packed(b.ids, b.cu))
+        if per_token:
+            m.set_ffn_intermediate_bits(32)
+            other = eg.ActivationObserver(dev)
+            try:
+                wide = m.forward_packed_with_observer(b.ids, b.cu, other)
+            finally:
+                other.free()
+            assert np.array_equal(wide, m.forward_packed(b.ids, b.cu))
+            assert not np.array_equal(wide, logits)
         rm.forward_packed(b, theirs)
         sites = _sites(cfg.num_layers)
         assert obs.sites() == sites
