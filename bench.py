@@ -14,13 +14,19 @@ Extra records (same JSON line, "workloads"): config 4's uniform 8x256 batch
 and config 5 (ESM-2 3B, 36 layers, 64 sequences of log-uniform 50..1024
 tokens), each with residues/s and its dominant GEMM's roofline.
 
-cpu_baseline: the reference's own CPU path (its kernels compiled from source
-into oracle/_ref/libesmref.so, driven in ForwardPackedInto order) on a
-bounded sample of the same batch, timed on this host with the reference's
-protocol (python/esm_cpp/bench/compare.py:172-191: 2 warmup + 5 timed runs,
-p50 and mean), both ForwardPacked and ForwardScheduled (PlanBatches groups).
+A third record times the x86-exact numerics (ESM_GFX950_NUMERICS_X86_AVX512,
+or _X86_AMX on an AMX host) on the headline batch: the mode whose logits
+equal the reference CPU path's bit for bit.
 
-parity: on that sample, the GPU in x86-exact numerics against the CPU run
+cpu_baseline: the reference's own CPU path (its kernels compiled from source
+into oracle/_ref/libesmref.so, driven in ForwardPackedInto order) on the
+identical packed batch (all 256 sequences by default), timed on this host
+with the reference's protocol (python/esm_cpp/bench/compare.py:172-191:
+warmup runs, then timed runs, p50 and mean; 1 + 3 by default instead of
+compare.py's 2 + 5, which would hold the GPU box two minutes for the CPU
+alone), both ForwardPacked and ForwardScheduled (PlanBatches groups).
+
+parity: on that batch, the GPU in x86-exact numerics against the CPU run
 (bit for bit), the GPU's per-tensor mode against it; and on the committed
 33-layer fixture (tests/golden/full_depth_650m.npz) the GPU's default modes
 against the oracle and the reference, next to the reference's own spread.
@@ -172,6 +178,25 @@ def roofline_of(sites, T, cfg, batch, workload, per_token=True):
     return r
 
 
+def x86_workload(dev, weights, batch, cfg, isa, args):
+    """The x86-exact numerics (logits equal to the reference CPU path's on an
+    `isa` host) on the headline batch: residues/s and per-site kernel times."""
+    numerics = eg.NUMERICS_X86_AMX if isa == "amx" else eg.NUMERICS_X86_AVX512
+    model = eg.Model(dev, weights, int8=True, act_mode=eg.ACT_PER_TENSOR)
+    try:
+        model.set_numerics(numerics)
+        ms, _, sites, used = measure(dev, model, batch, cfg, args.extra_steps, 1, 1)
+    finally:
+        model.free()
+    T = batch.total_tokens
+    return {"workload": f"x86-exact: config4 varlen, ESM-2-650M W8A8, numerics "
+                        f"{'X86_AMX' if numerics == eg.NUMERICS_X86_AMX else 'X86_AVX512'} (per-tensor activation "
+                        f"scales; logits equal the reference's {isa} CPU forward bit for bit)",
+            "tokens": T, "residues": batch.residues, "sequences": int(len(batch.lengths)),
+            "ms_per_step": round(ms, 3), "value": round(batch.residues / (ms * 1e-3), 1), "unit": "residues/s",
+            "tokens_per_s": round(T / (ms * 1e-3), 1), "streams": used, "kernel_sites": sites}
+
+
 def extra_workload(dev, name, cfg, weights, batch, args):
     model = eg.Model(dev, weights, int8=True, act_mode=eg.ACT_PER_TOKEN)
     try:
@@ -232,8 +257,9 @@ def cpu_baseline(weights, batch, dev, args):
     cpu = host_cpu()
     threads = max(1, min(cpu.get("affinity_cpus") or cpu["hardware_concurrency"] or 1, args.cpu_threads))
     ref = RefLib(threads=threads)
-    idx = list(range(0, len(batch.lengths), max(1, len(batch.lengths) // args.cpu_seqs)))[: args.cpu_seqs]
-    sample = batch.subset(idx)
+    nseq = len(batch.lengths) if args.cpu_seqs <= 0 else min(args.cpu_seqs, len(batch.lengths))
+    idx = list(range(0, len(batch.lengths), max(1, len(batch.lengths) // nseq)))[:nseq]
+    sample = batch if nseq == len(batch.lengths) else batch.subset(idx)
     rm = RefModel(ref, weights, int8=True)
     isa = ref.isa()
     log(f"cpu: isa={isa} threads={threads} host={cpu}")
@@ -298,7 +324,8 @@ def parity(dev, weights, sample, cpu_logits, isa):
         ids, cu = fx["ids"], fx["cu"]
         res = {"batch": f"{len(cu) - 1} sequences, {int(cu[-1])} tokens, 33 layers (tests/golden/full_depth_650m.npz)"}
         for name, mode, numerics_, key in (
-                ("per_token_vs_oracle", eg.ACT_PER_TOKEN, eg.NUMERICS_DEFAULT, "oracle_per_token"),
+                ("per_token_vs_oracle_ffn24", eg.ACT_PER_TOKEN, eg.NUMERICS_DEFAULT, "oracle_per_token_ffn24"),
+                ("per_token_vs_oracle_fp32_intermediate", eg.ACT_PER_TOKEN, eg.NUMERICS_DEFAULT, "oracle_per_token"),
                 ("per_tensor_vs_oracle", eg.ACT_PER_TENSOR, eg.NUMERICS_DEFAULT, "oracle_per_tensor"),
                 ("per_tensor_vs_reference_avx512vnni", eg.ACT_PER_TENSOR, eg.NUMERICS_DEFAULT, "ref_avx512vnni"),
                 ("x86_avx512_vs_reference_avx512vnni", eg.ACT_PER_TENSOR, eg.NUMERICS_X86_AVX512, "ref_avx512vnni"),
@@ -332,9 +359,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the uniform and config-5 records")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--extra-steps", type=int, default=5)
-    ap.add_argument("--cpu-seqs", type=int, default=64)
-    ap.add_argument("--cpu-warmup", type=int, default=2)
-    ap.add_argument("--cpu-iters", type=int, default=5)
+    ap.add_argument("--cpu-seqs", type=int, default=0, help="sequences in the CPU baseline (0: the whole batch)")
+    ap.add_argument("--cpu-warmup", type=int, default=1)
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--no-x86", action="store_true", help="skip the x86-exact numerics record")
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--parts", type=int, default=0,
                     help="concurrent sequence groups (streams) in the throughput pass; 0 = the library's "
@@ -379,6 +407,12 @@ def main():
     sample = cpu_logits = isa = None
     if not args.no_cpu_baseline and rank == 0:
         cpu, sample, cpu_logits, isa = cpu_baseline(weights, batch, dev, args)
+    if not args.no_x86 and args.workload == "varlen":
+        x86 = x86_workload(dev, weights, batch, cfg, isa or "avx512vnni", args)
+        if cpu and cpu["sample"].startswith(f"{len(batch.lengths)} of {len(batch.lengths)}"):
+            x86["gpu_over_cpu"] = round(x86["value"] / cpu["value"], 1)
+        workloads.append(x86)
+        log(f"extra {x86['workload']}: {x86['ms_per_step']} ms")
     if not args.no_parity and rank == 0:
         par = parity(dev, weights, sample, cpu_logits, isa or "avx512vnni")
     dev.close()

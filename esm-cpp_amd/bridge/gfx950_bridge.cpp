@@ -1,6 +1,7 @@
 // Reference-side bridge to the gfx950 backend (see gfx950_bridge.h). Host
 // code only: it includes the reference's headers and calls the C ABI of
-// libesm_gfx950.so; it links nothing of the reference.
+// libesm_gfx950.so. Its one reference dependency is BatchView's
+// constructor (src/batch.cpp), which the library it lives in already holds.
 #include "gfx950_bridge.h"
 
 #include <algorithm>
@@ -75,6 +76,7 @@ struct DevWeight {
   const std::int8_t* data = nullptr;
   int N = 0, K = 0;
   std::uint64_t scale_sum = 0;
+  std::uint64_t value_sum = 0;
 };
 
 // FNV-1a over the scales' bytes: N floats, cheap next to any call's staging.
@@ -84,12 +86,26 @@ std::uint64_t scale_checksum(const esm::quant::QuantizedTensor& W) {
   for (std::size_t i = 0; i < W.per_channel_scales.size() * sizeof(float); ++i) h = (h ^ b[i]) * 1099511628211ull;
   return h;
 }
+// FNV-1a over 4096 int8 values spread evenly over the tensor (all of them
+// when it has fewer) and its size: a rewrite in place of more than a few
+// values changes it.
+std::uint64_t value_checksum(const esm::quant::QuantizedTensor& W) {
+  constexpr std::size_t kSamples = 4096;
+  const std::size_t n = W.packed.size();
+  std::uint64_t h = 1469598103934665603ull ^ n;
+  const std::size_t step = n > kSamples ? n / kSamples : 1;
+  for (std::size_t i = 0; i < n; i += step)
+    h = (h ^ static_cast<unsigned char>(W.packed[i])) * 1099511628211ull;
+  return h;
+}
+
 std::unordered_map<const esm::quant::QuantizedTensor*, DevWeight> g_weights;
 
 esm_gfx950_weight* device_weight(const esm::quant::QuantizedTensor& W) {
   DevWeight& e = g_weights[&W];
-  const std::uint64_t sum = scale_checksum(W);
-  if (e.w && e.data == W.packed.data() && e.N == W.N && e.K == W.K && e.scale_sum == sum) return e.w;
+  const std::uint64_t sum = scale_checksum(W), vsum = value_checksum(W);
+  if (e.w && e.data == W.packed.data() && e.N == W.N && e.K == W.K && e.scale_sum == sum && e.value_sum == vsum)
+    return e.w;
   if (e.w) esm_gfx950_weight_free(Ctx(), e.w);
   e = DevWeight();
   if (static_cast<std::size_t>(W.N) * W.K != W.packed.size() ||
@@ -107,6 +123,7 @@ esm_gfx950_weight* device_weight(const esm::quant::QuantizedTensor& W) {
   e.N = W.N;
   e.K = W.K;
   e.scale_sum = sum;
+  e.value_sum = vsum;
   return e.w;
 }
 
@@ -251,6 +268,135 @@ bool AttentionVarlen(const float* q, const float* k, const float* v, const int* 
                                         static_cast<const float*>(dv), cu_seqlens, batch_size, num_heads, head_dim,
                                         static_cast<float*>(dy), precision)) &&
          download(out, dy, n);
+}
+
+namespace {
+
+// The model's vocabulary and layer count, read back from the library.
+bool model_dims(esm_gfx950_model* model, int* vocab, int* layers, int* hidden) {
+  esm_gfx950_model_config c;
+  if (esm_gfx950_model_get_config(model, &c) != ESM_GFX950_OK) {
+    g_error = "model_get_config failed";
+    return false;
+  }
+  *vocab = c.vocab_size;
+  *layers = c.num_layers;
+  *hidden = c.hidden_size;
+  return true;
+}
+
+}  // namespace
+
+bool ForwardPacked(esm_gfx950_model* model, const esm::BatchView& batch,
+                   std::vector<std::vector<float>>* logits_per_seq_out,
+                   std::vector<std::vector<float>>* hidden_packed_out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!Ctx()) return false;
+  if (!model) {
+    g_error = "ForwardPacked: null model";
+    return false;
+  }
+  const int T = static_cast<int>(batch.total_tokens());
+  const int B = batch.batch_size;
+  if (T == 0) {
+    if (logits_per_seq_out) logits_per_seq_out->clear();
+    if (hidden_packed_out) hidden_packed_out->clear();
+    return true;
+  }
+  int V = 0, layers = 0, d = 0;
+  if (!model_dims(model, &V, &layers, &d)) return false;
+  const std::int32_t* masks = batch.packed_masks.empty() ? nullptr : batch.packed_masks.data();
+  std::vector<float> packed(static_cast<std::size_t>(T) * V);
+  if (hidden_packed_out) {
+    std::vector<float> hidden(static_cast<std::size_t>(layers + 1) * T * d);
+    if (!ok(esm_gfx950_forward_hidden_states(Ctx(), model, batch.packed_ids.data(), masks, batch.cu_seqlens.data(),
+                                             B, T, packed.data(), hidden.data())))
+      return false;
+    const std::size_t Td = static_cast<std::size_t>(T) * d;
+    hidden_packed_out->assign(static_cast<std::size_t>(layers + 1), {});
+    for (int l = 0; l <= layers; ++l)
+      (*hidden_packed_out)[l].assign(hidden.begin() + l * Td, hidden.begin() + (l + 1) * Td);
+  } else if (!ok(esm_gfx950_forward_packed_masked(Ctx(), model, batch.packed_ids.data(), masks,
+                                                  batch.cu_seqlens.data(), B, T, packed.data(), 0))) {
+    return false;
+  }
+  if (logits_per_seq_out) {
+    // The per-sequence split of model.cpp:1240-1252.
+    logits_per_seq_out->resize(static_cast<std::size_t>(B));
+    for (int b = 0; b < B; ++b) {
+      const std::size_t start = static_cast<std::size_t>(batch.cu_seqlens[b]) * V;
+      const std::size_t n = static_cast<std::size_t>(batch.sequence_length(b)) * V;
+      (*logits_per_seq_out)[b].assign(packed.begin() + start, packed.begin() + start + n);
+    }
+  }
+  return true;
+}
+
+bool ForwardScheduled(esm_gfx950_model* model, const std::vector<std::vector<std::int32_t>>& input_ids,
+                      const std::vector<std::vector<std::int32_t>>& attention_masks,
+                      const esm::SchedulerConfig& cfg, std::vector<std::vector<float>>* out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!Ctx()) return false;
+  out->clear();
+  const std::size_t N = input_ids.size();
+  if (N == 0) return true;
+  if (!model) {
+    g_error = "ForwardScheduled: null model";
+    return false;
+  }
+  if (!attention_masks.empty() && attention_masks.size() != N) {
+    g_error = "attention_masks/input_ids batch size mismatch";
+    return false;
+  }
+  int V = 0, layers = 0, d = 0;
+  if (!model_dims(model, &V, &layers, &d)) return false;
+  out->resize(N);
+  std::vector<std::int32_t> lens(N);
+  for (std::size_t i = 0; i < N; ++i) {
+    lens[i] = static_cast<std::int32_t>(input_ids[i].size());
+    (*out)[i].resize(input_ids[i].size() * static_cast<std::size_t>(V));
+  }
+  if (attention_masks.empty()) {
+    std::vector<const std::int32_t*> ids(N);
+    std::vector<float*> outs(N);
+    for (std::size_t i = 0; i < N; ++i) {
+      ids[i] = input_ids[i].data();
+      outs[i] = (*out)[i].data();
+    }
+    return ok(esm_gfx950_forward_scheduled(Ctx(), model, ids.data(), lens.data(), static_cast<int>(N),
+                                           cfg.imbalance_threshold, cfg.max_batch_size, outs.data()));
+  }
+  // With masks: the plan of PlanBatches, each group one masked packed forward.
+  for (std::size_t i = 0; i < N; ++i)
+    if (attention_masks[i].size() != input_ids[i].size()) {
+      g_error = "attention_masks[" + std::to_string(i) + "] does not match input_ids";
+      return false;
+    }
+  std::vector<std::int32_t> order(N), sizes(N);
+  int groups = 0;
+  if (!ok(esm_gfx950_plan_batches(lens.data(), static_cast<int>(N), cfg.imbalance_threshold, cfg.max_batch_size,
+                                  order.data(), sizes.data(), &groups)))
+    return false;
+  std::size_t at = 0;
+  for (int g = 0; g < groups; ++g) {
+    std::vector<std::int32_t> ids, masks, cu{0};
+    const std::size_t first = at;
+    for (int k = 0; k < sizes[g]; ++k, ++at) {
+      const std::size_t i = static_cast<std::size_t>(order[at]);
+      ids.insert(ids.end(), input_ids[i].begin(), input_ids[i].end());
+      masks.insert(masks.end(), attention_masks[i].begin(), attention_masks[i].end());
+      cu.push_back(static_cast<std::int32_t>(ids.size()));
+    }
+    if (sizes[g] == 0 || ids.empty()) continue;
+    std::vector<float> packed(ids.size() * static_cast<std::size_t>(V));
+    if (!ok(esm_gfx950_forward_packed_masked(Ctx(), model, ids.data(), masks.data(), cu.data(), sizes[g],
+                                             static_cast<int>(ids.size()), packed.data(), 0)))
+      return false;
+    for (int k = 0; k < sizes[g]; ++k)
+      std::copy(packed.begin() + static_cast<std::size_t>(cu[k]) * V,
+                packed.begin() + static_cast<std::size_t>(cu[k + 1]) * V, (*out)[order[first + k]].begin());
+  }
+  return true;
 }
 
 }  // namespace esm::gfx950

@@ -21,8 +21,12 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
+#include <vector>
 
+#include "esm_cpp/batch.h"
 #include "esm_cpp/quant.h"
+#include "esm_cpp/scheduler.h"
 #include "esm_gfx950.h"
 
 namespace esm::gfx950 {
@@ -41,10 +45,12 @@ bool Linear(const float* A, const float* W, const float* bias, float* C, int M, 
 // reference's dynamic per-tensor activation scale. The weight's device copy
 // is built on first use (BuildKernelCache's role, pack.cpp:107-117) and kept
 // until ReleaseWeight or exit. It is found again by the tensor's address and
-// checked against its packed data pointer, shape and scales; a tensor whose
-// int8 values change in place keeps its old device copy, so call
-// ReleaseWeight before changing or destroying a tensor (the integration that
-// owns QuantizedTensor frees the copy in its destructor).
+// checked against its packed data pointer, shape, a checksum of its scales
+// and a checksum of 4096 of its int8 values spread evenly over the tensor;
+// a change in place that none of these sees (a few int8 values rewritten)
+// keeps the old device copy, so call ReleaseWeight after changing a tensor in
+// place and before destroying it (the integration that owns QuantizedTensor
+// frees the copy in its destructor).
 bool LinearInt8(const float* A, const esm::quant::QuantizedTensor& W, const float* bias, float* C, int M, int N,
                 int K);
 void ReleaseWeight(const esm::quant::QuantizedTensor& W);
@@ -70,5 +76,28 @@ bool RopeApplyVarlen(float* x, const float* cos, const float* sin, const int* cu
 // other head_dim <= 128.
 bool AttentionVarlen(const float* q, const float* k, const float* v, const int* cu_seqlens, int batch_size,
                      int num_heads, int head_dim, float* out);
+
+// Model::ForwardPackedInto's device path (model.cpp:1093-1255) for a model
+// built on the device (esm_gfx950_model_create from the Model's tensors, or
+// esm_gfx950_model_create_from_gguf): the packed forward of `batch`, masks
+// included (pads: esm_gfx950_forward_packed_masked), split into one logits
+// buffer per sequence, each [L_b * vocab_size], as model.cpp:1240-1252 does.
+// hidden_packed_out (nullable) receives num_hidden_layers + 1 packed [T, d]
+// states in ForwardPackedInto's layout (:1149-1189). An empty batch clears
+// logits_per_seq_out. Returns false when the device call fails.
+bool ForwardPacked(esm_gfx950_model* model, const esm::BatchView& batch,
+                   std::vector<std::vector<float>>* logits_per_seq_out,
+                   std::vector<std::vector<float>>* hidden_packed_out = nullptr);
+
+// Model::ForwardScheduled's device path (model.cpp:1298-1421): the
+// sequences planned as PlanBatches does (scheduler.cpp:54-75) and returned
+// in input order, one [L_i * vocab_size] buffer each. Without masks the
+// library runs the groups pipelined (esm_gfx950_forward_scheduled); with
+// masks (attention_masks.size() == input_ids.size()) each planned group runs
+// as one masked packed forward. Returns false when the device call fails or
+// the mask list does not match (the reference throws; the caller decides).
+bool ForwardScheduled(esm_gfx950_model* model, const std::vector<std::vector<std::int32_t>>& input_ids,
+                      const std::vector<std::vector<std::int32_t>>& attention_masks,
+                      const esm::SchedulerConfig& cfg, std::vector<std::vector<float>>* out);
 
 }  // namespace esm::gfx950

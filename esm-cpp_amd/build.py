@@ -69,9 +69,13 @@ def build_bridge(reference_include: str) -> str:
     """Builds lib/libesm_gfx950_bridge.so: the reference-side bridge
     (bridge/), compiled with the host compiler against the reference's own
     headers (reference_include = <esm.cpp>/include) and linked to
-    libesm_gfx950.so only. Needs build() first."""
+    libesm_gfx950.so. The reference's src/batch.cpp (BatchView's validating
+    constructor, which the forward-level arm takes) is compiled in from the
+    reference tree, where it lies, as the library the bridge joins in the
+    reference's own build already holds it. Needs build() first."""
     cxx = os.environ.get("CXX", "g++")
     srcs = [os.path.join(HERE, "bridge", f) for f in BRIDGE_SOURCES]
+    srcs.append(os.path.join(os.path.dirname(os.path.abspath(reference_include)), "src", "batch.cpp"))
     tmp = BRIDGE_LIB + ".tmp"
     cmd = [cxx, "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{reference_include}", f"-I{INCLUDE}",
            *srcs, f"-L{LIBDIR}", "-lesm_gfx950", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib", "-o", tmp]

@@ -43,30 +43,22 @@ int pad16(int k) { return (k + 15) & ~15; }
 // LinearInt8): the quantised activations, their scales and one absmax
 // scalar. Every GPU the library runs on holds its own copy until the
 // process ends. In host code `scratch` names a host-side stand-in, not device
-// memory: its device address is taken once per device at esm_gfx950_init
-// (hipGetSymbolAddress, that device current) and only that address is used.
+// memory: its device address is taken at every esm_gfx950_init
+// (hipGetSymbolAddress, that device current), kept in the context, and only
+// that address is used. Taking it per context rather than once per process
+// keeps it right after a hipDeviceReset, which may reload the code object.
 constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;
 static __device__ __align__(256) int8_t scratch[kNoAllocScratchBytes];
 
 namespace {
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device
-
-// The device address of `scratch` on `device` (the current device), taken
-// on the first call for that device.
-hipError_t scratch_address(int device, void** out) {
+// The device address of `scratch` on the current device.
+hipError_t scratch_address(void** out) {
   *out = nullptr;
-  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lk(g_scratch_mu);
-  if (!g_scratch_addr[device]) {
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) return e;
-    if (!p) return hipErrorInvalidSymbol;
-    g_scratch_addr[device] = p;
-  }
-  *out = g_scratch_addr[device];
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  *out = p;
   return hipSuccess;
 }
 }  // namespace
@@ -287,7 +279,7 @@ extern "C" int esm_gfx950_init(int device, esm_gfx950_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ESM_GFX950_HIP_ERROR;
   if (hipSetDevice(device) != hipSuccess) return ESM_GFX950_HIP_ERROR;
   void* noalloc = nullptr;
-  if (scratch_address(device, &noalloc) != hipSuccess) return ESM_GFX950_HIP_ERROR;
+  if (scratch_address(&noalloc) != hipSuccess) return ESM_GFX950_HIP_ERROR;
   auto* ctx = new esm_gfx950_ctx();
   ctx->device = device;
   ctx->noalloc_scratch = noalloc;
@@ -1951,9 +1943,9 @@ struct StreamScope {
 };
 
 // Stages one part: sequences [b0, b0 + B) of the packed batch, tokens
-// [cu[b0], cu[b0 + B]).
+// [cu[b0], cu[b0 + B]). masks (nullable, packed like ids): 0 marks a pad.
 int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part& P, const int32_t* ids,
-               const int32_t* cu, int b0, int B) {
+               const int32_t* masks, const int32_t* cu, int b0, int B) {
   const auto& c = m->cfg;
   const int H = c.num_heads, dh = c.head_dim;
   const int t0 = cu[b0];
@@ -1986,21 +1978,24 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
   }
   const Meta mh = meta_layout(P.cap_T, P.cap_B, P.cap_L, H, dh, static_cast<char*>(P.meta_host));
 
-  // Host metadata: ids, per-token embedding scale (Embed, model.cpp:737-778),
+  // Host metadata: ids, per-token embedding scale (Embed, model.cpp:737-778:
+  // real tokens counted by the mask, mask tokens counted over every token;
+  // a pad's scale is 0, which the embedding kernel turns into a zero row),
   // positions, cu_seqlens (rebased to the part), attention work list, rope
   // tables.
   ESM_HIP(ctx, hipEventSynchronize(P.meta_done));
   std::memcpy(mh.ids, ids + t0, static_cast<size_t>(T) * 4);
   for (int b = 0; b <= B; ++b) mh.cu[b] = cu[b0 + b] - t0;
+  const int32_t* mk = masks ? masks + t0 : nullptr;
   for (int b = 0; b < B; ++b) {
-    int src_len = 0, masks = 0;
+    int src_len = 0, mask_tokens = 0;
     for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) {
-      ++src_len;
-      if (mh.ids[t] == c.mask_token_id) ++masks;
+      if (!mk || mk[t] != 0) ++src_len;
+      if (mh.ids[t] == c.mask_token_id) ++mask_tokens;
     }
-    const float ratio = src_len > 0 ? static_cast<float>(masks) / static_cast<float>(src_len) : 0.0f;
+    const float ratio = src_len > 0 ? static_cast<float>(mask_tokens) / static_cast<float>(src_len) : 0.0f;
     const float scale = (1.0f - kTokenDropoutMaskRatioTrain) / std::max(1.0f - ratio, 1e-12f);
-    for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) mh.tok_scale[t] = scale;
+    for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) mh.tok_scale[t] = (mk && mk[t] == 0) ? 0.0f : scale;
   }
   build_pos(mh.cu, B, mh.pos);
   const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
@@ -2166,6 +2161,12 @@ int forward_part(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const esm_gfx95
 
 }  // namespace
 
+extern "C" int esm_gfx950_model_get_config(const esm_gfx950_model* m, esm_gfx950_model_config* out) {
+  if (!m || !out) return ESM_GFX950_INVALID_ARGUMENT;
+  *out = m->cfg;
+  return ESM_GFX950_OK;
+}
+
 extern "C" int esm_gfx950_model_staged_parts(const esm_gfx950_model* m, int* parts) {
   if (!m || !parts) return ESM_GFX950_INVALID_ARGUMENT;
   int n = 0;
@@ -2209,7 +2210,7 @@ int auto_part_count(const esm_gfx950_model_config& c, int T) {
 
 // Validates and stages a packed batch in at most max_parts sequence groups.
 int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, const int32_t* cu, int B, int T,
-                int max_parts) {
+                int max_parts, const int32_t* masks = nullptr) {
   ESM_TRY(validate_batch(ctx, cu, B, T));
   m->staged_T = 0;
   for (auto& p : m->parts) p.T = p.B = 0;
@@ -2232,7 +2233,7 @@ int stage_batch(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids, co
     const long target = static_cast<long>(T) * (p + 1) / np;
     while (b1 < B - (np - 1 - p) && cu[b1] < target) ++b1;
     if (p == np - 1) b1 = B;
-    ESM_TRY(stage_part(ctx, m, m->parts[p], ids, cu, b0, b1 - b0));
+    ESM_TRY(stage_part(ctx, m, m->parts[p], ids, masks, cu, b0, b1 - b0));
     b0 = b1;
   }
   m->staged_T = T;
@@ -2268,6 +2269,12 @@ extern "C" int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* m,
   return stage_batch(ctx, m, ids, cu, B, T, static_cast<int>(m->parts.size()));
 }
 
+extern "C" int esm_gfx950_batch_upload_masked(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                              const int32_t* masks, const int32_t* cu, int B, int T) {
+  if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
+  return stage_batch(ctx, m, ids, cu, B, T, static_cast<int>(m->parts.size()), masks);
+}
+
 extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* m, float* logits) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
   if (m->staged_T == 0) return ESM_GFX950_OK;
@@ -2293,8 +2300,14 @@ extern "C" int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* 
 
 extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
                                          const int32_t* cu, int B, int T, float* logits, int logits_on_device) {
+  return esm_gfx950_forward_packed_masked(ctx, m, ids, nullptr, cu, B, T, logits, logits_on_device);
+}
+
+extern "C" int esm_gfx950_forward_packed_masked(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
+                                                const int32_t* masks, const int32_t* cu, int B, int T,
+                                                float* logits, int logits_on_device) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
-  ESM_TRY(esm_gfx950_batch_upload(ctx, m, ids, cu, B, T));
+  ESM_TRY(esm_gfx950_batch_upload_masked(ctx, m, ids, masks, cu, B, T));
   if (T == 0) return ESM_GFX950_OK;
   ESM_REQUIRE(ctx, logits, "forward_packed: null logits");
   if (logits_on_device) return esm_gfx950_forward_device(ctx, m, logits);
@@ -2323,9 +2336,10 @@ extern "C" int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* 
 }
 
 extern "C" int esm_gfx950_forward_hidden_states(esm_gfx950_ctx* ctx, esm_gfx950_model* m, const int32_t* ids,
-                                                const int32_t* cu, int B, int T, float* logits, float* hidden) {
+                                                const int32_t* masks, const int32_t* cu, int B, int T, float* logits,
+                                                float* hidden) {
   if (!ctx || !m) return ESM_GFX950_INVALID_ARGUMENT;
-  ESM_TRY(esm_gfx950_batch_upload(ctx, m, ids, cu, B, T));
+  ESM_TRY(esm_gfx950_batch_upload_masked(ctx, m, ids, masks, cu, B, T));
   if (T == 0) return ESM_GFX950_OK;
   ESM_REQUIRE(ctx, logits && hidden, "forward_hidden_states: null logits or hidden");
   const int V = m->cfg.vocab_size, d = m->cfg.hidden_size;

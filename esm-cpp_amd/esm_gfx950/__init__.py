@@ -56,7 +56,8 @@ EXPORTED = [
     "esm_gfx950_expf_glibc", "esm_gfx950_linear_f32_avx512", "esm_gfx950_rope_apply_varlen_avx512",
     "esm_gfx950_attention_varlen_avx512", "esm_gfx950_model_set_numerics", "esm_gfx950_linear_i8_noalloc",
     "esm_gfx950_model_set_ffn_intermediate_bits", "esm_gfx950_linear_i8_gelu_quant_r24",
-    "esm_gfx950_forward_hidden_states",
+    "esm_gfx950_forward_hidden_states", "esm_gfx950_forward_packed_masked", "esm_gfx950_batch_upload_masked",
+    "esm_gfx950_model_get_config",
 ]
 
 
@@ -100,7 +101,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "esm_gfx950_quantize_act": (i32, [vp, vp, i32, i32, i32, vp, i32, vp]),
         "esm_gfx950_gelu_quantize_act": (i32, [vp, vp, i32, i32, vp, i32, vp]),
         "esm_gfx950_linear_i8_gelu_quant_r24": (i32, [vp, vp, i32, vp, vp, vp, i32, vp, vp, vp, i32, vp]),
-        "esm_gfx950_forward_hidden_states": (i32, [vp, vp, vp, vp, i32, i32, vp, vp]),
+        "esm_gfx950_forward_hidden_states": (i32, [vp, vp, vp, vp, vp, i32, i32, vp, vp]),
+        "esm_gfx950_forward_packed_masked": (i32, [vp, vp, vp, vp, vp, i32, i32, vp, i32]),
+        "esm_gfx950_batch_upload_masked": (i32, [vp, vp, vp, vp, vp, i32, i32]),
         "esm_gfx950_set_gemm_tile_rows": (i32, [i32]),
         "esm_gfx950_set_gemm_split_k": (i32, [i32]),
         "esm_gfx950_model_set_lm_dense_split": (i32, [vp, vp, i32]),
@@ -610,18 +613,38 @@ class Model:
                                                                len(cu) - 1, T, out.ptr, 1))
         return out
 
-    def forward_hidden_states(self, ids: np.ndarray, cu: np.ndarray):
+    def forward_hidden_states(self, ids: np.ndarray, cu: np.ndarray, masks: Optional[np.ndarray] = None):
         """Packed forward returning (logits [T, vocab], hidden [layers + 1, T, d]):
         post-embed, each layer's output, and the post-final-LN state last
-        (reference Model::ForwardWithHiddenStates, esm_gfx950_forward_hidden_states)."""
+        (reference Model::ForwardWithHiddenStates, esm_gfx950_forward_hidden_states).
+        masks: int32 [T], 0 marks a pad (None: every token real)."""
         ids = np.ascontiguousarray(ids, np.int32)
         cu = np.ascontiguousarray(cu, np.int32)
+        mk = None if masks is None else np.ascontiguousarray(masks, np.int32)
         T = int(ids.shape[0])
+        if mk is not None and mk.shape != ids.shape:
+            raise ValueError("masks must match ids")
         logits = np.empty((T, self.cfg.vocab_size), np.float32)
         hidden = np.empty((self.cfg.num_layers + 1, T, self.cfg.hidden_size), np.float32)
         self.dev._check(self.dev.lib.esm_gfx950_forward_hidden_states(
-            self.dev.ctx, self.handle, _ptr(ids), _ptr(cu), len(cu) - 1, T, _ptr(logits), _ptr(hidden)))
+            self.dev.ctx, self.handle, _ptr(ids), _ptr(mk) if mk is not None else None, _ptr(cu), len(cu) - 1, T,
+            _ptr(logits), _ptr(hidden)))
         return logits, hidden
+
+    def forward_packed_masked(self, ids: np.ndarray, masks: Optional[np.ndarray], cu: np.ndarray):
+        """Packed forward with BatchView's pad masks (int32 [T], 0 = pad; None:
+        every token real); host logits [T, vocab] (esm_gfx950_forward_packed_masked)."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        cu = np.ascontiguousarray(cu, np.int32)
+        mk = None if masks is None else np.ascontiguousarray(masks, np.int32)
+        if mk is not None and mk.shape != ids.shape:
+            raise ValueError("masks must match ids")
+        T = int(ids.shape[0])
+        logits = np.empty((T, self.cfg.vocab_size), np.float32)
+        self.dev._check(self.dev.lib.esm_gfx950_forward_packed_masked(
+            self.dev.ctx, self.handle, _ptr(ids), _ptr(mk) if mk is not None else None, _ptr(cu), len(cu) - 1, T,
+            _ptr(logits), 0))
+        return logits
 
     def forward_packed_with_observer(self, ids: np.ndarray, cu: np.ndarray, observer: "ActivationObserver"):
         """Packed forward that also feeds `observer` at the reference's four

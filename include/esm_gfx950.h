@@ -396,8 +396,8 @@ int esm_gfx950_model_set_numerics(esm_gfx950_ctx* ctx, esm_gfx950_model* model, 
 int esm_gfx950_model_set_act_mode(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int act_mode);
 
 /* Packed forward. ids [T] and cu_seqlens [batch_size + 1] are HOST arrays
- * validated like BatchView (batch.cpp:8-46); masks are not supported (all
- * tokens real). logits fp32 [T, vocab] is written to DEVICE memory when
+ * validated like BatchView (batch.cpp:8-46); every token is real (pads:
+ * esm_gfx950_forward_packed_masked). logits fp32 [T, vocab] is written to DEVICE memory when
  * logits_on_device != 0, else to HOST memory (the call then synchronises).
  * Equivalent to esm_gfx950_batch_upload + esm_gfx950_forward_device.
  * The device arena grows only when T exceeds every earlier batch. */
@@ -406,7 +406,8 @@ int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* model, cons
                               float* logits, int logits_on_device);
 /* Model::ForwardWithHiddenStates / ForwardPackedInto's hidden_packed_out
  * (include/esm_cpp/model.h:184-191, src/model.cpp:1149-1189): the packed
- * forward of esm_gfx950_forward_packed with HOST ids, cu_seqlens and logits
+ * forward of esm_gfx950_forward_packed_masked with HOST ids, masks (or NULL),
+ * cu_seqlens and logits
  * [T, vocab], that also writes every hidden state to HOST hidden
  * [num_layers + 1, T, hidden_size]: [0] after the embedding, [i] after layer
  * i, and [num_layers] the post-final-LayerNorm state in place of the last
@@ -414,13 +415,27 @@ int esm_gfx950_forward_packed(esm_gfx950_ctx* ctx, esm_gfx950_model* model, cons
  * add fc2's output into the hidden state in its GEMM; split-K partial sums
  * are not carried across a layer boundary in this call). Synchronises. */
 int esm_gfx950_forward_hidden_states(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
-                                     const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
-                                     float* hidden);
+                                     const int32_t* masks, const int32_t* cu_seqlens, int batch_size,
+                                     int total_tokens, float* logits, float* hidden);
+/* esm_gfx950_forward_packed with BatchView's packed_masks (batch.h:16-36):
+ * masks HOST int32 [T] or NULL (every token real); a 0 marks a pad. As in
+ * the reference's Embed (src/model.cpp:737-778), a pad's embedding row is
+ * zero and only real tokens count towards a sequence's length in the
+ * token-dropout ratio; nothing else changes (the attention takes no mask,
+ * AttentionVarlen, kernels.h:104-118). */
+int esm_gfx950_forward_packed_masked(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                                     const int32_t* masks, const int32_t* cu_seqlens, int batch_size,
+                                     int total_tokens, float* logits, int logits_on_device);
 /* Stages a packed batch in the model's device buffers: ids, per-token
  * embedding scale, in-sequence positions, cu_seqlens, the attention work
  * list and the RoPE tables (one pinned host-to-device copy). */
 int esm_gfx950_batch_upload(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                             const int32_t* cu_seqlens, int batch_size, int total_tokens);
+/* The same with pad masks (HOST int32 [T] or NULL), as in
+ * esm_gfx950_forward_packed_masked. */
+int esm_gfx950_batch_upload_masked(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
+                                   const int32_t* masks, const int32_t* cu_seqlens, int batch_size,
+                                   int total_tokens);
 /* Runs the forward on the staged batch with every input already in HBM;
  * logits fp32 [T, vocab] go to DEVICE memory. Stream-ordered, no host sync. */
 int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, float* logits);
@@ -438,6 +453,8 @@ int esm_gfx950_forward_device(esm_gfx950_ctx* ctx, esm_gfx950_model* model, floa
  * on its own sequence). No reference counterpart: the reference's
  * ForwardPacked (model.cpp:1093-1255) runs one thread pool. */
 int esm_gfx950_model_set_parts(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int parts);
+/* The model's configuration as created (Model::config, model.h:174). */
+int esm_gfx950_model_get_config(const esm_gfx950_model* model, esm_gfx950_model_config* out);
 /* The number of groups the last staged batch was split into (0 when none is
  * staged). No reference counterpart. */
 int esm_gfx950_model_staged_parts(const esm_gfx950_model* model, int* parts);

@@ -306,11 +306,16 @@ void or_round24_array(const float* x, float* out, size_t n) {
 }
 
 int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits) {
-  return or_forward_packed_hidden(m, ids, cu, B, T, logits, NULL);
+  return or_forward_packed_masked(m, ids, NULL, cu, B, T, logits, NULL);
 }
 
 int or_forward_packed_hidden(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits,
                              float* hidden_out) {
+  return or_forward_packed_masked(m, ids, NULL, cu, B, T, logits, hidden_out);
+}
+
+int or_forward_packed_masked(const or_model* m, const int32_t* ids, const int32_t* masks, const int32_t* cu, int B,
+                             int T, float* logits, float* hidden_out) {
   const int d = m->hidden, H = m->heads, dh = m->head_dim, f = m->ffn, V = m->vocab;
   const size_t Td = (size_t)T * d, Tf = (size_t)T * f;
   int maxL = 0;
@@ -331,22 +336,25 @@ int or_forward_packed_hidden(const or_model* m, const int32_t* ids, const int32_
   if (!hidden || !ln || !qkv || !attn || !proj || !inter || !inter_g || !cos_t || !sin_t || !qbuf || !sbuf || !acc)
     return -1;
 
-  /* Embed (model.cpp:737-778), no masks or pads. */
+  /* Embed (model.cpp:737-778): src_len counts real tokens (masks[t] != 0,
+   * every token when masks is NULL), mask tokens are counted over all
+   * tokens; mask-token and pad rows are zero. */
   const float k_drop = 0.15f * 0.8f;
   for (int b = 0; b < B; ++b) {
-    int src_len = 0, masks = 0;
+    int src_len = 0, mask_tokens = 0;
     for (int t = cu[b]; t < cu[b + 1]; ++t) {
-      ++src_len;
-      if (ids[t] == m->mask_token_id) ++masks;
+      if (!masks || masks[t] != 0) ++src_len;
+      if (ids[t] == m->mask_token_id) ++mask_tokens;
     }
-    const float ratio = src_len > 0 ? (float)masks / (float)src_len : 0.0f;
+    const float ratio = src_len > 0 ? (float)mask_tokens / (float)src_len : 0.0f;
     float denom = 1.0f - ratio;
     if (denom < 1e-12f) denom = 1e-12f;
     const float scale = (1.0f - k_drop) / denom;
     for (int t = cu[b]; t < cu[b + 1]; ++t) {
       const float* row = m->embed + (size_t)ids[t] * d;
       float* o = hidden + (size_t)t * d;
-      for (int i = 0; i < d; ++i) o[i] = ids[t] == m->mask_token_id ? 0.0f : row[i] * scale;
+      const int zero = ids[t] == m->mask_token_id || (masks && masks[t] == 0);
+      for (int i = 0; i < d; ++i) o[i] = zero ? 0.0f : row[i] * scale;
     }
   }
 

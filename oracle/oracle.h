@@ -126,6 +126,11 @@ int or_forward_packed(const or_model* m, const int32_t* ids, const int32_t* cu, 
  * (ForwardPackedInto's hidden_packed_out, model.cpp:1149-1189). */
 int or_forward_packed_hidden(const or_model* m, const int32_t* ids, const int32_t* cu, int B, int T, float* logits,
                              float* hidden_out);
+/* The same with BatchView's packed_masks (masks [T], 0 = pad; NULL: every
+ * token real): Embed zeroes pad rows and counts only real tokens in the
+ * token-dropout ratio's length (model.cpp:745-775); nothing else uses them. */
+int or_forward_packed_masked(const or_model* m, const int32_t* ids, const int32_t* masks, const int32_t* cu, int B,
+                             int T, float* logits, float* hidden_out);
 
 /* x rounded to its top 24 bits (sign, exponent, 15 mantissa bits): 0x80
  * added to the bit pattern, then the low byte cleared, i.e. round to

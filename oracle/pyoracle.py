@@ -116,6 +116,7 @@ class Oracle:
             "or_attention_varlen": [vp, vp, vp, vp, i32, i32, i32, vp],
             "or_forward_packed": [C.POINTER(_OrModel), vp, vp, i32, i32, vp],
             "or_forward_packed_hidden": [C.POINTER(_OrModel), vp, vp, i32, i32, vp, vp],
+            "or_forward_packed_masked": [C.POINTER(_OrModel), vp, vp, vp, i32, i32, vp, vp],
             "or_round24_array": [vp, vp, sz],
             "or_x86_gelu": [vp, vp, sz],
             "or_x86_layernorm": [vp, vp, vp, f32, vp, i32, i32],
@@ -282,13 +283,14 @@ class Oracle:
         return out
 
     def forward_packed(self, weights, batch, int8: bool, per_token: bool, fc1_fp16: bool = False,
-                       x86=False, ffn_bits: int = 32, hidden: bool = False):
+                       x86=False, ffn_bits: int = 32, hidden: bool = False, masks=None):
         """Restated packed forward. x86=True (or "avx512vnni") runs the
         reference's x86 AVX-512 kernels, per-tensor scales and LinearVnni in
         W8A8; x86="amx" the same with LinearAmx's row split. ffn_bits=24
         rounds fc1's output to 24 bits (per-token W8A8, the GPU's default).
         hidden=True also returns the hidden states [N + 1, T, d]
-        (ForwardWithHiddenStates' layout)."""
+        (ForwardWithHiddenStates' layout). masks: BatchView's packed_masks
+        (int32 [T], 0 = pad) or None."""
         if x86 and int8 and per_token:
             raise ValueError("the x86 path quantises activations per tensor")
         m, keep = make_or_model(weights, int8, per_token, fc1_fp16, 2 if x86 == "amx" else int(bool(x86)),
@@ -297,7 +299,10 @@ class Oracle:
         cfg = weights.cfg
         logits = np.empty((T, cfg.vocab_size), np.float32)
         hs = np.empty((cfg.num_layers + 1, T, cfg.hidden_size), np.float32) if hidden else None
-        rc = self.lib.or_forward_packed_hidden(C.byref(m), _p(_c(batch.ids, np.int32)),
+        mk = None if masks is None else _c(masks, np.int32)
+        if mk is not None and mk.shape != (T,):
+            raise ValueError("masks must have one entry per token")
+        rc = self.lib.or_forward_packed_masked(C.byref(m), _p(_c(batch.ids, np.int32)), _p(mk),
                                                _p(_c(batch.cu, np.int32)), len(batch.cu) - 1, T, _p(logits),
                                                _p(hs))
         if rc != 0:

@@ -19,6 +19,12 @@ SIGNATURES = {
     "esm_gfx950_bridge_scale": (i32, [vp, sz, f32]),
     "esm_gfx950_bridge_rope_apply_varlen": (i32, [vp, vp, vp, vp, i32, i32, i32]),
     "esm_gfx950_bridge_attention_varlen": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "esm_gfx950_bridge_forward_packed": (i32, [vp, vp, vp, vp, i32, i32, i32, vp, vp]),
+    "esm_gfx950_bridge_forward_scheduled": (i32, [vp, vp, vp, vp, i32, f32, i32, vp]),
+    "esm_gfx950_bridge_qt_create": (vp, [vp, vp, i32, i32]),
+    "esm_gfx950_bridge_qt_data": (vp, [vp]),
+    "esm_gfx950_bridge_linear_int8_qt": (i32, [vp, vp, vp, vp, i32]),
+    "esm_gfx950_bridge_qt_free": (None, [vp]),
 }
 
 
@@ -96,3 +102,29 @@ class Bridge:
         self._check(self.lib.esm_gfx950_bridge_attention_varlen(_p(q), _p(k), _p(v), _p(cu), len(cu) - 1, H, dh,
                                                                 _p(out)))
         return out
+
+    def forward_packed(self, model, ids, cu, masks=None, layers=None, hidden_size=None, vocab=33):
+        """ForwardPacked through a BatchView: (per-sequence logits list,
+        hidden [layers + 1, T, d] or None). Raises ValueError with BatchView's
+        message when it rejects the batch."""
+        ids, cu = _c(ids, np.int32), _c(cu, np.int32)
+        mk = None if masks is None else _c(masks, np.int32)
+        T = ids.shape[0]
+        logits = np.zeros((T, vocab), np.float32)
+        hidden = None if layers is None else np.zeros((layers + 1, T, hidden_size), np.float32)
+        rc = self.lib.esm_gfx950_bridge_forward_packed(model.handle, _p(ids), _p(mk), _p(cu), len(cu), len(cu) - 1,
+                                                       T, _p(logits), _p(hidden))
+        if rc == -1:
+            raise ValueError(self.error())
+        self._check(rc)
+        return [logits[cu[b]:cu[b + 1]] for b in range(len(cu) - 1)], hidden
+
+    def forward_scheduled(self, model, seqs, masks=None, threshold=1.2, max_batch=256, vocab=33):
+        lengths = np.array([len(x) for x in seqs], np.int32)
+        ids = _c(np.concatenate(seqs), np.int32)
+        mk = None if masks is None else _c(np.concatenate(masks), np.int32)
+        out = np.zeros((ids.shape[0], vocab), np.float32)
+        self._check(self.lib.esm_gfx950_bridge_forward_scheduled(model.handle, _p(ids), _p(lengths), _p(mk),
+                                                                 len(seqs), threshold, max_batch, _p(out)))
+        offs = np.concatenate([[0], np.cumsum(lengths)])
+        return [out[offs[i]:offs[i + 1]] for i in range(len(seqs))]

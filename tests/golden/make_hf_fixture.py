@@ -17,7 +17,14 @@ implementation computes:
                      state, hidden_0 = post-embed, hidden_1..5 = layer
                      outputs, hidden_6 = post-final-LN (the reference's
                      ForwardWithHiddenStates layout, include/esm_cpp/model.h:
-                     184-191; model.cpp:1149-1189).
+                     184-191; model.cpp:1149-1189);
+  * pad_*            two sequences with pads (attention_mask 0) run as one
+                     padded HF batch: the post-embed state only. HF zeroes
+                     pad rows and counts real tokens in the token-dropout
+                     ratio, as the reference's Embed does (model.cpp:745-775);
+                     past the embedding the two differ on purpose (HF masks
+                     pad keys in attention, the reference's AttentionVarlen
+                     takes no mask), so later states are not recorded.
 
 Only this .npz is used by the tests; transformers is imported here alone.
 Run:  python tests/golden/make_hf_fixture.py
@@ -47,6 +54,37 @@ def mask_batch() -> syn.PackedBatch:
         for p in pos:
             ids[cu[s] + p] = syn.MASK
     return syn.PackedBatch(ids, cu.copy(), b.lengths.copy())
+
+
+def pad_batch():
+    """(ids, masks, cu): two 30-token sequences; the first ends in six pads,
+    the second has three pads inside it and two mask tokens."""
+    b = syn.batch_from_lengths([30, 30], seed=12)
+    ids = b.ids.copy()
+    masks = np.ones_like(ids)
+    masks[24:30] = 0
+    ids[24:30] = syn.PAD
+    for p in (30 + 10, 30 + 11, 30 + 20):
+        masks[p] = 0
+        ids[p] = syn.PAD
+    ids[30 + 4] = ids[30 + 15] = syn.MASK
+    return ids, masks, b.cu.copy()
+
+
+def run_padded(m, ids, masks, cu):
+    """HF's post-embed state of the sequences as one padded batch."""
+    import torch
+
+    caps = []
+    h = m.esm.embeddings.register_forward_hook(lambda _m, _i, o: caps.append(o.clone()))
+    try:
+        with torch.no_grad():
+            x = torch.from_numpy(np.stack([ids[cu[i]:cu[i + 1]] for i in range(len(cu) - 1)]).astype(np.int64))
+            am = torch.from_numpy(np.stack([masks[cu[i]:cu[i + 1]] for i in range(len(cu) - 1)]).astype(np.int64))
+            m(input_ids=x, attention_mask=am)
+    finally:
+        h.remove()
+    return caps[0].numpy().reshape(-1, caps[0].shape[-1]).astype(np.float32)
 
 
 def hf_model(w):
@@ -139,8 +177,11 @@ def main():
         lg, hs = run_one(m, bm.ids[bm.cu[s]:bm.cu[s + 1]])
         m_logits.append(lg)
         m_hidden.append(hs)
+    p_ids, p_masks, p_cu = pad_batch()
+    p_hidden0 = run_padded(m, p_ids, p_masks, p_cu)
     np.savez_compressed(
         OUT,
+        pad_ids=p_ids, pad_masks=p_masks, pad_cu=p_cu, pad_hidden0=p_hidden0,
         seq_ids=b1.ids, seq_cu=b1.cu, seq_logits=np.concatenate(logits),
         mask_ids=bm.ids, mask_cu=bm.cu, mask_logits=np.concatenate(m_logits),
         mask_hidden=np.concatenate(m_hidden, axis=1),

@@ -131,3 +131,47 @@ def test_w8a8_hidden_states_vs_oracle(dev, oracle):
     _, want = oracle.forward_packed(w, b, int8=True, per_token=True, ffn_bits=24, hidden=True)
     for i in range(want.shape[0]):
         assert corr(hs[i], want[i]) >= 0.9999, i
+
+
+def test_gpu_pad_masks(dev, oracle, fx, w8m):
+    """BatchView's packed_masks on the device (esm_gfx950_forward_packed_masked,
+    forward_hidden_states with masks): the post-embed state against HF's
+    padded batch (1e-6), the logits against the oracle's masked forward
+    (config-1 bar 1e-5), and all-ones masks bit-identical to no masks."""
+    cu = fx["pad_cu"]
+    b = syn.PackedBatch(fx["pad_ids"], cu, np.diff(cu).astype(np.int32))
+    masks = fx["pad_masks"]
+    want_l = oracle.forward_packed(w8m, b, int8=False, per_token=False, masks=masks)
+    m = eg.Model(dev, w8m, int8=False)
+    try:
+        logits, hs = m.forward_hidden_states(b.ids, b.cu, masks=masks)
+        got = m.forward_packed_masked(b.ids, masks, b.cu)
+        plain = m.forward_packed(b.ids, b.cu)
+        ones = m.forward_packed_masked(b.ids, np.ones_like(masks), b.cu)
+    finally:
+        m.free()
+    assert np.all(hs[0][masks == 0] == 0)
+    np.testing.assert_allclose(hs[0], fx["pad_hidden0"], rtol=1e-6, atol=1e-6)
+    assert np.array_equal(logits, got)
+    np.testing.assert_allclose(got, want_l, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(ones, plain)
+    assert not np.array_equal(got, plain)
+
+
+def test_gpu_pad_masks_w8a8(dev, oracle):
+    """Pads in the per-token W8A8 forward against the oracle's same-mode
+    masked forward (correlation >= 0.9999), over two sequence groups."""
+    cfg = syn.ESM2_650M.with_layers(2)
+    w = syn.make_weights(cfg, seed=20261201 + 4, int8=True, keep_f32_linears=False)
+    b = syn.batch_from_lengths([130, 61, 250, 97], seed=9)
+    masks = np.ones_like(b.ids)
+    masks[b.cu[1] - 20:b.cu[1]] = 0
+    masks[b.cu[2] + 5:b.cu[2] + 9] = 0
+    m = eg.Model(dev, w, int8=True, act_mode=eg.ACT_PER_TOKEN)
+    try:
+        m.set_parts(2)
+        got = m.forward_packed_masked(b.ids, masks, b.cu)
+    finally:
+        m.free()
+    want = oracle.forward_packed(w, b, int8=True, per_token=True, ffn_bits=24, masks=masks)
+    assert corr(got, want) >= 0.9999

@@ -86,3 +86,23 @@ def test_hf_fixture_catches_planted_composition_mistakes(fx, w8m, oracle):
     w_nm.cfg = syn.EsmConfig("no-token-dropout", 6, 320, 20, 1280, mask_token_id=-1)
     bad = oracle.forward_packed(w_nm, b, int8=False, per_token=False)
     assert float(np.max(np.abs(bad - fx["mask_logits"]))) > REF_LOGITS_MAX
+
+
+def test_oracle_pad_embedding_matches_hf(fx, w8m, oracle):
+    """BatchView's packed_masks (pads) in the oracle's Embed against HF's
+    post-embed state of the same sequences as one padded batch: pad rows
+    zero, and the token-dropout ratio over real tokens only (the second
+    sequence holds mask tokens and pads). Ignoring the masks fails the bar."""
+    cu = fx["pad_cu"]
+    b = syn.PackedBatch(fx["pad_ids"], cu, np.diff(cu).astype(np.int32))
+    masks = fx["pad_masks"]
+    _, hs = oracle.forward_packed(w8m, b, int8=False, per_token=False, hidden=True, masks=masks)
+    want = fx["pad_hidden0"]
+    assert np.all(hs[0][masks == 0] == 0)
+    np.testing.assert_allclose(hs[0], want, rtol=1e-6, atol=1e-6)
+    _, unmasked = oracle.forward_packed(w8m, b, int8=False, per_token=False, hidden=True)
+    assert float(np.max(np.abs(unmasked[0] - want))) > 1e-3
+    ones = np.ones_like(masks)
+    lg1 = oracle.forward_packed(w8m, b, int8=False, per_token=False, masks=ones)
+    lg0 = oracle.forward_packed(w8m, b, int8=False, per_token=False)
+    assert np.array_equal(lg1, lg0)
