@@ -27,6 +27,7 @@
 // the tile space, which keeps the A rows and W columns it shares inside
 // that XCD's L2.
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -466,6 +467,17 @@ __device__ __forceinline__ T* row_at(T* tile, uint32_t ldc, int R, uint32_t lane
   return reinterpret_cast<T*>(row + lane_byte);
 }
 
+// Buffer resource over a tile's output (or residual input): the epilogues
+// address every access as this base plus a 32-bit lane offset (VGPR, the
+// same for every row) plus the row's 32-bit byte offset (SGPR), which the
+// buffer instructions add themselves -- no per-access address arithmetic.
+// Offsets stay far below the 4 GiB record range. Word 3 selects a 32-bit
+// data format (raw, untyped accesses).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
+}
+constexpr int kBufNT = 2;  // buffer access aux bits: non-temporal
+
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
 // rotary pair. hc: the head's first column relative to the tile origin.
@@ -536,16 +548,21 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
             x2 *= p.q_prescale;
           }
           const uint32_t w1 = split_f16_word(x1), w2 = split_f16_word(x2);
-          uint32_t* row0 = reinterpret_cast<uint32_t*>(p.C_f32) + static_cast<size_t>(m0) * ldc;
-          uint32_t* dst = row_at(row0, ldc, wr0 + static_cast<int>(dr), lane_s);
+          // Buffer stores relative to the tile's first row: the lane offset
+          // lane_s (VGPR) plus the row's byte offset (SGPR).
+          const __amdgpu_buffer_rsrc_t rows = tile_rsrc(reinterpret_cast<uint32_t*>(p.C_f32) +
+                                                        static_cast<size_t>(m0) * ldc);
+          const uint32_t soff = (static_cast<uint32_t>(wr0) + dr) * ldc * 4u;
           if constexpr (WHICH == 0) {
             // Q words, the rotary pair adjacent: one 8-byte store per lane.
-            __builtin_nontemporal_store(u32x2{w1, w2}, reinterpret_cast<u32x2*>(dst));
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{w1, w2}, rows, lane_s, soff, kBufNT);
           } else {
             // K / V: the pair's fp16 hi parts in the hi plane, lo parts in
             // the lo plane (d / 2 words further).
-            __builtin_nontemporal_store(__builtin_amdgcn_perm(w2, w1, 0x05040100u), dst);
-            __builtin_nontemporal_store(__builtin_amdgcn_perm(w2, w1, 0x07060302u), dst + dm / 2);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(w2, w1, 0x05040100u), rows, lane_s, soff,
+                                                  kBufNT);
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(w2, w1, 0x07060302u), rows, lane_s,
+                                                  soff + dm * 2u, kBufNT);
           }
         } else {
           // [M, d_model] outputs; column of the head inside its Q / K / V part.
@@ -571,7 +588,7 @@ template <int BLK_M, int BLK_N, int EPI, bool FULL, bool MAX>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
                                            const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
-                                           int n0, int32_t* c_i32) {
+                                           int n0, int32_t* c_i32, bool nan_risk) {
   const int lr0 = wm * BLK_M * 32 + hi * 4;
   const int lc0 = wn * BLK_N * 32 + l32;
   const uint32_t ldc = p.ldc;
@@ -626,38 +643,47 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       static_assert(BLK_N == 2, "the 24-bit layout pairs a lane's two 32-column blocks");
       const int gc = wn * 64;  // the wave's column group inside the tile
       if (!FULL && n0 + gc >= p.N) return;
-      uint16_t* htile = p.C_f16 + static_cast<size_t>(m0) * ldc + n0 + gc;
-      uint8_t* ltile = p.C_u8 + static_cast<size_t>(m0) * ldc + n0 + gc;
+      const __amdgpu_buffer_rsrc_t rh = tile_rsrc(p.C_f16 + static_cast<size_t>(m0) * ldc + n0 + gc);
+      const __amdgpu_buffer_rsrc_t rl = tile_rsrc(p.C_u8 + static_cast<size_t>(m0) * ldc + n0 + gc);
       const uint32_t lane_h = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32)) * 2u;
       const uint32_t lane_l = static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32);
+      // A NaN's bit pattern must not take the rounding add (it could carry
+      // into the sign or leave an infinity). fma(float(acc), a_scale *
+      // w_scale, bias) can be NaN only when a scale or bias is not finite or
+      // a scale product overflows; the prologue checks the tile's scales and
+      // biases (nan_risk), and only such a tile maps NaN to the quiet NaN
+      // value by value.
+      auto pass = [&](auto fix_nan) {
 #pragma unroll
-      for (int i = 0; i < BLK_M; ++i)
+        for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int lr = lr0 + i * 32 + q * 8;
-          const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
-          const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
+          for (int q = 0; q < 4; ++q) {
+            const int lr = lr0 + i * 32 + q * 8;
+            const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
+            const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int r = 4 * q + u;
-            if (!FULL && m0 + lr + u >= p.M) continue;
-            const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
-            const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
-            uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
-            // A NaN's bit pattern must not take the rounding add (it could
-            // carry into the sign or leave an infinity); one unordered
-            // compare per pair finds NaNs, which become the quiet NaN.
-            if (__builtin_expect(__builtin_isunordered(v0, v1), 0)) {
-              if (__builtin_isnan(v0)) b0 = 0x7fc00000u;
-              if (__builtin_isnan(v1)) b1 = 0x7fc00000u;
+            for (int u = 0; u < 4; ++u) {
+              const int r = 4 * q + u;
+              if (!FULL && m0 + lr + u >= p.M) continue;
+              const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
+              const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
+              uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
+              if constexpr (decltype(fix_nan)::value) {
+                b0 = __builtin_isnan(v0) ? 0x7fc00000u : b0;
+                b1 = __builtin_isnan(v1) ? 0x7fc00000u : b1;
+              }
+              const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(b1, b0, 0x07060302u), rh, lane_h,
+                                                    R * ldc * 2u, kBufNT);
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u)),
+                                                    rl, lane_l, R * ldc, kBufNT);
             }
-            const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
-            auto* hdst = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(htile) + static_cast<size_t>(R * ldc) * 2u + lane_h);
-            auto* ldst = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(ltile) + static_cast<size_t>(R * ldc) + lane_l);
-            __builtin_nontemporal_store(__builtin_amdgcn_perm(b1, b0, 0x07060302u), hdst);
-            __builtin_nontemporal_store(static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u)), ldst);
           }
-        }
+      };
+      if (__builtin_expect(nan_risk, 0))
+        pass(std::true_type{});
+      else
+        pass(std::false_type{});
       return;
     } else if constexpr (EPI == kEpiF32Resid) {
       // C += result, in groups of four rows x BLK_N columns (8 values per
@@ -667,17 +693,21 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       // would need 160 more registers). The sum is C + v, the residual add's
       // operands and rounding.
       constexpr int kGroups = BLK_M * 4, kDist = BLK_M >= 5 ? 3 : 4;
-      float* tile = p.C_f32 + static_cast<size_t>(m0) * ldc + n0;
+      const __amdgpu_buffer_rsrc_t rt = tile_rsrc(p.C_f32 + static_cast<size_t>(m0) * ldc + n0);
       const uint32_t lane_b = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(lc0)) * 4u;
+      // Byte offset of tile row R (uniform) plus column block j.
+      auto roff = [&](int R, int j) { return static_cast<uint32_t>(R) * ldc * 4u + static_cast<uint32_t>(j * 128); };
       float res[kDist + 1][4][BLK_N];
       auto load_group = [&](int g, float(&r)[4][BLK_N]) {
         const int dr0 = (g >> 2) * 32 + (g & 3) * 8;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const bool rok = FULL || m0 + lr0 + dr0 + u < p.M;
-          const float* src = row_at(tile, ldc, wr0 + dr0 + u, lane_b);
 #pragma unroll
-          for (int j = 0; j < BLK_N; ++j) r[u][j] = (rok && col_ok(lc0 + j * 32)) ? src[j * 32] : 0.0f;
+          for (int j = 0; j < BLK_N; ++j)
+            r[u][j] = (rok && col_ok(lc0 + j * 32))
+                          ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rt, lane_b, roff(wr0 + dr0 + u, j), 0))
+                          : 0.0f;
         }
       };
 #pragma unroll
@@ -692,12 +722,12 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const bool rok = FULL || m0 + lr + u < p.M;
-          float* dst = row_at(tile, ldc, wr0 + i * 32 + q * 8 + u, lane_b);
 #pragma unroll
           for (int j = 0; j < BLK_N; ++j) {
             const float v = __builtin_fmaf(static_cast<float>(acc[i][j][4 * q + u]), asv[u] * ws[j], bs[j]);
             if (rok && col_ok(lc0 + j * 32))
-              __builtin_nontemporal_store(res[g % (kDist + 1)][u][j] + v, dst + j * 32);
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(res[g % (kDist + 1)][u][j] + v), rt, lane_b,
+                                                    roff(wr0 + i * 32 + q * 8 + u, j), kBufNT);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -786,22 +816,33 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   const int nk = nk_all * (split + 1) / splits - kb0;
   const int8_t* const pA = p.A + kb0 * BK;
   const int8_t* const pW = p.W + kb0 * BK;
+  // kEpiF32R24: whether a value of the tile can be NaN (a scale or bias not
+  // finite, or a scale above 2^60, so that a product of two could overflow).
+  bool nan_risk = false;
   if constexpr (EPI != kEpiI32) {
     // Per-row activation scales and per-column weight scales / bias of the
     // tile, read once here instead of per element in the epilogue.
+    int risk = 0;
     for (int t = threadIdx.x; t < BM + BN; t += kThreads) {
       if (t < BM) {
         const int row = m0 + t;
-        s_as[t] = row < p.M ? p.a_scale[row] : 0.0f;
+        const float a = row < p.M ? p.a_scale[row] : 0.0f;
+        s_as[t] = a;
+        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(a) <= 0x1p60f);
         if constexpr (kRope) s_pos[t] = row < p.M ? p.pos[row] : 0;
       } else {
         const int c = t - BM, col = n0 + c;
         const bool ok = col < p.N;
-        s_ws[c] = ok ? p.w_scale[col] : 0.0f;
-        s_bs[c] = (ok && p.bias) ? p.bias[col] : 0.0f;
+        const float w = ok ? p.w_scale[col] : 0.0f, b = (ok && p.bias) ? p.bias[col] : 0.0f;
+        s_ws[c] = w;
+        s_bs[c] = b;
+        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(w) <= 0x1p60f) | !(__builtin_fabsf(b) <= 0x1p127f);
       }
     }
-    __syncthreads();
+    if constexpr (EPI == kEpiF32R24)
+      nan_risk = __syncthreads_or(risk) != 0;
+    else
+      __syncthreads();
   }
   // The wave index is uniform across the wave; readfirstlane tells the
   // compiler so, keeping per-wave decisions (Q/K/V head, RoPE) scalar.
@@ -829,13 +870,9 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
 #pragma unroll
   for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i), goff[i], ldst + i * 1024);
 
+  // The accumulators start as the first products (the first sub-step's
+  // MFMAs take a zero C operand), so no register is cleared beforehand.
   i32x16 acc[BLK_M][BLK_N];
-#pragma unroll
-  for (int i = 0; i < BLK_M; ++i)
-#pragma unroll
-    for (int j = 0; j < BLK_N; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
   // Fragments are double-buffered in registers: the reads of K sub-step
   // q + 1 (32 bytes of K) are issued between the MFMAs of sub-step q, one
@@ -867,6 +904,13 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
 #pragma unroll
       for (int j = 0; j < BLK_N; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
   };
+  auto mfmas_first = [&](const i32x4(&fa)[BLK_M], const i32x4(&fb)[BLK_N]) {
+    const i32x16 zero = {};
+#pragma unroll
+    for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) acc[i][j] = mfma32(fa[i], fb[j], zero);
+  };
   // Order the reads issued during a sub-step's MFMAs: read, MFMA, read,
   // MFMA ... then the remaining MFMAs.
   // Short tiles (BLK_M 1) issue more reads than MFMAs per sub-step; the
@@ -895,12 +939,17 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   read_frags(smem, 0, fa0, fb0);
   static_assert(kSub == 4, "the sub-step rotation below assumes four 32-byte sub-steps per stage");
   // Buffer of stage kt (kt mod kNStage), kept as a wave-uniform counter.
+  // Stage 0 is the loop body with its first sub-step's MFMAs starting the
+  // accumulators.
   int bcur = 0;
-  for (int kt = 0; kt < nk; ++kt) {
+  auto stage = [&](int kt, auto first) {
     const int8_t* cur = smem + bcur * kStage;
     const int bnext = bcur + 1 == kNStage ? 0 : bcur + 1;
     read_frags(cur, 1, fa1, fb1);
-    mfmas(fa0, fb0);
+    if constexpr (decltype(first)::value)
+      mfmas_first(fa0, fb0);
+    else
+      mfmas(fa0, fb0);
     interleave();
     read_frags(cur, 2, fa0, fb0);
     mfmas(fa1, fb1);
@@ -931,7 +980,9 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
     mfmas(fa1, fb1);
     interleave();
     bcur = bnext;
-  }
+  };
+  stage(0, std::true_type{});
+  for (int kt = 1; kt < nk; ++kt) stage(kt, std::false_type{});
 
   const float* s_cosT = nullptr;
   const float* s_sinT = nullptr;
@@ -969,17 +1020,17 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
       epilogue32<BLK_M, BLK_N, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32);
+          c_i32, nan_risk);
     else
       epilogue32<BLK_M, BLK_N, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32);
+          c_i32, nan_risk);
   } else {
     if (full)
       epilogue32<BLK_M, BLK_N, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32);
+          c_i32, nan_risk);
     else
       epilogue32<BLK_M, BLK_N, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32);
+          c_i32, nan_risk);
   }
 }
 
