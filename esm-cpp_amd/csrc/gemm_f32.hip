@@ -143,12 +143,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_kernel(const GemmF32Args
 // wave layout as above on v_mfma_f32_16x16x32_f16: each lane holds eight
 // consecutive k of one row for A and W, so one MFMA covers a 32-wide K stage.
 // A (fp32) is split into hi / lo fp16 planes while it is staged in LDS; W's
-// planes come split. LDS rows are 80 bytes (64 + 16 pad): the 16 rows one
-// 16-lane group reads sit 20 banks apart, so the fragment reads are
-// conflict-free.
-constexpr int kX3Pitch = 80;                    // bytes per 32-half row
+// planes come split. LDS rows are 64 bytes (four 16-byte chunks), chunk c of
+// row r stored at position c ^ ((r / 4) mod 4): the 16-byte fragment reads
+// of 16 rows at one chunk then cover all 64 banks once, and so do the stage
+// writes of four consecutive rows (an 80-byte padded pitch kept the reads
+// conflict-free but made every write pass conflict).
+constexpr int kX3Pitch = 64;                    // bytes per 32-half row
 constexpr int kX3Plane = 128 * kX3Pitch;        // one 128-row plane
 constexpr int kX3Stage = 4 * kX3Plane;          // A hi, A lo, W hi, W lo
+
+// Byte offset of 16-byte chunk c of row r in a plane.
+__device__ __forceinline__ int x3_off(int r, int c) { return r * kX3Pitch + ((c ^ ((r >> 2) & 3)) << 4); }
 
 __device__ __forceinline__ uint2 pack_f16x4(float a, float b, float c, float d) {
   return make_uint2(static_cast<uint32_t>(f32_to_f16_bits(a)) | (static_cast<uint32_t>(f32_to_f16_bits(b)) << 16),
@@ -185,7 +190,7 @@ __device__ __forceinline__ void x3_store(uint8_t* st, const f32x4 (&ra)[4], cons
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int idx = t + kThreads * i;
-    const int off = (idx >> 3) * kX3Pitch + (idx & 7) * 8;
+    const int off = x3_off(idx >> 3, (idx & 7) >> 1) + (idx & 1) * 8;
     const f32x4 x = ra[i];
     const float hx = f16_bits_to_f32(f32_to_f16_bits(x[0])), hy = f16_bits_to_f32(f32_to_f16_bits(x[1]));
     const float hz = f16_bits_to_f32(f32_to_f16_bits(x[2])), hw = f16_bits_to_f32(f32_to_f16_bits(x[3]));
@@ -195,7 +200,7 @@ __device__ __forceinline__ void x3_store(uint8_t* st, const f32x4 (&ra)[4], cons
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int idx = t + kThreads * i;
-    const int off = (idx >> 2) * kX3Pitch + (idx & 3) * 16;
+    const int off = x3_off(idx >> 2, idx & 3);
     *reinterpret_cast<i32x4*>(st + 2 * kX3Plane + off) = rh[i];
     *reinterpret_cast<i32x4*>(st + 3 * kX3Plane + off) = rl[i];
   }
@@ -230,8 +235,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_x3_kernel(const GemmX3Args p
     f16x8 ah[4], al[4], bh[4], bl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ao = (wm * 64 + i * 16 + lr) * kX3Pitch + lg * 16;
-      const int bo = (wn * 64 + i * 16 + lr) * kX3Pitch + lg * 16;
+      const int ao = x3_off(wm * 64 + i * 16 + lr, lg);
+      const int bo = x3_off(wn * 64 + i * 16 + lr, lg);
       ah[i] = *reinterpret_cast<const f16x8*>(cur + ao);
       al[i] = *reinterpret_cast<const f16x8*>(cur + kX3Plane + ao);
       bh[i] = *reinterpret_cast<const f16x8*>(cur + 2 * kX3Plane + bo);

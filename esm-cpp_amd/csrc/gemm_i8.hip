@@ -477,11 +477,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, 0x00020000);
 }
 constexpr int kBufNT = 2;  // buffer access aux bits: non-temporal
-// LDS bytes per wave for epilogues that restage a 32-row block through LDS
-// (the 24-bit fc1 output): a high plane of 32 rows x 128 bytes and a low
-// plane of 32 rows x 64 bytes, rows padded to 144 / 80 bytes.
-constexpr int kR24HiPitch = 144, kR24LoPitch = 80;
-constexpr int kEpiLdsPerWave = 32 * (kR24HiPitch + kR24LoPitch);
 
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
@@ -593,7 +588,7 @@ template <int BLK_M, int BLK_N, int EPI, bool FULL, bool MAX>
 __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int wm, int wn,
                                            int l32, int hi, const float* s_as, const float* s_ws,
                                            const float* s_bs, const float* s_cosT, const float* s_sinT, int m0,
-                                           int n0, int32_t* c_i32, bool nan_risk, int8_t* lds_wave) {
+                                           int n0, int32_t* c_i32, bool nan_risk) {
   const int lr0 = wm * BLK_M * 32 + hi * 4;
   const int lc0 = wn * BLK_N * 32 + l32;
   const uint32_t ldc = p.ldc;
@@ -641,24 +636,17 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       return;
     } else if constexpr (EPI == kEpiF32R24) {
       // The lane's two columns (l32 and 32 + l32 of the wave's 64) round to
-      // 24 bits (+0x80, then the top three bytes): their high halves form one
-      // 4-byte word at stored positions 2 l32, 2 l32 + 1 of the group, their
-      // low bytes one 2-byte word. Each 32-row block is restaged through the
-      // wave's LDS slice and leaves as whole rows, 16 bytes per lane: four
-      // 16-byte stores for the high plane and two for the low plane per
-      // block instead of 32 narrow ones (store issue bounded this epilogue).
+      // 24 bits (+0x80, then the top three bytes) and go out as one 4-byte
+      // word of their high halves and one 2-byte word of their low bytes, at
+      // stored positions 2 l32 and 2 l32 + 1 of the group: whole 128-byte
+      // rows of the high plane per half-wave.
       static_assert(BLK_N == 2, "the 24-bit layout pairs a lane's two 32-column blocks");
       const int gc = wn * 64;  // the wave's column group inside the tile
       if (!FULL && n0 + gc >= p.N) return;
       const __amdgpu_buffer_rsrc_t rh = tile_rsrc(p.C_f16 + static_cast<size_t>(m0) * ldc + n0 + gc);
       const __amdgpu_buffer_rsrc_t rl = tile_rsrc(p.C_u8 + static_cast<size_t>(m0) * ldc + n0 + gc);
-      int8_t* const lh = lds_wave;
-      int8_t* const ll = lds_wave + 32 * kR24HiPitch;
-      const int lane = hi * 32 + l32;
-      // Restaged reads: high plane, lane -> row k * 8 + lane / 8, chunk lane % 8;
-      // low plane, lane -> row k * 16 + lane / 4, chunk lane % 4.
-      const uint32_t vh = static_cast<uint32_t>(lane >> 3) * ldc * 2u + static_cast<uint32_t>(lane & 7) * 16u;
-      const uint32_t vl = static_cast<uint32_t>(lane >> 2) * ldc + static_cast<uint32_t>(lane & 3) * 16u;
+      const uint32_t lane_h = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32)) * 2u;
+      const uint32_t lane_l = static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32);
       // A NaN's bit pattern must not take the rounding add (it could carry
       // into the sign or leave an infinity). fma(float(acc), a_scale *
       // w_scale, bias) can be NaN only when a scale or bias is not finite or
@@ -667,7 +655,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       // value by value.
       auto pass = [&](auto fix_nan) {
 #pragma unroll
-        for (int i = 0; i < BLK_M; ++i) {
+        for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int lr = lr0 + i * 32 + q * 8;
@@ -676,6 +664,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               const int r = 4 * q + u;
+              if (!FULL && m0 + lr + u >= p.M) continue;
               const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
               const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
               uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
@@ -683,35 +672,13 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
                 b0 = __builtin_isnan(v0) ? 0x7fc00000u : b0;
                 b1 = __builtin_isnan(v1) ? 0x7fc00000u : b1;
               }
-              const int br = q * 8 + hi * 4 + u;  // row inside the block
-              *reinterpret_cast<uint32_t*>(lh + br * kR24HiPitch + 4 * l32) = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
-              *reinterpret_cast<uint16_t*>(ll + br * kR24LoPitch + 2 * l32) =
-                  static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u));
+              const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
+              __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(b1, b0, 0x07060302u), rh, lane_h,
+                                                    R * ldc * 2u, kBufNT);
+              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u)),
+                                                    rl, lane_l, R * ldc, kBufNT);
             }
           }
-          // LDS accesses of one wave complete in order: the reads below see
-          // every lane's writes, and the next block's writes follow them. The
-          // compiler barriers keep that order in the emitted code (the writes
-          // and reads use different access types, so alias analysis alone
-          // would let them move past each other).
-          asm volatile("" ::: "memory");
-          const int R0 = wr0 + i * 32;  // the block's first tile row
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const int br = k * 8 + (lane >> 3);
-            const u32x4 v = *reinterpret_cast<const u32x4*>(lh + br * kR24HiPitch + (lane & 7) * 16);
-            if (FULL || m0 + R0 + br < p.M)
-              __builtin_amdgcn_raw_buffer_store_b128(v, rh, vh, static_cast<uint32_t>(R0 + k * 8) * ldc * 2u, kBufNT);
-          }
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const int br = k * 16 + (lane >> 2);
-            const u32x4 v = *reinterpret_cast<const u32x4*>(ll + br * kR24LoPitch + (lane & 3) * 16);
-            if (FULL || m0 + R0 + br < p.M)
-              __builtin_amdgcn_raw_buffer_store_b128(v, rl, vl, static_cast<uint32_t>(R0 + k * 16) * ldc, kBufNT);
-          }
-          asm volatile("" ::: "memory");
-        }
       };
       if (__builtin_expect(nan_risk, 0))
         pass(std::true_type{});
@@ -1059,25 +1026,20 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   }
   constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
-  // The operand buffers are idle after the main loop (its last barrier
-  // retired every read of real stage data); epilogues that restage their
-  // outputs take a wave-private slice of them.
-  int8_t* const lds_wave = smem + wave * kEpiLdsPerWave;
-  static_assert(TL::kWaves * kEpiLdsPerWave <= kNStage * kStage, "epilogue staging fits in the operand buffers");
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
       epilogue32<BLK_M, BLK_N, EPI, true, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32, nan_risk, lds_wave);
+          c_i32, nan_risk);
     else
       epilogue32<BLK_M, BLK_N, EPI, false, kMaxable>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32, nan_risk, lds_wave);
+          c_i32, nan_risk);
   } else {
     if (full)
       epilogue32<BLK_M, BLK_N, EPI, true, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32, nan_risk, lds_wave);
+          c_i32, nan_risk);
     else
       epilogue32<BLK_M, BLK_N, EPI, false, false>(p, acc, wm, wn, l32, hi, s_as, s_ws, s_bs, s_cosT, s_sinT, m0, n0,
-          c_i32, nan_risk, lds_wave);
+          c_i32, nan_risk);
   }
 }
 

@@ -271,7 +271,15 @@ def test_linear_i8_gelu_quant_r24(dev, oracle, M, N, K, ldq):
     want = oracle.round24(oracle.dequant(acc, a_s, w_s, bias))
     assert np.all(np.isnan(inter[nan_row]))
     ok = np.arange(M) != nan_row
-    assert np.array_equal(inter[ok].view(np.uint32), want[ok].view(np.uint32))
+    bad = np.argwhere((inter.view(np.uint32) != want.view(np.uint32)) & ok[:, None])
+    if bad.size:
+        g32, w32 = inter.view(np.uint32), want.view(np.uint32)
+        detail = [(int(r), int(c), hex(int(g32[r, c])), hex(int(w32[r, c]))) for r, c in bad[:6]]
+        # where else does the wrong value occur in the expected array (same row or rows nearby)?
+        r0, c0 = bad[0]
+        hits = np.argwhere(w32[max(r0 - 8, 0):r0 + 8] == g32[r0, c0])
+        raise AssertionError(f"{len(bad)} values differ; {detail}; rows {np.unique(bad[:, 0])[:16].tolist()}; "
+                             f"cols {np.unique(bad[:, 1])[:40].tolist()}; got value found at {(hits + [max(r0 - 8, 0), 0])[:4].tolist()}")
 
     g = oracle.gelu(want[ok])
     q_ref, s_ref = oracle.quant_act_rows(g)
