@@ -27,6 +27,7 @@
 // the tile space, which keeps the A rows and W columns it shares inside
 // that XCD's L2.
 #include <atomic>
+#include <cmath>
 #include <type_traits>
 
 #include "common.hpp"
@@ -481,7 +482,11 @@ constexpr int kBufNT = 2;  // buffer access aux bits: non-temporal
 // One 64-column head of Q (WHICH 0), K (1) or V (2): blocks (2g, 2g+1) of the
 // wave, so lane column l32 holds head dims l32 and 32 + l32 -- exactly a
 // rotary pair. hc: the head's first column relative to the tile origin.
-template <int BLK_M, int BLK_N, int EPI, bool FULL, int WHICH>
+// QS: multiply Q by p.q_scale (skipped when the model folded it into the Q
+// weights, p.q_scale == 1, so the product would be exact anyway).
+// kEpiQkvSplit: the Q columns' weight scales and bias arrive already
+// multiplied by p.q_prescale (see the kernel's scale staging).
+template <int BLK_M, int BLK_N, int EPI, bool FULL, int WHICH, bool QS = true>
 __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc)[BLK_M][BLK_N], int g, int hc,
                                          int wr0, int lr0, int l32, const float* s_as, const float (&ws)[BLK_N],
                                          const float (&bs)[BLK_N], const float* s_cosT, const float* s_sinT, int m0,
@@ -520,7 +525,7 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
         if (!FULL && m0 + lr + u >= p.M) continue;
         float x1 = __builtin_fmaf(static_cast<float>(acc[i][2 * g][r]), asv[u] * ws[2 * g], bs[2 * g]);
         float x2 = __builtin_fmaf(static_cast<float>(acc[i][2 * g + 1][r]), asv[u] * ws[2 * g + 1], bs[2 * g + 1]);
-        if constexpr (WHICH == 0) {
+        if constexpr (WHICH == 0 && QS) {
           x1 *= p.q_scale;
           x2 *= p.q_scale;
         }
@@ -543,11 +548,9 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
           dst[0] = x1;
           dst[32] = x2;
         } else if constexpr (EPI == kEpiQkvSplit) {
-          if constexpr (WHICH == 0) {
-            x1 *= p.q_prescale;
-            x2 *= p.q_prescale;
-          }
-          const uint32_t w1 = split_f16_word(x1), w2 = split_f16_word(x2);
+          // Q: x already carries q_prescale (a power of two folded into the
+          // staged scales and bias: fma(acc, a*(w*2^e), b*2^e) and every later
+          // product and fma are the unfolded values times 2^e exactly).
           // Buffer stores relative to the tile's first row: the lane offset
           // lane_s (VGPR) plus the row's byte offset (SGPR).
           const __amdgpu_buffer_rsrc_t rows = tile_rsrc(reinterpret_cast<uint32_t*>(p.C_f32) +
@@ -555,14 +558,18 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
           const uint32_t soff = (static_cast<uint32_t>(wr0) + dr) * ldc * 4u;
           if constexpr (WHICH == 0) {
             // Q words, the rotary pair adjacent: one 8-byte store per lane.
+            const uint32_t w1 = split_f16_word(x1), w2 = split_f16_word(x2);
             __builtin_amdgcn_raw_buffer_store_b64(u32x2{w1, w2}, rows, lane_s, soff, kBufNT);
           } else {
             // K / V: the pair's fp16 hi parts in the hi plane, lo parts in
-            // the lo plane (d / 2 words further).
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(w2, w1, 0x05040100u), rows, lane_s, soff,
-                                                  kBufNT);
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(w2, w1, 0x07060302u), rows, lane_s,
-                                                  soff + dm * 2u, kBufNT);
+            // the lo plane (d / 2 words further), each pair converted at
+            // once (the values pinned in registers first, so the conversion
+            // rounds these fp32 values and no fused form of them).
+            asm("" : "+v"(x1), "+v"(x2));
+            uint32_t hw, lw;
+            split_pair(x1, x2, &hw, &lw);
+            __builtin_amdgcn_raw_buffer_store_b32(hw, rows, lane_s, soff, kBufNT);
+            __builtin_amdgcn_raw_buffer_store_b32(lw, rows, lane_s, soff + dm * 2u, kBufNT);
           }
         } else {
           // [M, d_model] outputs; column of the head inside its Q / K / V part.
@@ -626,7 +633,10 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
         const int hc = wn * BLK_N * 32 + g * 64;  // uniform: the wave index is
         if (!FULL && n0 + hc >= p.N) break;
         const int which = (n0 + hc) / p.d_model;
-        if (which == 0)
+        if (which == 0 && p.q_scale == 1.0f)
+          qkv_head<BLK_M, BLK_N, EPI, FULL, 0, false>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0,
+                                                      n0);
+        else if (which == 0)
           qkv_head<BLK_M, BLK_N, EPI, FULL, 0>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
         else if (which == 1)
           qkv_head<BLK_M, BLK_N, EPI, FULL, 1>(p, acc, g, hc, wr0, lr0, l32, s_as, ws, bs, s_cosT, s_sinT, m0, n0);
@@ -833,7 +843,14 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
       } else {
         const int c = t - BM, col = n0 + c;
         const bool ok = col < p.N;
-        const float w = ok ? p.w_scale[col] : 0.0f, b = (ok && p.bias) ? p.bias[col] : 0.0f;
+        float w = ok ? p.w_scale[col] : 0.0f, b = (ok && p.bias) ? p.bias[col] : 0.0f;
+        if constexpr (EPI == kEpiQkvSplit) {
+          // Q columns: q_prescale (a power of two) folded in here, exactly.
+          if (col < p.d_model) {
+            w *= p.q_prescale;
+            b *= p.q_prescale;
+          }
+        }
         s_ws[c] = w;
         s_bs[c] = b;
         if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(w) <= 0x1p60f) | !(__builtin_fabsf(b) <= 0x1p127f);
@@ -1304,6 +1321,10 @@ bool gemm_i8_pipelined_ok(const GemmI8Args& p) {
 
 hipError_t launch_gemm_i8_variant(const GemmI8Args& p, int epi, int variant, hipStream_t s) {
   if (p.M <= 0 || p.N <= 0) return hipSuccess;
+  // The split epilogue folds q_prescale into the staged Q scales, which is
+  // exact only for a power of two.
+  int e = 0;
+  if (epi == kEpiQkvSplit && std::frexp(p.q_prescale, &e) != 0.5f) return hipErrorInvalidValue;
   if (variant == 2) {
     if (!gemm_i8_pipelined_ok(p)) return hipErrorInvalidValue;
     return launch_v3(p, epi, s);
