@@ -301,7 +301,9 @@ __global__ __launch_bounds__(256) void rope_x86_kernel(float* __restrict__ x, in
 // AttentionVarlenAvx512 / RunOneHeadAvx512Impl (reference
 // src/kernels/attention.cpp:240-430, 770-811). One wave per (sequence, head,
 // 64 queries), one query per lane; the sequence's keys and values pass
-// through LDS 64 rows at a time. Per query, as the reference:
+// through LDS 16 rows at a time (8 KB per wave at head_dim 64, so the
+// register file, not the LDS, bounds the waves per CU). Per query, as the
+// reference:
 //   score_j = red16 of the 16 lanes of fma(q[d], k_j[d], acc) over d
 //   ascending in 16-wide steps (DotAvx512 and the 16-accumulator loop agree);
 //   max over all keys;
@@ -331,10 +333,10 @@ __device__ __forceinline__ float score_x86(const float (&q)[DH], const float* __
   return red16(acc);
 }
 
-constexpr int kX86Keys = 64;  // keys staged per LDS pass
+constexpr int kX86Keys = 16;  // keys staged per LDS pass (one 16-key chunk of the reference)
 
 template <int DH>
-__global__ __launch_bounds__(64) void attn_x86_kernel(const float* __restrict__ q, const float* __restrict__ k,
+__global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, int ld, const int* __restrict__ cu,
                                                       int heads, float* __restrict__ out, int ldo) {
   __shared__ __attribute__((aligned(16))) float ks[kX86Keys][DH];
@@ -359,16 +361,20 @@ __global__ __launch_bounds__(64) void attn_x86_kernel(const float* __restrict__ 
     }
   }
   const int Lfull = L & ~15;
-  // Stages rows [kc, kc + 64) of K (and V) into LDS; lane r copies row r.
+  // Stages rows [kc, kc + 16) of K (and V) into LDS, 16 bytes per lane per
+  // step: item t is float4 t % (DH / 4) of row t / (DH / 4). Rows past the
+  // sequence are not read (their LDS slots are never used).
   auto stage = [&](int kc, bool with_v) {
     __syncthreads();
-    const int j = kc + lane;
-    if (j < L) {
-      const size_t o = static_cast<size_t>(s0 + j) * ld + static_cast<size_t>(h) * DH;
+    constexpr int kItems = kX86Keys * DH / 4;
 #pragma unroll
-      for (int d4 = 0; d4 < DH / 4; ++d4) {
-        *reinterpret_cast<float4*>(&ks[lane][d4 * 4]) = *reinterpret_cast<const float4*>(k + o + d4 * 4);
-        if (with_v) *reinterpret_cast<float4*>(&vs[lane][d4 * 4]) = *reinterpret_cast<const float4*>(v + o + d4 * 4);
+    for (int t0 = 0; t0 < kItems; t0 += 64) {
+      const int t = t0 + lane;
+      const int r = t / (DH / 4), d4 = t % (DH / 4);
+      if ((kItems % 64 == 0 || t < kItems) && kc + r < L) {
+        const size_t o = static_cast<size_t>(s0 + kc + r) * ld + static_cast<size_t>(h) * DH + d4 * 4;
+        *reinterpret_cast<float4*>(&ks[r][d4 * 4]) = *reinterpret_cast<const float4*>(k + o);
+        if (with_v) *reinterpret_cast<float4*>(&vs[r][d4 * 4]) = *reinterpret_cast<const float4*>(v + o);
       }
     }
     __syncthreads();
