@@ -450,7 +450,19 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(
   const float inv = 1.0f / scale;
   const float* xr = x + static_cast<size_t>(row) * ldx;
   int8_t* qr = q + static_cast<size_t>(row) * ldq;
-  for (int c = lane; c < cols; c += 64) qr[c] = static_cast<int8_t>(quant_i8(xr[c], inv));
+  int c0 = 0;
+  if ((cols | ldx | ldq) % 4 == 0) {
+    // Four values per lane per step: one 16-byte load, quant_i8 of each
+    // (its NaN rule included), one packed 4-byte store.
+    for (int c = lane * 4; c < cols; c += 256) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + c);
+      *reinterpret_cast<uint32_t*>(qr + c) =
+          (static_cast<uint32_t>(quant_i8(v.x, inv)) & 0xffu) | ((static_cast<uint32_t>(quant_i8(v.y, inv)) & 0xffu) << 8) |
+          ((static_cast<uint32_t>(quant_i8(v.z, inv)) & 0xffu) << 16) | (static_cast<uint32_t>(quant_i8(v.w, inv)) << 24);
+    }
+    c0 = cols;
+  }
+  for (int c = c0 + lane; c < cols; c += 64) qr[c] = static_cast<int8_t>(quant_i8(xr[c], inv));
   for (int c = cols + lane; c < ldq; c += 64) qr[c] = 0;
   if (lane == 0) scales[row] = scale;
 }
@@ -461,8 +473,7 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
     m = fmaxf(m, fabsf(x[i]));
-  m = wave_max(m);
-  if ((threadIdx.x & 63) == 0) atomic_max_nonneg(absmax, m);
+  block_atomic_max_nonneg(absmax, m);
 }
 
 __global__ void fill_kernel(float* x, size_t n, float v) {
@@ -705,7 +716,7 @@ hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols, cons
 hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s) {
   if (n == 0) return hipSuccess;
   size_t g = (n + 255) / 256;
-  if (g > 4096) g = 4096;
+  if (g > 1024) g = 1024;  // four per CU: one atomic each
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
   return hipGetLastError();
 }

@@ -145,8 +145,10 @@ __device__ __forceinline__ float expf_glibc(float x) {
 // leftover 16-element blocks go to accumulator 0 (lanes 0..15), the last
 // d % 16 elements into a scalar sum. With resid, hidden += resid first
 // (ResidualAddInplace, written back). absmax (optional): atomic max of
-// |out| for the per-tensor activation scale. round16: the output rounded to
-// fp16 and back (RoundToFp16Inplace, reference src/model.cpp:912-930).
+// |out| for the per-tensor activation scale, one atomic per block (the
+// waves walk rows grid-stride, so a launch sends at most one per block of its
+// bounded grid). round16: the output rounded to fp16 and back
+// (RoundToFp16Inplace, reference src/model.cpp:912-930).
 template <int NB>
 __global__ __launch_bounds__(256) void layernorm_x86_kernel(float* __restrict__ x, const float* __restrict__ resid,
                                                              const float* __restrict__ gamma,
@@ -154,108 +156,112 @@ __global__ __launch_bounds__(256) void layernorm_x86_kernel(float* __restrict__ 
                                                              float* __restrict__ out, int rows, int d,
                                                              float* __restrict__ absmax, int round16) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  float* xr = x + static_cast<size_t>(row) * d;
-  const float* rr = resid ? resid + static_cast<size_t>(row) * d : nullptr;
-  const int nfull = d >> 6;
-  const int rem = d - (nfull << 6);
-  const int rem16 = rem >> 4;
-  const int tail = rem & 15;
-  float xv[NB];
-#pragma unroll
-  for (int t = 0; t < NB; ++t) {
-    if (t < nfull) {
-      float v = xr[(t << 6) + lane];
-      if (rr) {
-        v = v + rr[(t << 6) + lane];
-        xr[(t << 6) + lane] = v;
-      }
-      xv[t] = v;
-    }
-  }
-  float xrem = 0.0f;
-  if (lane < rem) {
-    xrem = xr[(nfull << 6) + lane];
-    if (rr) {
-      xrem = xrem + rr[(nfull << 6) + lane];
-      xr[(nfull << 6) + lane] = xrem;
-    }
-  }
-  const float inv_d = 1.0f / static_cast<float>(d);
-
-  // Pass 1: mean.
-  float s = 0.0f;
-#pragma unroll
-  for (int t = 0; t < NB; ++t)
-    if (t < nfull) s = s + xv[t];
-  for (int bb = 0; bb < rem16; ++bb) {
-    const float v = __shfl(xrem, (bb << 4) + (lane & 15));
-    if (lane < 16) s = s + v;
-  }
-  float tsum = 0.0f;
-  for (int i = 0; i < tail; ++i) tsum += __shfl(xrem, (rem16 << 4) + i);
-  float a = s + __shfl_down(s, 16);
-  float v16 = a + __shfl_down(a, 32);
-  const float mean = (__shfl(red16_lanes(v16), 0) + tsum) * inv_d;
-
-  // Pass 2: variance.
-  s = 0.0f;
-#pragma unroll
-  for (int t = 0; t < NB; ++t)
-    if (t < nfull) {
-      const float df = xv[t] - mean;
-      s = __builtin_fmaf(df, df, s);
-    }
-  for (int bb = 0; bb < rem16; ++bb) {
-    const float df = __shfl(xrem, (bb << 4) + (lane & 15)) - mean;
-    if (lane < 16) s = __builtin_fmaf(df, df, s);
-  }
-  float vtail = 0.0f;
-  for (int i = 0; i < tail; ++i) {
-    const float df = __shfl(xrem, (rem16 << 4) + i) - mean;
-    vtail = __builtin_fmaf(df, df, vtail);
-  }
-  a = s + __shfl_down(s, 16);
-  v16 = a + __shfl_down(a, 32);
-  const float ve = __builtin_fmaf(__shfl(red16_lanes(v16), 0) + vtail, inv_d, eps);
-  const float inv_std = static_cast<float>(1.0 / static_cast<double>(static_cast<float>(sqrt(static_cast<double>(ve)))));
-
-  // Pass 3.
-  float* yr = out + static_cast<size_t>(row) * d;
   float m = 0.0f;
-  auto emit = [&](int c, float xc) {
-    float y = __builtin_fmaf((xc - mean) * inv_std, gamma[c], beta[c]);
-    if (round16) y = static_cast<float>(static_cast<_Float16>(y));
-    yr[c] = y;
-    m = fmaxf(m, fabsf(y));
-  };
+  for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += gridDim.x * 4) {
+    float* xr = x + static_cast<size_t>(row) * d;
+    const float* rr = resid ? resid + static_cast<size_t>(row) * d : nullptr;
+    const int nfull = d >> 6;
+    const int rem = d - (nfull << 6);
+    const int rem16 = rem >> 4;
+    const int tail = rem & 15;
+    float xv[NB];
 #pragma unroll
-  for (int t = 0; t < NB; ++t)
-    if (t < nfull) emit((t << 6) + lane, xv[t]);
-  if (lane < rem) emit((nfull << 6) + lane, xrem);
-  if (absmax) {
-    m = wave_max(m);
-    if (lane == 0) atomic_max_nonneg(absmax, m);
+    for (int t = 0; t < NB; ++t) {
+      if (t < nfull) {
+        float v = xr[(t << 6) + lane];
+        if (rr) {
+          v = v + rr[(t << 6) + lane];
+          xr[(t << 6) + lane] = v;
+        }
+        xv[t] = v;
+      }
+    }
+    float xrem = 0.0f;
+    if (lane < rem) {
+      xrem = xr[(nfull << 6) + lane];
+      if (rr) {
+        xrem = xrem + rr[(nfull << 6) + lane];
+        xr[(nfull << 6) + lane] = xrem;
+      }
+    }
+    const float inv_d = 1.0f / static_cast<float>(d);
+
+    // Pass 1: mean.
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+      if (t < nfull) s = s + xv[t];
+    for (int bb = 0; bb < rem16; ++bb) {
+      const float v = __shfl(xrem, (bb << 4) + (lane & 15));
+      if (lane < 16) s = s + v;
+    }
+    float tsum = 0.0f;
+    for (int i = 0; i < tail; ++i) tsum += __shfl(xrem, (rem16 << 4) + i);
+    float a = s + __shfl_down(s, 16);
+    float v16 = a + __shfl_down(a, 32);
+    const float mean = (__shfl(red16_lanes(v16), 0) + tsum) * inv_d;
+
+    // Pass 2: variance.
+    s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+      if (t < nfull) {
+        const float df = xv[t] - mean;
+        s = __builtin_fmaf(df, df, s);
+      }
+    for (int bb = 0; bb < rem16; ++bb) {
+      const float df = __shfl(xrem, (bb << 4) + (lane & 15)) - mean;
+      if (lane < 16) s = __builtin_fmaf(df, df, s);
+    }
+    float vtail = 0.0f;
+    for (int i = 0; i < tail; ++i) {
+      const float df = __shfl(xrem, (rem16 << 4) + i) - mean;
+      vtail = __builtin_fmaf(df, df, vtail);
+    }
+    a = s + __shfl_down(s, 16);
+    v16 = a + __shfl_down(a, 32);
+    const float ve = __builtin_fmaf(__shfl(red16_lanes(v16), 0) + vtail, inv_d, eps);
+    const float sd = static_cast<float>(sqrt(static_cast<double>(ve)));
+    const float inv_std = static_cast<float>(1.0 / static_cast<double>(sd));
+
+    // Pass 3.
+    float* yr = out + static_cast<size_t>(row) * d;
+    auto emit = [&](int c, float xc) {
+      float y = __builtin_fmaf((xc - mean) * inv_std, gamma[c], beta[c]);
+      if (round16) y = static_cast<float>(static_cast<_Float16>(y));
+      yr[c] = y;
+      m = fmaxf(m, fabsf(y));
+    };
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+      if (t < nfull) emit((t << 6) + lane, xv[t]);
+    if (lane < rem) emit((nfull << 6) + lane, xrem);
   }
+  if (absmax) block_atomic_max_nonneg(absmax, m);
 }
 
 // --------------------------------------------------------------- GELU
-// GeluAvx512 elementwise; in place allowed. absmax (optional): atomic max of
-// |out|.
+// GeluAvx512 elementwise; in place allowed. vec: x and out 16-byte aligned,
+// four values per thread per step. absmax (optional): atomic max of |out|,
+// one per block.
 __global__ __launch_bounds__(256) void gelu_x86_kernel(const float* __restrict__ x, float* __restrict__ out, size_t n,
-                                                       float* __restrict__ absmax) {
+                                                       float* __restrict__ absmax, int vec) {
   float m = 0.0f;
-  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
-       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  const size_t first = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  const size_t n4 = vec ? n / 4 : 0;
+  for (size_t i = first; i < n4; i += stride) {
+    const float4 v = reinterpret_cast<const float4*>(x)[i];
+    const float4 y = make_float4(gelu_x86(v.x), gelu_x86(v.y), gelu_x86(v.z), gelu_x86(v.w));
+    reinterpret_cast<float4*>(out)[i] = y;
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  }
+  for (size_t i = n4 * 4 + first; i < n; i += stride) {
     const float y = gelu_x86(x[i]);
     out[i] = y;
     m = fmaxf(m, fabsf(y));
   }
-  if (absmax) {
-    m = wave_max(m);
-    if ((threadIdx.x & 63) == 0) atomic_max_nonneg(absmax, m);
-  }
+  if (absmax) block_atomic_max_nonneg(absmax, m);
 }
 
 // Elementwise expf_glibc (checks of the restated std::exp).
@@ -517,7 +523,7 @@ int grid_for(size_t n, int block, int cap) {
 hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma, const float* beta, float eps,
                                 float* out, int rows, int d, float* absmax, int round16, hipStream_t s) {
   if (rows <= 0 || d <= 0) return hipSuccess;
-  const dim3 grid((rows + 3) / 4), block(256);
+  const dim3 grid(grid_for(static_cast<size_t>(rows), 4, 1024)), block(256);  // rows walked grid-stride
   const int nb = d >> 6;
   if (nb <= 5)
     hipLaunchKernelGGL(layernorm_x86_kernel<5>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, d, absmax,
@@ -535,7 +541,9 @@ hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma
 
 hipError_t launch_gelu_x86(const float* x, float* out, size_t n, float* absmax, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(gelu_x86_kernel, dim3(grid_for(n, 256, 8192)), dim3(256), 0, s, x, out, n, absmax);
+  const int vec = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+  hipLaunchKernelGGL(gelu_x86_kernel, dim3(grid_for(vec ? n / 4 : n, 256, 1024)), dim3(256), 0, s, x, out, n, absmax,
+                     vec);
   return hipGetLastError();
 }
 
