@@ -92,19 +92,24 @@ __device__ __forceinline__ void atomic_max_nonneg(float* addr, float v) {
   atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
 }
 
-// atomic_max_nonneg of the maximum of v over a 256-thread block: the four
+// atomic_max_nonneg of the maximum of v over a block of WAVES waves: the
 // waves' maxima meet in LDS and one lane issues the atomic. Atomics on one
 // address serialise in L2, so a launch that sends one per block instead of
 // one per wave (and has a bounded grid) spends correspondingly less time on
 // them; the maximum itself does not depend on the order. Every thread of the
 // block must call it.
+template <int WAVES = 4>
 __device__ __forceinline__ void block_atomic_max_nonneg(float* addr, float v) {
-  __shared__ float s_wave_max[4];
+  __shared__ float s_wave_max[WAVES];
   v = wave_max(v);
   if ((threadIdx.x & 63) == 0) s_wave_max[threadIdx.x >> 6] = v;
   __syncthreads();
-  if (threadIdx.x == 0)
-    atomic_max_nonneg(addr, fmaxf(fmaxf(s_wave_max[0], s_wave_max[1]), fmaxf(s_wave_max[2], s_wave_max[3])));
+  if (threadIdx.x == 0) {
+    float m = s_wave_max[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_wave_max[w]);
+    atomic_max_nonneg(addr, m);
+  }
 }
 
 // Exact-erf GELU: x * 0.5 * (1 + erf(x / sqrt(2))). erff is the HIP

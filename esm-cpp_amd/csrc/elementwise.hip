@@ -66,8 +66,14 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
     float* scales, int round16, SplitResid split = SplitResid()) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  // With a per-tensor absmax every wave of the block joins the block's
+  // reduction at the end: a wave past the last row recomputes that row and
+  // stores nothing. Otherwise such a wave leaves at once.
+  const int row0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const bool live = row0 < rows;
+  const bool reduce = !QUANT && tensor_absmax;
+  if (!live && !reduce) return;
+  const int row = live ? row0 : rows - 1;
   float* xr = x + static_cast<size_t>(row) * d;
   float4 v[NV];
   load_row_vec<NV>(xr, d, lane, v);
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
       v[j].z += r[j].z;
       v[j].w += r[j].w;
       const int c = (j * 64 + lane) * 4;
-      if (c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
+      if (live && c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
     }
   }
   float sum = 0.f;
@@ -143,7 +149,8 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     v[j] = y;
     if (c < d) {
       amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-      if constexpr (!QUANT) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = y;
+      if constexpr (!QUANT)
+        if (live) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = y;
     }
   }
   if constexpr (QUANT) {
@@ -159,9 +166,8 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     }
     for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
     if (lane == 0) scales[row] = scale;
-  } else if (tensor_absmax) {
-    amax = wave_max(amax);
-    if (lane == 0) atomic_max_nonneg(tensor_absmax, amax);
+  } else if (reduce) {
+    block_atomic_max_nonneg(tensor_absmax, live ? amax : 0.0f);
   }
 }
 
@@ -171,10 +177,14 @@ __global__ __launch_bounds__(256) void layernorm_any_kernel(
     const float* __restrict__ beta, float eps, float* __restrict__ out,
     int rows, int d, float* tensor_absmax, int round16) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  // As layernorm_vec_kernel: with a per-tensor absmax a wave past the last
+  // row recomputes that row, stores nothing and joins the block's reduction.
+  const int row0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const bool live = row0 < rows;
+  if (!live && !tensor_absmax) return;
+  const int row = live ? row0 : rows - 1;
   float* xr = x + static_cast<size_t>(row) * d;
-  if (resid) {
+  if (resid && live) {
     const float* rr = resid + static_cast<size_t>(row) * d;
     for (int c = lane; c < d; c += 64) xr[c] += rr[c];
   }
@@ -193,13 +203,10 @@ __global__ __launch_bounds__(256) void layernorm_any_kernel(
   for (int c = lane; c < d; c += 64) {
     float y = (xr[c] - mean) * inv_std * gamma[c] + beta[c];
     if (round16) y = static_cast<float>(static_cast<_Float16>(y));
-    yr[c] = y;
+    if (live) yr[c] = y;
     amax = fmaxf(amax, fabsf(y));
   }
-  if (tensor_absmax) {
-    amax = wave_max(amax);
-    if (lane == 0) atomic_max_nonneg(tensor_absmax, amax);
-  }
+  if (tensor_absmax) block_atomic_max_nonneg(tensor_absmax, live ? amax : 0.0f);
 }
 
 template <int KIND>

@@ -787,10 +787,8 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
           }
         }
       if constexpr (MAX) {
-        if (p.tensor_absmax) {
-          tmax = wave_max(tmax);
-          if ((threadIdx.x & 63) == 0) atomic_max_nonneg(p.tensor_absmax, tmax);
-        }
+        // One atomic per workgroup (every wave reaches this point).
+        if (p.tensor_absmax) block_atomic_max_nonneg<Tile<BLK_M, BLK_N>::kWaves>(p.tensor_absmax, tmax);
       }
     }
   }
