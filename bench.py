@@ -12,9 +12,10 @@ dominant kernel's average launch duration for the roofline line.
 
 Extra records (same JSON line, "workloads"): config 4's uniform 8x256 batch
 and config 5 (ESM-2 3B, 36 layers, 64 sequences of log-uniform 50..1024
-tokens), each with residues/s and its dominant GEMM's roofline.
+tokens), each with residues/s and its dominant GEMM's roofline; the headline
+batch with the reference's per-tensor activation scales (default numerics).
 
-A third record times the x86-exact numerics (ESM_GFX950_NUMERICS_X86_AVX512,
+A further record times the x86-exact numerics (ESM_GFX950_NUMERICS_X86_AVX512,
 or _X86_AMX on an AMX host) on the headline batch: the mode whose logits
 equal the reference CPU path's bit for bit.
 
@@ -197,8 +198,8 @@ def x86_workload(dev, weights, batch, cfg, isa, args):
             "tokens_per_s": round(T / (ms * 1e-3), 1), "streams": used, "kernel_sites": sites}
 
 
-def extra_workload(dev, name, cfg, weights, batch, args):
-    model = eg.Model(dev, weights, int8=True, act_mode=eg.ACT_PER_TOKEN)
+def extra_workload(dev, name, cfg, weights, batch, args, act_mode=eg.ACT_PER_TOKEN):
+    model = eg.Model(dev, weights, int8=True, act_mode=act_mode)
     try:
         ms, _, sites, used = measure(dev, model, batch, cfg, args.extra_steps, 2, args.parts)
     finally:
@@ -207,7 +208,8 @@ def extra_workload(dev, name, cfg, weights, batch, args):
     return {"workload": name, "tokens": T, "residues": batch.residues, "sequences": int(len(batch.lengths)),
             "ms_per_step": round(ms, 3), "value": round(batch.residues / (ms * 1e-3), 1), "unit": "residues/s",
             "tokens_per_s": round(T / (ms * 1e-3), 1), "streams": used, "kernel_sites": sites,
-            "roofline": roofline_of(sites, T, cfg, batch, name.split(":")[0])}
+            "roofline": roofline_of(sites, T, cfg, batch, name.split(":")[0],
+                                    per_token=act_mode == eg.ACT_PER_TOKEN)}
 
 
 def host_cpu():
@@ -402,6 +404,15 @@ def main():
                                         syn.config5_batch(), args))
         del w5
         log(f"extra {workloads[-1]['workload']}: {workloads[-1]['ms_per_step']} ms")
+        if args.workload == "varlen" and mode == eg.ACT_PER_TOKEN:
+            # The reference's own activation scaling (one dynamic scale per
+            # tensor), default numerics: one sequence group (the scale spans
+            # the batch).
+            workloads.append(extra_workload(
+                dev, "per-tensor: config4 varlen, ESM-2-650M W8A8, per-tensor activation scales (the reference's "
+                     "dynamic per-tensor quantisation), default numerics", cfg, weights, batch, args,
+                act_mode=eg.ACT_PER_TENSOR))
+            log(f"extra {workloads[-1]['workload']}: {workloads[-1]['ms_per_step']} ms")
 
     cpu = par = None
     sample = cpu_logits = isa = None

@@ -513,6 +513,103 @@ __global__ __launch_bounds__(256) void linear_x86_kernel(const float* __restrict
   }
 }
 
+// The same sums with 32 x 32 outputs per 256-thread workgroup. Thread t owns
+// the reference's accumulator lanes 4q .. 4q + 3 (q = t % 4) of a 4 x 4
+// block of outputs (rows 4 (b / 8) + i, columns 4 (b % 8) + j, b = t / 4), so
+// each 16-wide K step reads eight 16-byte LDS words for 64 FMAs instead of
+// one word per FMA; every accumulator lane still takes its products in K
+// order. The four threads of a block then add their lanes in red16's order
+// (lanes l and l + 8 first: threads q and q ^ 2; then l and l + 4: q and
+// q ^ 1), and thread q = 0 stores the block.
+template <int EPI>
+__global__ __launch_bounds__(256) void linear_x86_blk_kernel(const float* __restrict__ A, int lda,
+                                                             const float* __restrict__ W, int ldw,
+                                                             const float* __restrict__ bias, float* __restrict__ C,
+                                                             int ldc, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) float as[32][kLinKc + 4];
+  __shared__ __attribute__((aligned(16))) float ws[32][kLinKc + 4];
+  const int t = threadIdx.x, q = t & 3, b = t >> 2, bm = b >> 3, bn = b & 7;
+  const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  float acc[4][4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][j][e] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += kLinKc) {
+    __syncthreads();
+    // 256 threads copy 32 rows x 64 columns of A and of W (8 floats each);
+    // columns past K read as zero (fma(0, 0, acc) == acc).
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = t + 256 * u;
+      const int r = idx >> 4, c = (idx & 15) * 4;
+      const int ar = min(m0 + r, M - 1), wr = min(n0 + r, N - 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kk = k0 + c + e;
+        as[r][c + e] = kk < K ? A[static_cast<size_t>(ar) * lda + kk] : 0.0f;
+        ws[r][c + e] = kk < K ? W[static_cast<size_t>(wr) * ldw + kk] : 0.0f;
+      }
+    }
+    __syncthreads();
+    const int steps = min(kLinKc, K - k0);
+    for (int s0 = 0; s0 < steps; s0 += 16) {
+      float4 a[4], w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(&as[4 * bm + i][s0 + 4 * q]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const float4*>(&ws[4 * bn + j][s0 + 4 * q]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j][0] = __builtin_fmaf(a[i].x, w[j].x, acc[i][j][0]);
+          acc[i][j][1] = __builtin_fmaf(a[i].y, w[j].y, acc[i][j][1]);
+          acc[i][j][2] = __builtin_fmaf(a[i].z, w[j].z, acc[i][j][2]);
+          acc[i][j][3] = __builtin_fmaf(a[i].w, w[j].w, acc[i][j][3]);
+        }
+    }
+  }
+  // red16: t3[l] = v[l + 8] + v[l] (l < 8), t6[l] = t3[l + 4] + t3[l]
+  // (l < 4), then (t6[0] + t6[2]) + (t6[1] + t6[3]). Thread q holds lanes
+  // 4q + e; after the first exchange thread 0 holds t3[0..3] and thread 1
+  // t3[4..7], after the second thread 0 holds t6[0..3].
+  float out[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float t3[4], t6[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t3[e] = __shfl_xor(acc[i][j][e], 2, 4) + acc[i][j][e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t6[e] = __shfl_xor(t3[e], 1, 4) + t3[e];
+      out[i][j] = (t6[0] + t6[2]) + (t6[1] + t6[3]);
+    }
+  if (q != 0) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + 4 * bm + i;
+    if (m >= M) break;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + 4 * bn + j;
+      if (n >= N) break;
+      const float y = (bias ? bias[n] : 0.0f) + out[i][j];
+      float* c = C + static_cast<size_t>(m) * ldc + n;
+      if constexpr (EPI == kF32Gelu) {
+        *c = gelu_x86(y);
+      } else if constexpr (EPI == kF32Resid) {
+        *c = *c + y;
+      } else {
+        *c = y;
+      }
+    }
+  }
+}
+
 int grid_for(size_t n, int block, int cap) {
   const size_t g = (n + block - 1) / block;
   return static_cast<int>(g < static_cast<size_t>(cap) ? g : cap);
@@ -580,6 +677,22 @@ hipError_t launch_attention_x86(const float* q, const float* k, const float* v, 
 hipError_t launch_linear_x86(const float* A, int lda, const float* W, int ldw, const float* bias, float* C, int ldc,
                              int M, int N, int K, int epi, hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
+  if (M >= 32 && N >= 32) {
+    const dim3 grid((N + 31) / 32, (M + 31) / 32), block(256);
+    switch (epi) {
+      case kF32Store:
+        hipLaunchKernelGGL(linear_x86_blk_kernel<kF32Store>, grid, block, 0, s, A, lda, W, ldw, bias, C, ldc, M, N, K);
+        break;
+      case kF32Gelu:
+        hipLaunchKernelGGL(linear_x86_blk_kernel<kF32Gelu>, grid, block, 0, s, A, lda, W, ldw, bias, C, ldc, M, N, K);
+        break;
+      case kF32Resid:
+        hipLaunchKernelGGL(linear_x86_blk_kernel<kF32Resid>, grid, block, 0, s, A, lda, W, ldw, bias, C, ldc, M, N, K);
+        break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid((N + 15) / 16, (M + 15) / 16), block(256);
   switch (epi) {
     case kF32Store:
