@@ -307,14 +307,18 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_kernel(
 }
 
 // The same pass over the INT8 GEMM's 24-bit fc1 output (kEpiF32R24): a
-// high plane xh of bits 31..16 and a low plane xl of bits 15..8, in which
-// stored position 2 i + j of each aligned 64-column group holds column
-// 32 j + i. WAVES waves share a row (1: four rows per block; 2: two rows;
-// 4: one row; several waves' maxima meet in LDS), each wave NV * 512 stored
-// positions, eight
-// consecutive ones per lane per step: one 16-byte high and one 8-byte low
-// load give columns 4 k .. 4 k + 3 and 32 + 4 k .. (k = position / 8 within
-// the group), whose int8 values go out as two 4-byte words. cols % 64 == 0.
+// high plane xh of bits 31..16 (row pitch ldx) and a low plane xl of bits
+// 15..8 that interleaves row pairs (byte (r & ~1) ldx + 4 (p / 2) + 2 (r & 1)
+// + (p & 1) holds row r, stored position p); stored position 2 i + j of each
+// aligned 64-column group holds column 32 j + i. WAVES waves share a row (1:
+// four rows per block; 2: two rows; 4: one row, several waves' maxima
+// meeting in LDS), each wave NV * 512 stored positions, eight consecutive
+// ones per lane per step: one 16-byte high load, and one 16-byte low load
+// that holds them for both rows of the pair (the pair's two rows are read
+// by the same block, or for WAVES 4 by two blocks on the same XCD, so the
+// line comes from HBM once), give columns 4 k .. 4 k + 3 and 32 + 4 k ..
+// (k = position / 8 within the group), whose int8 values go out as two
+// 4-byte words. cols % 64 == 0.
 template <int NV, int WAVES>
 __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
     const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl, int ldx, int rows, int cols,
@@ -322,22 +326,27 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
   static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4, "one, two or four waves per row");
   __shared__ float s_max[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = blockIdx.x * (kRowsPerBlock / WAVES) + wave / WAVES;
+  // WAVES 4 (one row per block): blocks 16 g + 8 h + x take row 16 g + 2 x +
+  // h, so a row pair's two blocks land on XCD x (the dispatcher sends block
+  // b to XCD b mod 8) and share that XCD's L2.
+  const int row = WAVES == 4 ? (blockIdx.x & ~15) + 2 * (blockIdx.x & 7) + ((blockIdx.x >> 3) & 1)
+                             : blockIdx.x * (kRowsPerBlock / WAVES) + wave / WAVES;
   if (WAVES == 1 && row >= rows) return;
   // Several waves per row: every wave reaches the barrier below; a row past
   // the end reads row 0 and stores nothing.
   const bool live = row < rows;
   const int part = wave % WAVES;
-  const uint16_t* hr = xh + static_cast<size_t>(live ? row : 0) * ldx;
-  const uint8_t* lr = xl + static_cast<size_t>(live ? row : 0) * ldx;
-  uint4 hv[NV];
-  uint2 lv[NV];
+  const int rr = live ? row : 0;
+  const uint16_t* hr = xh + static_cast<size_t>(rr) * ldx;
+  const uint8_t* lr = xl + static_cast<size_t>(rr & ~1) * ldx;
+  const uint32_t odd = static_cast<uint32_t>(rr & 1);
+  uint4 hv[NV], lv[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int p0 = (part * NV + j) * 512 + lane * 8;
     const int pc = p0 < cols ? p0 : 0;  // in bounds; zeroed below
     hv[j] = *reinterpret_cast<const uint4*>(hr + pc);
-    lv[j] = *reinterpret_cast<const uint2*>(lr + pc);
+    lv[j] = *reinterpret_cast<const uint4*>(lr + 2 * pc);
   }
   float v[NV][8];
   float amax = 0.f;
@@ -345,13 +354,14 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
   for (int j = 0; j < NV; ++j) {
     const bool ok = (part * NV + j) * 512 + lane * 8 < cols;
     const uint32_t hw[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
-    const uint32_t lw[2] = {lv[j].x, lv[j].y};
+    const uint32_t lw[4] = {lv[j].x, lv[j].y, lv[j].z, lv[j].w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      // bytes: 0, the low plane's byte e % 4, the high plane's 16 bits of e
-      const uint32_t sel = 0x0cu | (static_cast<uint32_t>(e & 3) << 8) | ((4u + 2u * (e & 1)) << 16) |
+      // bytes: 0, this row's low byte of position e (word e / 2, byte
+      // (e & 1) + 2 odd), the high plane's 16 bits of e
+      const uint32_t sel = 0x0cu | ((static_cast<uint32_t>(e & 1) + 2u * odd) << 8) | ((4u + 2u * (e & 1)) << 16) |
                            ((5u + 2u * (e & 1)) << 24);
-      const float x = __uint_as_float(__builtin_amdgcn_perm(hw[e >> 1], lw[e >> 2], sel));
+      const float x = __uint_as_float(__builtin_amdgcn_perm(hw[e >> 1], lw[e >> 1], sel));
       v[j][e] = ok ? gelu2_as(x) : 0.0f;
       amax = fmaxf(amax, fabsf(v[j][e]));
     }
@@ -498,16 +508,19 @@ __global__ void observe_gather_kernel(const float* __restrict__ x, const uint32_
   out[w] = fabsf(v);
 }
 
-// The same over kEpiF32R24's planes (xh bits 31..16, xl bits 15..8, row
-// pitch cols; stored position 2 i + j of each 64-column group holds column
-// 32 j + i): |GELU(x)| of the 24-bit values the GELU + quantisation pass reads.
+// The same over kEpiF32R24's planes (xh bits 31..16 with row pitch cols;
+// xl bits 15..8 with row pairs interleaved; stored position 2 i + j of each
+// 64-column group holds column 32 j + i): |GELU(x)| of the 24-bit values the
+// GELU + quantisation pass reads.
 __global__ void observe_gather_r24_kernel(const uint16_t* __restrict__ xh, const uint8_t* __restrict__ xl, int cols,
                                           const uint32_t* __restrict__ pos, int count, float* __restrict__ out) {
   const int w = blockIdx.x * blockDim.x + threadIdx.x;
   if (w >= count) return;
   const uint32_t i = pos[w], r = i / static_cast<uint32_t>(cols), c = i - r * static_cast<uint32_t>(cols);
-  const size_t at = static_cast<size_t>(r) * cols + (c & ~63u) + 2u * (c & 31u) + ((c >> 5) & 1u);
-  const float v = __uint_as_float((static_cast<uint32_t>(xh[at]) << 16) | (static_cast<uint32_t>(xl[at]) << 8));
+  const uint32_t p = (c & ~63u) + 2u * (c & 31u) + ((c >> 5) & 1u);  // stored position of column c
+  const size_t at = static_cast<size_t>(r) * cols + p;
+  const size_t lo = static_cast<size_t>(r & ~1u) * cols + 4u * (p >> 1) + 2u * (r & 1u) + (p & 1u);
+  const float v = __uint_as_float((static_cast<uint32_t>(xh[at]) << 16) | (static_cast<uint32_t>(xl[lo]) << 8));
   out[w] = fabsf(0.5f * gelu2_as(v));
 }
 
@@ -687,8 +700,8 @@ hipError_t launch_gelu_quant_rows_r24(const uint16_t* xh, const uint8_t* xl, int
     hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<10, 1>), rows_grid(rows), b, 0, s, xh, xl, ldx, rows, cols, q, ldq,
                        scales);
   else
-    hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<5, 4>), dim3(rows), b, 0, s, xh, xl, ldx, rows, cols, q, ldq,
-                       scales);
+    hipLaunchKernelGGL((gelu_quant_rows_r24_kernel<5, 4>), dim3((rows + 15) & ~15), b, 0, s, xh, xl, ldx, rows, cols,
+                       q, ldq, scales);
   return hipGetLastError();
 }
 

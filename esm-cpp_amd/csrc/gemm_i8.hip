@@ -646,17 +646,20 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
       return;
     } else if constexpr (EPI == kEpiF32R24) {
       // The lane's two columns (l32 and 32 + l32 of the wave's 64) round to
-      // 24 bits (+0x80, then the top three bytes) and go out as one 4-byte
-      // word of their high halves and one 2-byte word of their low bytes, at
-      // stored positions 2 l32 and 2 l32 + 1 of the group: whole 128-byte
-      // rows of the high plane per half-wave.
+      // 24 bits (+0x80, then the top three bytes). Their high halves go out
+      // as one 4-byte word at stored positions 2 l32, 2 l32 + 1 of the group:
+      // whole 128-byte rows of the high plane per half-wave. The low plane
+      // interleaves row pairs (rows 2k and 2k + 1 share 2 ldc bytes; byte
+      // (r & ~1) ldc + 4 (p / 2) + 2 (r & 1) + (p & 1) holds row r, stored
+      // position p), so the lane's rows R and R + 1 (R even) go out as one
+      // 4-byte word and each half-wave store writes a whole 128-byte line.
       static_assert(BLK_N == 2, "the 24-bit layout pairs a lane's two 32-column blocks");
       const int gc = wn * 64;  // the wave's column group inside the tile
       if (!FULL && n0 + gc >= p.N) return;
       const __amdgpu_buffer_rsrc_t rh = tile_rsrc(p.C_f16 + static_cast<size_t>(m0) * ldc + n0 + gc);
-      const __amdgpu_buffer_rsrc_t rl = tile_rsrc(p.C_u8 + static_cast<size_t>(m0) * ldc + n0 + gc);
+      const __amdgpu_buffer_rsrc_t rl = tile_rsrc(p.C_u8 + static_cast<size_t>(m0) * ldc + 2 * (n0 + gc));
       const uint32_t lane_h = (static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32)) * 2u;
-      const uint32_t lane_l = static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(2 * l32);
+      const uint32_t lane_l = static_cast<uint32_t>(hi * 4) * ldc + static_cast<uint32_t>(4 * l32);
       // A NaN's bit pattern must not take the rounding add (it could carry
       // into the sign or leave an infinity). fma(float(acc), a_scale *
       // w_scale, bias) can be NaN only when a scale or bias is not finite or
@@ -672,21 +675,32 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
             const float4 as4 = *reinterpret_cast<const float4*>(s_as + lr);
             const float asv[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int r = 4 * q + u;
-              if (!FULL && m0 + lr + u >= p.M) continue;
-              const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
-              const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
-              uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
-              if constexpr (decltype(fix_nan)::value) {
-                b0 = __builtin_isnan(v0) ? 0x7fc00000u : b0;
-                b1 = __builtin_isnan(v1) ? 0x7fc00000u : b1;
+            for (int u2 = 0; u2 < 4; u2 += 2) {
+              uint32_t lo[2];  // the low bytes of rows R and R + 1 at positions 2 l32, 2 l32 + 1
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {
+                const int u = u2 + h, r = 4 * q + u;
+                const float v0 = __builtin_fmaf(static_cast<float>(acc[i][0][r]), asv[u] * ws[0], bs[0]);
+                const float v1 = __builtin_fmaf(static_cast<float>(acc[i][1][r]), asv[u] * ws[1], bs[1]);
+                uint32_t b0 = __float_as_uint(v0) + 0x80u, b1 = __float_as_uint(v1) + 0x80u;
+                if constexpr (decltype(fix_nan)::value) {
+                  b0 = __builtin_isnan(v0) ? 0x7fc00000u : b0;
+                  b1 = __builtin_isnan(v1) ? 0x7fc00000u : b1;
+                }
+                lo[h] = __builtin_amdgcn_perm(b1, b0, 0x0c0c0501u);
+                const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
+                if (FULL || m0 + lr + u < p.M)
+                  __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(b1, b0, 0x07060302u), rh, lane_h,
+                                                        R * ldc * 2u, kBufNT);
               }
-              const uint32_t R = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u);
-              __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(b1, b0, 0x07060302u), rh, lane_h,
-                                                    R * ldc * 2u, kBufNT);
-              __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(__builtin_amdgcn_perm(b1, b0, 0x0c0c0501u)),
-                                                    rl, lane_l, R * ldc, kBufNT);
+              const uint32_t R0 = static_cast<uint32_t>(wr0 + i * 32 + q * 8 + u2);
+              if (FULL || m0 + lr + u2 + 1 < p.M) {
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_amdgcn_perm(lo[1], lo[0], 0x05040100u), rl, lane_l,
+                                                      R0 * ldc, kBufNT);
+              } else if (m0 + lr + u2 < p.M) {
+                // The last row of an odd row count: its own two bytes only.
+                __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(lo[0]), rl, lane_l, R0 * ldc, kBufNT);
+              }
             }
           }
       };

@@ -25,10 +25,13 @@ enum GemmEpilogue : int {
   kEpiF32R24 = 8,     // kEpiF32's value rounded to its top 24 bits (sign,
                       // exponent, 15 mantissa bits; nearest, ties away;
                       // NaN -> the quiet NaN 0x7fc00000):
-                      // bits 31..16 to C_f16 [M, ldc], bits 15..8 to C_u8
-                      // [M, ldc]; in each aligned group of 64 columns, stored
-                      // position 2 i + j holds column 32 j + i (i < 32, j < 2).
-                      // Pipelined kernel only; N % 64 == 0.
+                      // bits 31..16 to C_f16 [M, ldc], bits 15..8 to C_u8;
+                      // in each aligned group of 64 columns, stored position
+                      // 2 i + j holds column 32 j + i (i < 32, j < 2). C_u8
+                      // interleaves row pairs: byte (r & ~1) ldc + 4 (p / 2)
+                      // + 2 (r & 1) + (p & 1) holds row r, position p, so it
+                      // spans (M + (M & 1)) ldc bytes. Pipelined kernel only;
+                      // N % 64 == 0.
 };
 
 // Split-fp16 word of an fp32 value x: low half fp16(x), high half

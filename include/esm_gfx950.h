@@ -180,8 +180,10 @@ int esm_gfx950_linear_i8_q(esm_gfx950_ctx* ctx, const int8_t* A, int lda, const 
  * fma(float(acc), a_scale[m] * w_scale[n], bias[n]) is rounded to its top 24
  * bits (0x80 added to the bit pattern, the low byte cleared: nearest, ties
  * away from zero; NaN becomes the quiet NaN 0x7fc00000) and stored as two
- * planes, inter_hi uint16 [M, N] (bits 31..16) and inter_lo uint8 [M, N]
- * (bits 15..8), in which stored position 64 g + 2 i + j holds column
+ * planes, inter_hi uint16 [M, N] (bits 31..16) and inter_lo uint8 of
+ * (M + (M & 1)) * N bytes (bits 15..8, row pairs interleaved: byte
+ * (m & ~1) N + 4 (p / 2) + 2 (m & 1) + (p & 1) holds row m, position p), in
+ * both of which stored position p = 64 g + 2 i + j holds column
  * 64 g + 32 j + i; the GELU + quantisation pass reads them and writes q int8
  * [M, ldq] (zero past N) and q_scale fp32 [M]. A int8 [M, lda], a_scale
  * fp32 [M], bias fp32 [N] or NULL; all device pointers. Requires N % 64 == 0,

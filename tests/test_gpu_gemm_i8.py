@@ -225,8 +225,13 @@ def test_gelu_quantize_act_rejects_bad_shapes(dev):
 
 def _planes_to_f32(hi, lo):
     """The 24-bit intermediate's two planes back in column order: stored
-    position 64 g + 2 i + j holds column 64 g + 32 j + i."""
+    position p = 64 g + 2 i + j holds column 64 g + 32 j + i; the low plane
+    interleaves row pairs, byte (r & ~1) N + 4 (p // 2) + 2 (r & 1) + (p & 1)
+    holding row r, position p."""
     M, N = hi.shape
+    Mp = M + (M & 1)
+    lo = lo.reshape(-1)[:Mp * N].reshape(Mp // 2, N // 2, 2, 2)  # [pair, p // 2, r & 1, p & 1]
+    lo = lo.transpose(0, 2, 1, 3).reshape(Mp, N)[:M]            # [row, p]
     bits = (hi.astype(np.uint32) << 16) | (lo.astype(np.uint32) << 8)
     g = bits.reshape(M, N // 64, 32, 2)           # [.., i, j] at position 2 i + j
     cols = g.transpose(0, 1, 3, 2).reshape(M, N)  # column 32 j + i
@@ -260,7 +265,7 @@ def test_linear_i8_gelu_quant_r24(dev, oracle, M, N, K, ldq):
     a_s_dev[nan_row] = np.nan
     w = dev.weight_i8(W, w_s)
     dA, da, db = dev.array(A), dev.array(a_s_dev), dev.array(bias)
-    dh, dl = dev.empty((M, N), np.uint16), dev.empty((M, N), np.uint8)
+    dh, dl = dev.empty((M, N), np.uint16), dev.empty((M + (M & 1), N), np.uint8)
     dq, ds = dev.array(np.full((M, ldq), 99, np.int8)), dev.empty((M,), np.float32)
     dev.linear_i8_gelu_quant_r24(dA, K, da, w, db, M, dh, dl, dq, ldq, ds)
     inter = _planes_to_f32(dh.numpy(), dl.numpy())
