@@ -1033,19 +1033,32 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
       float* cosT = reinterpret_cast<float*>(smem);
       float* sinT = cosT + 32 * kRopeTPitch;
       __syncthreads();
-      for (int u = threadIdx.x; u < 2 * BM; u += kThreads) {
-        const int t = u >> 1;
-        const bool odd = u & 1;
-        const float4* src =
-            reinterpret_cast<const float4*>((odd ? p.rope_sin : p.rope_cos) + static_cast<size_t>(s_pos[t]) * 64);
-        float* dst = (odd ? sinT : cosT) + t;
+      // Each thread copies items threadIdx.x + k * kThreads; every item's
+      // loads are issued before the first LDS write, so the table reads'
+      // latency is paid once.
+      constexpr int kItems = (2 * BM + kThreads - 1) / kThreads;
+      float4 v[kItems][8];
 #pragma unroll
-        for (int c4 = 0; c4 < 8; ++c4) {
-          const float4 v = src[c4];
-          dst[(4 * c4 + 0) * kRopeTPitch] = v.x;
-          dst[(4 * c4 + 1) * kRopeTPitch] = v.y;
-          dst[(4 * c4 + 2) * kRopeTPitch] = v.z;
-          dst[(4 * c4 + 3) * kRopeTPitch] = v.w;
+      for (int k = 0; k < kItems; ++k) {
+        const int u = threadIdx.x + k * kThreads;
+        const int uc = u < 2 * BM ? u : 0;
+        const float4* src = reinterpret_cast<const float4*>((uc & 1 ? p.rope_sin : p.rope_cos) +
+                                                            static_cast<size_t>(s_pos[uc >> 1]) * 64);
+#pragma unroll
+        for (int c4 = 0; c4 < 8; ++c4) v[k][c4] = src[c4];
+      }
+#pragma unroll
+      for (int k = 0; k < kItems; ++k) {
+        const int u = threadIdx.x + k * kThreads;
+        if (u < 2 * BM) {
+          float* dst = (u & 1 ? sinT : cosT) + (u >> 1);
+#pragma unroll
+          for (int c4 = 0; c4 < 8; ++c4) {
+            dst[(4 * c4 + 0) * kRopeTPitch] = v[k][c4].x;
+            dst[(4 * c4 + 1) * kRopeTPitch] = v[k][c4].y;
+            dst[(4 * c4 + 2) * kRopeTPitch] = v[k][c4].z;
+            dst[(4 * c4 + 3) * kRopeTPitch] = v[k][c4].w;
+          }
         }
       }
       __syncthreads();
