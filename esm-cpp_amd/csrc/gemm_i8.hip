@@ -838,50 +838,6 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   const int nk = nk_all * (split + 1) / splits - kb0;
   const int8_t* const pA = p.A + kb0 * BK;
   const int8_t* const pW = p.W + kb0 * BK;
-  // kEpiF32R24: whether a value of the tile can be NaN (a scale or bias not
-  // finite, or a scale above 2^60, so that a product of two could overflow).
-  bool nan_risk = false;
-  if constexpr (EPI != kEpiI32) {
-    // Per-row activation scales and per-column weight scales / bias of the
-    // tile, read once here instead of per element in the epilogue.
-    int risk = 0;
-    for (int t = threadIdx.x; t < BM + BN; t += kThreads) {
-      if (t < BM) {
-        const int row = m0 + t;
-        const float a = row < p.M ? p.a_scale[row] : 0.0f;
-        s_as[t] = a;
-        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(a) <= 0x1p60f);
-        if constexpr (kRope) s_pos[t] = row < p.M ? p.pos[row] : 0;
-      } else {
-        const int c = t - BM, col = n0 + c;
-        const bool ok = col < p.N;
-        float w = ok ? p.w_scale[col] : 0.0f, b = (ok && p.bias) ? p.bias[col] : 0.0f;
-        if constexpr (EPI == kEpiQkvSplit) {
-          // Q columns: q_prescale (a power of two) folded in here, exactly.
-          if (col < p.d_model) {
-            w *= p.q_prescale;
-            b *= p.q_prescale;
-          }
-        }
-        s_ws[c] = w;
-        s_bs[c] = b;
-        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(w) <= 0x1p60f) | !(__builtin_fabsf(b) <= 0x1p127f);
-      }
-    }
-    if constexpr (EPI == kEpiF32R24) {
-      // Each wave's verdict through LDS, read by every wave after the barrier.
-      __shared__ int s_risk[TL::kWaves];
-      const bool wave_risk = __builtin_amdgcn_ballot_w64(risk != 0) != 0;
-      if ((threadIdx.x & 63) == 0) s_risk[threadIdx.x >> 6] = wave_risk;
-      __syncthreads();
-      int any = 0;
-#pragma unroll
-      for (int w = 0; w < TL::kWaves; ++w) any |= s_risk[w];
-      nan_risk = any != 0;
-    } else {
-      __syncthreads();
-    }
-  }
   // The wave index is uniform across the wave; readfirstlane tells the
   // compiler so, keeping per-wave decisions (Q/K/V head, RoPE) scalar.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -905,8 +861,72 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
   }
   auto gbase = [&](int i) { return wave * kPer + i < BM / 8 ? pA : pW; };
   const uint32_t ldst = lds_addr(smem) + static_cast<uint32_t>(wave * kPer * 1024);
+  // Stage 0 first, so that its loads and the scale loads below are in flight
+  // together.
 #pragma unroll
   for (int i = 0; i < kPer; ++i) dma16_async_so(gbase(i), goff[i], ldst + i * 1024);
+
+  // kEpiF32R24: whether a value of the tile can be NaN (a scale or bias not
+  // finite, or a scale above 2^60, so that a product of two could overflow).
+  // Each wave's verdict goes to LDS here and is combined before the
+  // epilogue.
+  __shared__ int s_risk[TL::kWaves];
+  if constexpr (EPI != kEpiI32) {
+    // Per-row activation scales and per-column weight scales / bias of the
+    // tile, read once here instead of per element in the epilogue, every
+    // item's loads issued before the first LDS write. The epilogue (and the
+    // RoPE staging) read them after the main loop's barriers, each of which
+    // follows an lgkmcnt(0) wait, so no barrier of their own is needed.
+    constexpr int kItems = (BM + BN + kThreads - 1) / kThreads;
+    float va[kItems], vb[kItems];
+    int vp[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int t = threadIdx.x + k * kThreads;
+      va[k] = vb[k] = 0.0f;
+      vp[k] = 0;
+      if (t < BM) {
+        const int row = m0 + t;
+        if (row < p.M) {
+          va[k] = p.a_scale[row];
+          if constexpr (kRope) vp[k] = p.pos[row];
+        }
+      } else if (t < BM + BN) {
+        const int col = n0 + t - BM;
+        if (col < p.N) {
+          va[k] = p.w_scale[col];
+          if (p.bias) vb[k] = p.bias[col];
+        }
+      }
+    }
+    int risk = 0;
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+      const int t = threadIdx.x + k * kThreads;
+      if (t < BM) {
+        s_as[t] = va[k];
+        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(va[k]) <= 0x1p60f);
+        if constexpr (kRope) s_pos[t] = vp[k];
+      } else if (t < BM + BN) {
+        const int c = t - BM;
+        float w = va[k], b = vb[k];
+        if constexpr (EPI == kEpiQkvSplit) {
+          // Q columns: q_prescale (a power of two) folded in here, exactly.
+          if (n0 + c < p.d_model) {
+            w *= p.q_prescale;
+            b *= p.q_prescale;
+          }
+        }
+        s_ws[c] = w;
+        s_bs[c] = b;
+        if constexpr (EPI == kEpiF32R24) risk |= !(__builtin_fabsf(w) <= 0x1p60f) | !(__builtin_fabsf(b) <= 0x1p127f);
+      }
+    }
+    if constexpr (EPI == kEpiF32R24) {
+      const bool wave_risk = __builtin_amdgcn_ballot_w64(risk != 0) != 0;
+      if (lane == 0) s_risk[wave] = wave_risk;
+    }
+  }
 
   // The accumulators start as the first products (the first sub-step's
   // MFMAs take a zero C operand), so no register is cleared beforehand.
@@ -1065,6 +1085,13 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
       s_cosT = cosT;
       s_sinT = sinT;
     }
+  }
+  bool nan_risk = false;
+  if constexpr (EPI == kEpiF32R24) {
+    int any = 0;
+#pragma unroll
+    for (int w = 0; w < TL::kWaves; ++w) any |= s_risk[w];
+    nan_risk = any != 0;
   }
   constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
