@@ -1500,6 +1500,10 @@ class ObsRun {
 // dequantises and adds. With split_out set (per-token mode, not the last
 // layer), this layer's fc2 may leave its output that way too: split_out
 // says whether it did.
+// Whether the per-tensor LayerNorm + quantisation can take the two-pass form
+// (launch_layernorm's maximum alone, then launch_layernorm_quant_tensor).
+bool ln_tensor_quant_ok(int d) { return d % 4 == 0 && d <= 2560; }
+
 int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L, int round16, const Arena& a,
                const Meta& md, int T, int nwork, int max_len, const float* resid_in, ObsRun* ob, int cus,
                const SplitResid* split_in = nullptr, SplitResid* split_out = nullptr) {
@@ -1531,10 +1535,21 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
       ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
     }
   } else {
-    ESM_HIP(ctx, launch_fill_f32(a.absmax, 1, 0.0f, s));
-    ESM_HIP(ctx, launch_layernorm(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
-    if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
-    ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax, a.xq, ldq_d, a.xs, s));
+    // The layer's four per-tensor maxima (attention LN, attention output,
+    // FFN LN, FFN intermediate) start at zero.
+    ESM_HIP(ctx, launch_fill_f32(a.absmax, 4, 0.0f, s));
+    if (!ob && ln_tensor_quant_ok(d)) {
+      // The LN's maximum first (no fp32 output), then the LN again,
+      // quantised with the tensor scale: the same codes as LN + quant_tensor.
+      ESM_HIP(ctx, launch_layernorm(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, nullptr, T, d, a.absmax,
+                                    s));
+      ESM_HIP(ctx, launch_layernorm_quant_tensor(a.hidden, L.ln1_w, L.ln1_b, c.layer_norm_eps, T, d, a.absmax, a.xq,
+                                                 ldq_d, a.xs, s));
+    } else {
+      ESM_HIP(ctx, launch_layernorm(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, s));
+      if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+      ESM_HIP(ctx, launch_quant_tensor(a.ln, d, T, d, a.absmax, a.xq, ldq_d, a.xs, s));
+    }
   }
 
   // QKV projection (one GEMM over the concatenated [3d, d] weight)
@@ -1592,7 +1607,6 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
 
   // attention
   float* amax_attn = tok ? nullptr : a.absmax + 1;
-  if (!tok) ESM_HIP(ctx, launch_fill_f32(a.absmax + 1, 1, 0.0f, s));
   ESM_TRY(ctx->time_begin("attention", &slot));
   if (f32qkv) {
     if (c.attention_mode == ESM_GFX950_ATTN_MODE_F16X3) {
@@ -1655,8 +1669,12 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
       ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, s));
       ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
     }
+  } else if (!ob && ln_tensor_quant_ok(d)) {
+    ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, nullptr, T, d, a.absmax + 2,
+                                  s, round16));
+    ESM_HIP(ctx, launch_layernorm_quant_tensor(a.hidden, L.ln2_w, L.ln2_b, c.layer_norm_eps, T, d, a.absmax + 2, a.xq,
+                                               ldq_d, a.xs, s, round16));
   } else {
-    ESM_HIP(ctx, launch_fill_f32(a.absmax + 2, 1, 0.0f, s));
     ESM_HIP(ctx, launch_layernorm(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
                                   s, round16));
     if (ob && round16) {
@@ -1709,10 +1727,12 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
     ESM_HIP(ctx, launch_gelu_quant_rows(a.inter, f, T, f, a.xq, ldq_f, a.xs, s));
     ESM_TRY(ctx->time_end(slot));
   } else {
-    ESM_HIP(ctx, launch_fill_f32(a.absmax + 3, 1, 0.0f, s));
+    // GELU with the erf of the fused GELU + quantisation passes (Abramowitz
+    // & Stegun 7.1.26, as the reference's AVX-512 Gelu) in the epilogue,
+    // with the tensor's maximum.
     g.tensor_absmax = a.absmax + 3;
     ESM_TRY(ctx->time_begin("fc1", &slot));
-    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32Gelu, s));
+    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32GeluAs, s));
     ESM_TRY(ctx->time_end(slot));
     if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
     ESM_HIP(ctx, launch_quant_tensor(a.inter, f, T, f, a.absmax + 3, a.xq, ldq_f, a.xs, s));

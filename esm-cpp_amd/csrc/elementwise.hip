@@ -59,23 +59,15 @@ __device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int c
 // residual add that precedes the next LayerNorm, reference src/model.cpp:1013
 // and :1063), and the LayerNorm runs on the sum.
 // SPLIT: the residual arrives as split-K partial sums (SplitResid).
-template <int NV, bool QUANT, bool SPLIT = false>
-__global__ __launch_bounds__(256) void layernorm_vec_kernel(
-    float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
-    const float* __restrict__ beta, float eps, float* __restrict__ out,
-    int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
-    float* scales, int round16, SplitResid split = SplitResid()) {
-  const int lane = threadIdx.x & 63;
-  // With a per-tensor absmax every wave of the block joins the block's
-  // reduction at the end: a wave past the last row recomputes that row and
-  // stores nothing. Otherwise such a wave leaves at once.
-  const int row0 = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  const bool live = row0 < rows;
-  const bool reduce = !QUANT && tensor_absmax;
-  if (!live && !reduce) return;
-  const int row = live ? row0 : rows - 1;
+// One wave's row: the residual update, the LayerNorm into v, and the row's
+// absolute maximum (returned). The kernels below share this body, so every
+// pass over a row computes the same values.
+template <int NV, bool SPLIT>
+__device__ __forceinline__ float ln_row(float* __restrict__ x, const float* __restrict__ resid,
+                                        const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+                                        int row, int rows, int d, int lane, int round16, const SplitResid& split,
+                                        float4 (&v)[NV]) {
   float* xr = x + static_cast<size_t>(row) * d;
-  float4 v[NV];
   load_row_vec<NV>(xr, d, lane, v);
   if (SPLIT || resid) {
     float4 r[NV];
@@ -83,7 +75,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
       // The residual's GEMM epilogue on its summed split-K partial sums:
       // fma(float(acc), a_scale * w_scale, bias), the same expression and
       // operands. The row's a_scale is read here, before `scales` (which it
-      // may be) receives this row's new scale below.
+      // may be) receives this row's new scale.
       const float as = split.a_scale[row];
       const size_t plane = static_cast<size_t>(rows) * d;
 #pragma unroll
@@ -116,7 +108,7 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
       v[j].z += r[j].z;
       v[j].w += r[j].w;
       const int c = (j * 64 + lane) * 4;
-      if (live && c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
+      if (c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
     }
   }
   float sum = 0.f;
@@ -147,27 +139,83 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
     y.w = (v[j].w - mean) * inv_std * g[j].w + bt[j].w;
     if (round16) y = round_f16(y);
     v[j] = y;
-    if (c < d) {
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-      if constexpr (!QUANT)
-        if (live) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = y;
-    }
+    if (c < d) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
   }
-  if constexpr (QUANT) {
-    const float scale = act_scale_from_absmax(wave_max(amax));
-    const float inv = 1.0f / scale;
-    int8_t* qr = q + static_cast<size_t>(row) * ldq;
+  return amax;
+}
+
+// !QUANT: the LayerNorm stored to out (if not null). With a per-tensor
+// absmax the grid is bounded and walks the rows (one atomic per block: the
+// atomics on the one address serialise in L2), every wave reaching the
+// block's reduction.
+// QUANT: int8 codes and the row's scale; the scale from the row's own
+// maximum (per-token), or with tensor_absmax from that device value, each
+// code then quant_i8 as the per-tensor quantisation kernel forms it.
+template <int NV, bool QUANT, bool SPLIT = false>
+__global__ __launch_bounds__(256) void layernorm_vec_kernel(
+    float* __restrict__ x, const float* __restrict__ resid, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ out,
+    int rows, int d, float* tensor_absmax, int8_t* __restrict__ q, int ldq,
+    float* scales, int round16, SplitResid split = SplitResid()) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float4 v[NV];
+  if (!QUANT && tensor_absmax) {
+    float am = 0.f;
+    for (int base = blockIdx.x * kRowsPerBlock; base < rows; base += gridDim.x * kRowsPerBlock) {
+      const int row = base + wave;
+      if (row < rows) {
+        am = fmaxf(am, ln_row<NV, SPLIT>(x, resid, gamma, beta, eps, row, rows, d, lane, round16, split, v));
+        if (out) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int c = (j * 64 + lane) * 4;
-      if (c < d) {
-        *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
+          for (int j = 0; j < NV; ++j) {
+            const int c = (j * 64 + lane) * 4;
+            if (c < d) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = v[j];
+          }
+        }
       }
     }
-    for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
-    if (lane == 0) scales[row] = scale;
-  } else if (reduce) {
-    block_atomic_max_nonneg(tensor_absmax, live ? amax : 0.0f);
+    block_atomic_max_nonneg(tensor_absmax, am);
+    return;
+  }
+  const int row = blockIdx.x * kRowsPerBlock + wave;
+  if (row >= rows) return;
+  const float amax = ln_row<NV, SPLIT>(x, resid, gamma, beta, eps, row, rows, d, lane, round16, split, v);
+  if constexpr (QUANT) {
+    int8_t* qr = q + static_cast<size_t>(row) * ldq;
+    if (tensor_absmax) {
+      const float scale = act_scale_from_absmax(*tensor_absmax);
+      const float inv = 1.0f / scale;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 4;
+        if (c < d)
+          *reinterpret_cast<uint32_t*>(qr + c) = (static_cast<uint32_t>(quant_i8(v[j].x, inv)) & 0xffu) |
+                                                 ((static_cast<uint32_t>(quant_i8(v[j].y, inv)) & 0xffu) << 8) |
+                                                 ((static_cast<uint32_t>(quant_i8(v[j].z, inv)) & 0xffu) << 16) |
+                                                 (static_cast<uint32_t>(quant_i8(v[j].w, inv)) << 24);
+      }
+      for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
+      if (lane == 0) scales[row] = scale;
+    } else {
+      const float scale = act_scale_from_absmax(wave_max(amax));
+      const float inv = 1.0f / scale;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 4;
+        if (c < d) *reinterpret_cast<uint32_t*>(qr + c) = quant_pack4(v[j], inv);
+      }
+      for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
+      if (lane == 0) scales[row] = scale;
+    }
+  } else {
+    if (out) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 4;
+        if (c < d) *reinterpret_cast<float4*>(out + static_cast<size_t>(row) * d + c) = v[j];
+      }
+    }
   }
 }
 
@@ -484,12 +532,34 @@ __global__ __launch_bounds__(256) void quant_tensor_kernel(
   if (lane == 0) scales[row] = scale;
 }
 
+__device__ __forceinline__ float absmax4(float m, const float4& v) {
+  return fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+}
+
+// max |x[i]| over n values into *absmax (NaNs ignored, as fmaxf does). A
+// 16-byte aligned x is read as float4, eight loads in flight per thread.
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x,
                                                      size_t n, float* absmax) {
   float m = 0.f;
-  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
-       i += static_cast<size_t>(gridDim.x) * blockDim.x)
-    m = fmaxf(m, fabsf(x[i]));
+  const size_t tid = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  size_t done = 0;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const size_t n4 = n / 4;
+    constexpr int kU = 8;
+    size_t i = tid;
+    for (; i + (kU - 1) * stride < n4; i += kU * stride) {
+      float4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = x4[i + u * stride];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) m = absmax4(m, v[u]);
+    }
+    for (; i < n4; i += stride) m = absmax4(m, x4[i]);
+    done = n4 * 4;
+  }
+  for (size_t i = done + tid; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
   block_atomic_max_nonneg(absmax, m);
 }
 
@@ -616,12 +686,21 @@ inline dim3 grid_for(size_t n, int block = 256) {
 
 inline dim3 rows_grid(int rows) { return dim3((rows + kRowsPerBlock - 1) / kRowsPerBlock); }
 
+// Grid bound of the kernels that fold a per-tensor maximum with one atomic
+// per block (four blocks per CU).
+constexpr unsigned kReduceBlocks = 1024;
+
 }  // namespace
 
 hipError_t launch_layernorm(float* x, const float* resid, const float* gamma, const float* beta, float eps,
                             float* out, int rows, int d, float* tensor_absmax, hipStream_t s, int round16) {
   if (rows <= 0 || d <= 0) return hipSuccess;
-  const dim3 g = rows_grid(rows), b(256);
+  dim3 g = rows_grid(rows);
+  const dim3 b(256);
+  // With a per-tensor maximum the vectorised kernel walks the rows with a
+  // bounded grid: one atomic per block.
+  if (tensor_absmax && d % 4 == 0 && d <= 2560 && g.x > kReduceBlocks) g.x = kReduceBlocks;
+  if (!out && !(tensor_absmax && d % 4 == 0 && d <= 2560)) return hipErrorInvalidValue;
   if (d % 4 == 0 && d <= 1280) {
     hipLaunchKernelGGL((layernorm_vec_kernel<5, false>), g, b, 0, s, x, resid, gamma, beta, eps, out, rows, d,
                        tensor_absmax, nullptr, 0, nullptr, round16);
@@ -646,6 +725,23 @@ hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gam
   } else {
     hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, resid, gamma, beta, eps, nullptr, rows, d,
                        nullptr, q, ldq, scales, round16);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_layernorm_quant_tensor(float* x, const float* gamma, const float* beta, float eps, int rows, int d,
+                                         const float* absmax, int8_t* q, int ldq, float* scales, hipStream_t s,
+                                         int round16) {
+  if (rows <= 0 || d <= 0) return hipSuccess;
+  if (d % 4 != 0 || d > 2560 || !absmax) return hipErrorInvalidValue;
+  const dim3 g = rows_grid(rows), b(256);
+  float* amax = const_cast<float*>(absmax);  // read only in the QUANT instantiation
+  if (d <= 1280) {
+    hipLaunchKernelGGL((layernorm_vec_kernel<5, true>), g, b, 0, s, x, nullptr, gamma, beta, eps, nullptr, rows, d,
+                       amax, q, ldq, scales, round16);
+  } else {
+    hipLaunchKernelGGL((layernorm_vec_kernel<10, true>), g, b, 0, s, x, nullptr, gamma, beta, eps, nullptr, rows, d,
+                       amax, q, ldq, scales, round16);
   }
   return hipGetLastError();
 }
@@ -735,8 +831,9 @@ hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols, cons
 
 hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s) {
   if (n == 0) return hipSuccess;
-  size_t g = (n + 255) / 256;
-  if (g > 1024) g = 1024;  // four per CU: one atomic each
+  size_t g = (n / 4 + 255) / 256;
+  if (g < 1) g = 1;
+  if (g > 512) g = 512;  // two per CU: one atomic each
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
   return hipGetLastError();
 }

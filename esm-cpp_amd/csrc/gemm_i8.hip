@@ -256,6 +256,7 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
             const int col = cb + bn * 16 + lr;
             float v = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
             if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
+            if constexpr (EPI == kEpiF32GeluAs) v = 0.5f * gelu2_as(v);
             if (rok && col < p.N) {
               const size_t o = static_cast<size_t>(row) * p.ldc + col;
               if constexpr (EPI == kEpiF32Resid) {
@@ -269,7 +270,7 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
               }
             }
           }
-          if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32) {
+          if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32) {
             if (p.row_absmax) {
               // Lanes sharing lg hold the same row; reduce over the 16 of them.
 #pragma unroll
@@ -280,7 +281,7 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
             tmax = fmaxf(tmax, rmax);
           }
         }
-      if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32) {
+      if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32) {
         if (p.tensor_absmax) {
           tmax = wave_max(tmax);
           if ((threadIdx.x & 63) == 0) atomic_max_nonneg(p.tensor_absmax, tmax);
@@ -777,6 +778,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
             for (int j = 0; j < BLK_N; ++j) {
               float v = __builtin_fmaf(static_cast<float>(acc[i][j][r]), asv[u] * ws[j], bs[j]);
               if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
+              if constexpr (EPI == kEpiF32GeluAs) v = 0.5f * gelu2_as(v);
               if (rok && col_ok(lc0 + j * 32)) {
                 const uint32_t off = lane_c + static_cast<uint32_t>(i * 32 + q * 8 + u) * ldc + j * 32;
                 if constexpr (EPI == kEpiF32GeluQ) {
@@ -1093,7 +1095,7 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
     for (int w = 0; w < TL::kWaves; ++w) any |= s_risk[w];
     nan_risk = any != 0;
   }
-  constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32;
+  constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
@@ -1172,6 +1174,7 @@ hipError_t launch_v1(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32Resid>), grid, block, 0, s, p); break;
     case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRope>), grid, block, 0, s, p); break;
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiF32GeluAs: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluAs>), grid, block, 0, s, p); break;
     case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRopeF32>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
@@ -1191,6 +1194,9 @@ hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiF32Resid: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32Resid>), grid, block, 0, s, p); break;
     case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRope>), grid, block, 0, s, p); break;
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluQ>), grid, block, 0, s, p); break;
+    case kEpiF32GeluAs:
+      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluAs>), grid, block, 0, s, p);
+      break;
     case kEpiQkvRopeF32:
       hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRopeF32>), grid, block, 0, s, p);
       break;
@@ -1238,13 +1244,14 @@ int gemm_i8_tile_rows(int M, int N, int K, int epi, int cus) {
   const int all = device_cus();
   if (cus <= 0) cus = all;
   // Ties go to 320 rows: at equal rounds the taller tile re-reads less of
-  // A and W (fc1 at config 4: 270 vs 282 us). The GELU and bf16/fp32 RoPE
-  // epilogues stay at 256 rows: at BLK_M = 5 they exceed 256 VGPRs. The
+  // A and W (fc1 at config 4: 270 vs 282 us). The erff GELU and bf16/fp32
+  // RoPE epilogues stay at 256 rows: at BLK_M = 5 they exceed 256 VGPRs. The
   // split-word QKV epilogue spills 72 bytes there too, but runs faster at
   // 320 rows all the same (216 vs 224 us at config 4). Rounds are counted
   // over the whole device: concurrent launches fill each other's last round.
   const bool tall_ok =
-      epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit || epi == kEpiF32R24;
+      epi == kEpiI32 || epi == kEpiF32 || epi == kEpiF32Resid || epi == kEpiQkvSplit || epi == kEpiF32R24 ||
+      epi == kEpiF32GeluAs;
   if (tiles_of(M, N, 256) >= cus)
     return tall_ok && tile_cost(M, N, 320, all) <= tile_cost(M, N, 256, all) ? 320 : 256;
   // The 256-row grid leaves CUs idle (one workgroup per CU): shorter tiles

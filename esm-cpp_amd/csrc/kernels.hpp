@@ -32,6 +32,10 @@ enum GemmEpilogue : int {
                       // + 2 (r & 1) + (p & 1) holds row r, position p, so it
                       // spans (M + (M & 1)) ldc bytes. Pipelined kernel only;
                       // N % 64 == 0.
+  kEpiF32GeluAs = 9,  // as kEpiF32Gelu with the erf of Abramowitz & Stegun
+                      // 7.1.26 (gelu2_as / 2, the GELU of the fused GELU +
+                      // quantisation passes and of the reference's AVX-512
+                      // Gelu) instead of erff
 };
 
 // Split-fp16 word of an fp32 value x: low half fp16(x), high half
@@ -203,10 +207,21 @@ constexpr int kAttnF32QTile = 64;
 // (x += resid) and normalised after the add.
 // round16: round each output to the nearest fp16 and back (the reference's
 // first-block fc1 escape, src/model.cpp:1028-1033).
+// tensor_absmax != null: the maximum |output| is folded into it (atomic
+// max); out may then be null (the maximum alone, for
+// launch_layernorm_quant_tensor).
 hipError_t launch_layernorm(float* x, const float* resid, const float* gamma,
                             const float* beta, float eps, float* out,
                             int rows, int d, float* tensor_absmax,
                             hipStream_t s, int round16 = 0);
+// The same LayerNorm (no residual add: x already holds the sum) quantised
+// with the per-tensor scale of launch_quant_tensor, scale = absmax / 127 from
+// the device value absmax that launch_layernorm folded: the codes and scales
+// of launch_layernorm followed by launch_quant_tensor, without the fp32
+// output. d % 4 == 0, d <= 2560.
+hipError_t launch_layernorm_quant_tensor(float* x, const float* gamma, const float* beta, float eps, int rows, int d,
+                                         const float* absmax, int8_t* q, int ldq, float* scales, hipStream_t s,
+                                         int round16 = 0);
 // LayerNorm (with the same optional residual add) fused with per-token
 // symmetric int8 quantisation.
 hipError_t launch_layernorm_quant(float* x, const float* resid, const float* gamma,
