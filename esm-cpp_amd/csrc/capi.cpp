@@ -962,6 +962,7 @@ struct esm_gfx950_model {
     int rope_len = 0;                // rows currently in the device rope tables
     int T = 0, B = 0, nwork = 0, t0 = 0;
     int maxL = 0;                    // longest sequence of the staged part
+    size_t x86_score_floats = 0;     // attention_x86_score_floats of the staged part
   };
   std::vector<Part> parts = std::vector<Part>(1);
   // Automatic group count (esm_gfx950_model_set_parts(0), the default): each
@@ -1820,6 +1821,13 @@ int layer_f32(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L,
   return ESM_GFX950_OK;
 }
 
+// The x86-exact attention's score scratch: the FFN buffer (dead while the
+// attention runs) when the part's scores fit there and in 32-bit offsets.
+float* x86_score_scratch(const esm_gfx950_model::Part& P, const Arena& a, size_t Tf, int heads) {
+  const size_t per_head = P.x86_score_floats / static_cast<size_t>(heads);
+  return P.x86_score_floats <= Tf && per_head < (static_cast<size_t>(1) << 32) ? a.inter : nullptr;
+}
+
 // TransformerBlock (reference src/model.cpp:932-1066) on the reference's x86
 // AVX-512 VNNI kernels, bit for bit: LayerNormAvx512, LinearVnni (per-tensor
 // activation scale, QuantizeActPrefixAvx512; the INT8 GEMM's dequant
@@ -1886,7 +1894,8 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
   ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
   ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_TRY(ctx->time_begin("attention", &slot));
-  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s));
+  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
+                                    x86_score_scratch(P, a, Tf, H)));
   ESM_TRY(ctx->time_end(slot));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
@@ -1929,7 +1938,8 @@ int layer_f32_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer
   const float q_scale = 1.0f / std::sqrt(static_cast<float>(dh));
   ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
   ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
-  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s));
+  ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
+                                    x86_score_scratch(P, a, Tf, H)));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   ESM_TRY(linear(a.attn, L.out, a.hidden, kF32Resid));
   ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr,
@@ -2038,6 +2048,7 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
   P.t0 = t0;
   P.maxL = maxL;
   P.nwork = static_cast<int>(work.size());
+  P.x86_score_floats = attention_x86_score_floats(mh.cu, B, m->cfg.num_heads);
   return ESM_GFX950_OK;
 }
 

@@ -306,8 +306,14 @@ hipError_t launch_expf_glibc(const float* x, float* out, size_t n, hipStream_t s
 hipError_t launch_rope_x86(float* x, int ld, const int* pos, int T, int heads, int head_dim, const float* cos_t,
                            const float* sin_t, int ldt, float scale, hipStream_t s);
 bool attention_x86_supported(int head_dim);
+// scores: null, or a scratch of attention_x86_score_floats(cu, batch, heads)
+// floats (host cu) for the kernel to keep each score and exponential it
+// computes instead of recomputing them in the later passes (same results).
+// The scratch must fit 32-bit float offsets per head (cu's total below 2^32).
 hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
-                                int batch, int heads, int max_len, float* out, int ldo, hipStream_t s);
+                                int batch, int heads, int max_len, float* out, int ldo, hipStream_t s,
+                                float* scores = nullptr);
+size_t attention_x86_score_floats(const int* cu, int batch, int heads);
 hipError_t launch_linear_x86(const float* A, int lda, const float* W, int ldw, const float* bias, float* C, int ldc,
                              int M, int N, int K, int epi, hipStream_t s);
 

@@ -341,10 +341,37 @@ __device__ __forceinline__ float score_x86(const float (&q)[DH], const float* __
 
 constexpr int kX86Keys = 16;  // keys staged per LDS pass (one 16-key chunk of the reference)
 
-template <int DH>
+// Scratch offset (floats) of sequence b's scores when every sequence b'
+// before it holds heads x pad64(L_b') x L_b' of them: the wave sums those
+// sizes 64 sequences at a time.
+__device__ __forceinline__ size_t score_base(const int* __restrict__ cu, int b, int heads) {
+  const int lane = threadIdx.x & 63;
+  uint32_t pre = 0;
+  for (int c = 0; c < b; c += 64) {
+    const int bb = c + lane;
+    uint32_t t = 0;
+    if (bb < b) {
+      const uint32_t L = static_cast<uint32_t>(cu[bb + 1] - cu[bb]);
+      t = ((L + 63u) & ~63u) * L;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+    pre += t;
+  }
+  return static_cast<size_t>(pre) * static_cast<size_t>(heads);
+}
+
+// SC: the scores of pass 1 are stored in `scores` (this wave's region,
+// key j of lane l at j * 64 + l) and pass 2 replaces each with its
+// exponential, so passes 2 and 3 read what pass 1 and pass 2 computed
+// instead of recomputing it: the same values, the same order of operations.
+// Regions: sequence b at score_base, then head h at h x pad64(L) x L, then
+// query tile t at t x 64 x L. Without SC every pass recomputes the scores.
+template <int DH, bool SC>
 __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, int ld, const int* __restrict__ cu,
-                                                      int heads, float* __restrict__ out, int ldo) {
+                                                      int heads, float* __restrict__ out, int ldo,
+                                                      float* __restrict__ scores) {
   __shared__ __attribute__((aligned(16))) float ks[kX86Keys][DH];
   __shared__ __attribute__((aligned(16))) float vs[kX86Keys][DH];
   const int b = blockIdx.z, h = blockIdx.y;
@@ -354,6 +381,12 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
   const int lane = threadIdx.x;
   const int i = min(q0 + lane, L - 1);
   const bool active = q0 + lane < L;
+  float* sc_w = nullptr;  // this lane's key-0 slot
+  if constexpr (SC) {
+    const size_t Lp = static_cast<size_t>((L + 63) & ~63);
+    sc_w = scores + score_base(cu, b, heads) + static_cast<size_t>(h) * Lp * L +
+           static_cast<size_t>(q0) * L + lane;
+  }
   float qv[DH];
   {
     const float* qr = q + static_cast<size_t>(s0 + i) * ld + static_cast<size_t>(h) * DH;
@@ -367,10 +400,10 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
     }
   }
   const int Lfull = L & ~15;
-  // Stages rows [kc, kc + 16) of K (and V) into LDS, 16 bytes per lane per
+  // Stages rows [kc, kc + 16) of K and / or V into LDS, 16 bytes per lane per
   // step: item t is float4 t % (DH / 4) of row t / (DH / 4). Rows past the
   // sequence are not read (their LDS slots are never used).
-  auto stage = [&](int kc, bool with_v) {
+  auto stage = [&](int kc, bool with_k, bool with_v) {
     __syncthreads();
     constexpr int kItems = kX86Keys * DH / 4;
 #pragma unroll
@@ -379,7 +412,7 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
       const int r = t / (DH / 4), d4 = t % (DH / 4);
       if ((kItems % 64 == 0 || t < kItems) && kc + r < L) {
         const size_t o = static_cast<size_t>(s0 + kc + r) * ld + static_cast<size_t>(h) * DH + d4 * 4;
-        *reinterpret_cast<float4*>(&ks[r][d4 * 4]) = *reinterpret_cast<const float4*>(k + o);
+        if (with_k) *reinterpret_cast<float4*>(&ks[r][d4 * 4]) = *reinterpret_cast<const float4*>(k + o);
         if (with_v) *reinterpret_cast<float4*>(&vs[r][d4 * 4]) = *reinterpret_cast<const float4*>(v + o);
       }
     }
@@ -389,10 +422,11 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
   // Pass 1: maximum score.
   float mx = -INFINITY;
   for (int kc = 0; kc < L; kc += kX86Keys) {
-    stage(kc, false);
+    stage(kc, true, false);
     const int nk = min(kX86Keys, L - kc);
     for (int jj = 0; jj < nk; ++jj) {
       const float sc = score_x86<DH>(qv, ks[jj]);
+      if constexpr (SC) sc_w[static_cast<size_t>(kc + jj) * 64] = sc;
       mx = sc > mx ? sc : mx;
     }
   }
@@ -404,16 +438,39 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
   float sum = 0.0f;
   bool summed = false;
   for (int kc = 0; kc < L; kc += kX86Keys) {
-    stage(kc, false);
+    if constexpr (!SC) stage(kc, true, false);
     const int nk = min(kX86Keys, L - kc);
     for (int jb = 0; jb < nk; jb += 16) {
       if (kc + jb + 16 <= L) {
+        if constexpr (SC) {
+          float* p = sc_w + static_cast<size_t>(kc + jb) * 64;
+          float sv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) vsum[u] = vsum[u] + exp_x86(score_x86<DH>(qv, ks[jb + u]) - mx);
+          for (int u = 0; u < 16; ++u) sv[u] = p[u * 64];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            const float e = exp_x86(sv[u] - mx);
+            p[u * 64] = e;
+            vsum[u] = vsum[u] + e;
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < 16; ++u) vsum[u] = vsum[u] + exp_x86(score_x86<DH>(qv, ks[jb + u]) - mx);
+        }
       } else {
         sum = red16(vsum);
         summed = true;
-        for (int u = 0; kc + jb + u < L; ++u) sum += expf_glibc(score_x86<DH>(qv, ks[jb + u]) - mx);
+        for (int u = 0; kc + jb + u < L; ++u) {
+          float e;
+          if constexpr (SC) {
+            float* p = sc_w + static_cast<size_t>(kc + jb + u) * 64;
+            e = expf_glibc(*p - mx);
+            *p = e;
+          } else {
+            e = expf_glibc(score_x86<DH>(qv, ks[jb + u]) - mx);
+          }
+          sum += e;
+        }
       }
     }
   }
@@ -425,11 +482,21 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
 #pragma unroll
   for (int d = 0; d < DH; ++d) o[d] = 0.0f;
   for (int kc = 0; kc < L; kc += kX86Keys) {
-    stage(kc, true);
+    stage(kc, !SC, true);
     const int nk = min(kX86Keys, L - kc);
+    float ec[kX86Keys];
+    if constexpr (SC) {
+#pragma unroll
+      for (int jj = 0; jj < kX86Keys; ++jj) ec[jj] = jj < nk ? sc_w[static_cast<size_t>(kc + jj) * 64] : 0.0f;
+    }
     for (int jj = 0; jj < nk; ++jj) {
-      const float sc = score_x86<DH>(qv, ks[jj]) - mx;
-      const float e = kc + jj < Lfull ? exp_x86(sc) : expf_glibc(sc);
+      float e;
+      if constexpr (SC) {
+        e = ec[jj];
+      } else {
+        const float sc = score_x86<DH>(qv, ks[jj]) - mx;
+        e = kc + jj < Lfull ? exp_x86(sc) : expf_glibc(sc);
+      }
       const float w = e * inv;
       if (w == 0.0f) continue;
 #pragma unroll
@@ -661,16 +728,32 @@ hipError_t launch_rope_x86(float* x, int ld, const int* pos, int T, int heads, i
 
 bool attention_x86_supported(int head_dim) { return head_dim == 16 || head_dim == 32 || head_dim == 64; }
 
+size_t attention_x86_score_floats(const int* cu, int batch, int heads) {
+  size_t n = 0;
+  for (int b = 0; b < batch; ++b) {
+    const size_t L = static_cast<size_t>(cu[b + 1] - cu[b]);
+    n += ((L + 63) & ~static_cast<size_t>(63)) * L;
+  }
+  return n * static_cast<size_t>(heads);
+}
+
 hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
-                                int batch, int heads, int max_len, float* out, int ldo, hipStream_t s) {
+                                int batch, int heads, int max_len, float* out, int ldo, hipStream_t s,
+                                float* scores) {
   if (batch <= 0 || max_len <= 0) return hipSuccess;
   const dim3 grid((max_len + 63) / 64, heads, batch), block(64);
+#define ESM_ATTN_X86(DH)                                                                                           \
+  if (scores)                                                                                                      \
+    hipLaunchKernelGGL((attn_x86_kernel<DH, true>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, scores);  \
+  else                                                                                                             \
+    hipLaunchKernelGGL((attn_x86_kernel<DH, false>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, nullptr);
   switch (head_dim) {
-    case 16: hipLaunchKernelGGL(attn_x86_kernel<16>, grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo); break;
-    case 32: hipLaunchKernelGGL(attn_x86_kernel<32>, grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo); break;
-    case 64: hipLaunchKernelGGL(attn_x86_kernel<64>, grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo); break;
+    case 16: ESM_ATTN_X86(16) break;
+    case 32: ESM_ATTN_X86(32) break;
+    case 64: ESM_ATTN_X86(64) break;
     default: return hipErrorInvalidValue;
   }
+#undef ESM_ATTN_X86
   return hipGetLastError();
 }
 
