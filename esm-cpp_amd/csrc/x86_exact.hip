@@ -240,6 +240,76 @@ __global__ __launch_bounds__(256) void layernorm_x86_kernel(float* __restrict__ 
   if (absmax) block_atomic_max_nonneg(absmax, m);
 }
 
+// The same for rows of exactly NB 64-element blocks (d = 64 NB: no leftover
+// blocks, no tail), with the operations above in the same order: every
+// load of a row goes out before its first use and no per-block branch
+// splits them.
+template <int NB>
+__global__ __launch_bounds__(256) void layernorm_x86_rows_kernel(float* __restrict__ x,
+                                                                  const float* __restrict__ resid,
+                                                                  const float* __restrict__ gamma,
+                                                                  const float* __restrict__ beta, float eps,
+                                                                  float* __restrict__ out, int rows,
+                                                                  float* __restrict__ absmax, int round16) {
+  constexpr int d = NB * 64;
+  const int lane = threadIdx.x & 63;
+  float m = 0.0f;
+  for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += gridDim.x * 4) {
+    float* xr = x + static_cast<size_t>(row) * d;
+    float xv[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) xv[t] = xr[(t << 6) + lane];
+    if (resid) {
+      const float* rr = resid + static_cast<size_t>(row) * d;
+      float rv[NB];
+#pragma unroll
+      for (int t = 0; t < NB; ++t) rv[t] = rr[(t << 6) + lane];
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        xv[t] = xv[t] + rv[t];
+        xr[(t << 6) + lane] = xv[t];
+      }
+    }
+    const float inv_d = 1.0f / static_cast<float>(d);
+    const float tsum = 0.0f, vtail = 0.0f;  // no tail elements
+
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NB; ++t) s = s + xv[t];
+    float a = s + __shfl_down(s, 16);
+    float v16 = a + __shfl_down(a, 32);
+    const float mean = (__shfl(red16_lanes(v16), 0) + tsum) * inv_d;
+
+    s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const float df = xv[t] - mean;
+      s = __builtin_fmaf(df, df, s);
+    }
+    a = s + __shfl_down(s, 16);
+    v16 = a + __shfl_down(a, 32);
+    const float ve = __builtin_fmaf(__shfl(red16_lanes(v16), 0) + vtail, inv_d, eps);
+    const float sd = static_cast<float>(sqrt(static_cast<double>(ve)));
+    const float inv_std = static_cast<float>(1.0 / static_cast<double>(sd));
+
+    float* yr = out + static_cast<size_t>(row) * d;
+    float gv[NB], bv[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      gv[t] = gamma[(t << 6) + lane];
+      bv[t] = beta[(t << 6) + lane];
+    }
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      float y = __builtin_fmaf((xv[t] - mean) * inv_std, gv[t], bv[t]);
+      if (round16) y = static_cast<float>(static_cast<_Float16>(y));
+      yr[(t << 6) + lane] = y;
+      m = fmaxf(m, fabsf(y));
+    }
+  }
+  if (absmax) block_atomic_max_nonneg(absmax, m);
+}
+
 // --------------------------------------------------------------- GELU
 // GeluAvx512 elementwise; in place allowed. vec: x and out 16-byte aligned,
 // four values per thread per step. absmax (optional): atomic max of |out|,
@@ -689,6 +759,16 @@ hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma
   if (rows <= 0 || d <= 0) return hipSuccess;
   const dim3 grid(grid_for(static_cast<size_t>(rows), 4, 1024)), block(256);  // rows walked grid-stride
   const int nb = d >> 6;
+  if (d == 1280) {  // ESM-2 650M
+    hipLaunchKernelGGL(layernorm_x86_rows_kernel<20>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, absmax,
+                       round16);
+    return hipGetLastError();
+  }
+  if (d == 320) {  // ESM-2 8M
+    hipLaunchKernelGGL(layernorm_x86_rows_kernel<5>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, absmax,
+                       round16);
+    return hipGetLastError();
+  }
   if (nb <= 5)
     hipLaunchKernelGGL(layernorm_x86_kernel<5>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, d, absmax,
                        round16);
