@@ -1895,7 +1895,7 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
   ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_TRY(ctx->time_begin("attention", &slot));
   ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
-                                    x86_score_scratch(P, a, Tf, H)));
+                                    x86_score_scratch(P, a, Tf, H), md.work, P.nwork));
   ESM_TRY(ctx->time_end(slot));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
@@ -1939,7 +1939,7 @@ int layer_f32_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer
   ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
   ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
   ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
-                                    x86_score_scratch(P, a, Tf, H)));
+                                    x86_score_scratch(P, a, Tf, H), md.work, P.nwork));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
   ESM_TRY(linear(a.attn, L.out, a.hidden, kF32Resid));
   ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, nullptr,
@@ -2028,7 +2028,9 @@ int stage_part(esm_gfx950_ctx* ctx, esm_gfx950_model* m, esm_gfx950_model::Part&
     for (int t = mh.cu[b]; t < mh.cu[b + 1]; ++t) mh.tok_scale[t] = (mk && mk[t] == 0) ? 0.0f : scale;
   }
   build_pos(mh.cu, B, mh.pos);
-  const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32;
+  // The x86-exact attention takes 64-query tiles, longest sequences first.
+  const bool mfma_attn = c.weights_int8 && c.attention_mode != ESM_GFX950_ATTN_MODE_FP32 &&
+                         m->numerics == ESM_GFX950_NUMERICS_DEFAULT;
   std::vector<AttnWork> work;
   build_work(mh.cu, B, H, mfma_attn ? kAttnMfmaQTile : kAttnF32QTile, &work, mfma_attn);
   if (work.size() > mh.work_cap)

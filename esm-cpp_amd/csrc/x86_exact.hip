@@ -437,16 +437,24 @@ __device__ __forceinline__ size_t score_base(const int* __restrict__ cu, int b, 
 // instead of recomputing it: the same values, the same order of operations.
 // Regions: sequence b at score_base, then head h at h x pad64(L) x L, then
 // query tile t at t x 64 x L. Without SC every pass recomputes the scores.
+// work: null (the grid is (query tiles, heads, sequences)), or one
+// (sequence, head, 64-query tile) item per workgroup, longest sequences
+// first so that their long items start early and the short ones fill in.
 template <int DH, bool SC>
 __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, int ld, const int* __restrict__ cu,
                                                       int heads, float* __restrict__ out, int ldo,
-                                                      float* __restrict__ scores) {
+                                                      float* __restrict__ scores, const AttnWork* __restrict__ work) {
   __shared__ __attribute__((aligned(16))) float ks[kX86Keys][DH];
   __shared__ __attribute__((aligned(16))) float vs[kX86Keys][DH];
-  const int b = blockIdx.z, h = blockIdx.y;
+  int b = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * 64;
+  if (work) {
+    const AttnWork w = work[blockIdx.x];
+    b = w.seq;
+    h = w.head;
+    q0 = w.q0;
+  }
   const int s0 = cu[b], L = cu[b + 1] - s0;
-  const int q0 = blockIdx.x * 64;
   if (q0 >= L) return;
   const int lane = threadIdx.x;
   const int i = min(q0 + lane, L - 1);
@@ -819,14 +827,17 @@ size_t attention_x86_score_floats(const int* cu, int batch, int heads) {
 
 hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
                                 int batch, int heads, int max_len, float* out, int ldo, hipStream_t s,
-                                float* scores) {
+                                float* scores, const AttnWork* work, int nwork) {
   if (batch <= 0 || max_len <= 0) return hipSuccess;
-  const dim3 grid((max_len + 63) / 64, heads, batch), block(64);
+  if (work && nwork <= 0) return hipSuccess;
+  const dim3 grid = work ? dim3(nwork) : dim3((max_len + 63) / 64, heads, batch), block(64);
 #define ESM_ATTN_X86(DH)                                                                                           \
   if (scores)                                                                                                      \
-    hipLaunchKernelGGL((attn_x86_kernel<DH, true>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, scores);  \
+    hipLaunchKernelGGL((attn_x86_kernel<DH, true>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, scores,   \
+                       work);                                                                                      \
   else                                                                                                             \
-    hipLaunchKernelGGL((attn_x86_kernel<DH, false>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, nullptr);
+    hipLaunchKernelGGL((attn_x86_kernel<DH, false>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, nullptr, \
+                       work);
   switch (head_dim) {
     case 16: ESM_ATTN_X86(16) break;
     case 32: ESM_ATTN_X86(32) break;
