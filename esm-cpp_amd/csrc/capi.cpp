@@ -1889,10 +1889,39 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
   if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
   // Q, K and V are three linears of N = d each in the reference.
   ESM_TRY(quant(a.ln, d, ldq_d, a.absmax, d, a.absmax + 4));
-  ESM_TRY(linear(L.qkv, ldq_d, a.qkv, "qkv"));
   const float q_scale = m->q_scale_folded ? 1.0f : 1.0f / std::sqrt(static_cast<float>(dh));
-  ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
-  ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+  {
+    // ScaleInplace and RopeApplyVarlenAvx512 in the QKV GEMM's epilogue
+    // (64-wide heads, pipelined kernel), else as passes of their own.
+    GemmI8Args g;
+    g.A = a.xq;
+    g.lda = ldq_d;
+    g.W = L.qkv.w8;
+    g.ldw = L.qkv.ldk;
+    g.M = T;
+    g.N = L.qkv.N;
+    g.K = L.qkv.ldk;
+    g.a_scale = a.xs;
+    g.w_scale = L.qkv.ws;
+    g.bias = L.qkv.bias;
+    g.C_f32 = a.qkv;
+    g.ldc = L.qkv.N;
+    g.d_model = d;
+    g.pos = md.pos;
+    g.rope_cos = md.cos_t;
+    g.rope_sin = md.sin_t;
+    g.q_scale = q_scale;
+    g.rope_x86 = 1;
+    if (dh == kHeadDimMfma && gemm_i8_pipelined_ok(g)) {
+      ESM_TRY(ctx->time_begin("qkv", &slot));
+      ESM_HIP(ctx, launch_gemm_i8(g, kEpiQkvRopeF32, s));
+      ESM_TRY(ctx->time_end(slot));
+    } else {
+      ESM_TRY(linear(L.qkv, ldq_d, a.qkv, "qkv"));
+      ESM_HIP(ctx, launch_rope_x86(a.qkv, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, q_scale, s));
+      ESM_HIP(ctx, launch_rope_x86(a.qkv + d, 3 * d, md.pos, T, H, dh, md.cos_t, md.sin_t, dh, 1.0f, s));
+    }
+  }
   ESM_TRY(ctx->time_begin("attention", &slot));
   ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
                                     x86_score_scratch(P, a, Tf, H), md.work, P.nwork));

@@ -535,7 +535,10 @@ __device__ __forceinline__ void qkv_head(const GemmI8Args& p, const i32x16 (&acc
           const float sn = u == 0 ? s4.x : u == 1 ? s4.y : u == 2 ? s4.z : s4.w;
           // Explicit fused forms: every instantiation (full / edge tile)
           // rounds a row identically, whatever the compiler would contract.
-          const float y1 = __builtin_fmaf(x1, c, -(x2 * sn));
+          float y1 = __builtin_fmaf(x1, c, -(x2 * sn));
+          if constexpr (EPI == kEpiQkvRopeF32) {
+            if (p.rope_x86) y1 = __builtin_fmaf(-x2, sn, x1 * c);
+          }
           const float y2 = __builtin_fmaf(x2, c, x1 * sn);
           x1 = y1;
           x2 = y2;

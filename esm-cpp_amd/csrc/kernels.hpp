@@ -68,6 +68,10 @@ struct GemmI8Args {
   const float* rope_sin = nullptr;   // [max_len, 32]
   float q_scale = 1.0f;
   float q_prescale = 1.0f;  // kEpiQkvSplit: power of two applied to Q before the split
+  // kEpiQkvRopeF32, pipelined kernel: rotate as RopeApplyVarlenAvx512 does
+  // (reference src/kernels/rope.cpp:90-152), the first element of each pair
+  // as fma(-hi, s, lo * c) instead of fma(lo, c, -(hi * s)).
+  int rope_x86 = 0;
   int cus = 0;              // CUs the launch can expect to have to itself (0: the device's)
   // Split-K, int32 output (kEpiI32): the grid holds splits x tiles
   // workgroups, and C_i32 holds `splits` consecutive [M, ldc] planes of
