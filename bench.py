@@ -32,6 +32,10 @@ parity: on that batch, the GPU in x86-exact numerics against the CPU run
 33-layer fixture (tests/golden/full_depth_650m.npz) the GPU's default modes
 against the oracle and the reference, next to the reference's own spread.
 
+--act-mode tensor times the headline batch with per-tensor activation
+scales, --numerics x86_avx512 / x86_amx in the x86-exact numerics (per-tensor
+scales): the records the profiles of those modes come from.
+
 Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
 """
 from __future__ import annotations
@@ -357,6 +361,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=["varlen", "uniform"], default="varlen")
     ap.add_argument("--act-mode", choices=["token", "tensor"], default="token")
+    ap.add_argument("--numerics", choices=["default", "x86_avx512", "x86_amx"], default="default",
+                    help="numerics of the timed forward; the x86-exact modes take per-tensor activation scales")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the uniform and config-5 records")
     ap.add_argument("--no-parity", action="store_true")
@@ -383,8 +389,12 @@ def main():
     log(f"weights + batch in {time.time() - t0:.1f}s: T={batch.total_tokens} residues={batch.residues}")
 
     dev = eg.Device(0)
-    mode = eg.ACT_PER_TOKEN if args.act_mode == "token" else eg.ACT_PER_TENSOR
+    numerics = {"default": eg.NUMERICS_DEFAULT, "x86_avx512": eg.NUMERICS_X86_AVX512,
+                "x86_amx": eg.NUMERICS_X86_AMX}[args.numerics]
+    mode = eg.ACT_PER_TOKEN if args.act_mode == "token" and numerics == eg.NUMERICS_DEFAULT else eg.ACT_PER_TENSOR
     model = eg.Model(dev, weights, int8=True, act_mode=mode)
+    if numerics != eg.NUMERICS_DEFAULT:
+        model.set_numerics(numerics)
     T = batch.total_tokens
     ms_plain, ms_events, sites, used = measure(dev, model, batch, cfg, args.steps, args.warmup, args.parts)
     model.free()
@@ -404,7 +414,7 @@ def main():
                                         syn.config5_batch(), args))
         del w5
         log(f"extra {workloads[-1]['workload']}: {workloads[-1]['ms_per_step']} ms")
-        if args.workload == "varlen" and mode == eg.ACT_PER_TOKEN:
+        if args.workload == "varlen" and mode == eg.ACT_PER_TOKEN and numerics == eg.NUMERICS_DEFAULT:
             # The reference's own activation scaling (one dynamic scale per
             # tensor), default numerics: one sequence group (the scale spans
             # the batch).
@@ -444,6 +454,7 @@ def main():
                                f"{len(batch.lengths)} sequences",
                    "tokens": T, "residues": batch.residues, "sequences": int(len(batch.lengths)),
                    "act_quant": "per-token" if mode == eg.ACT_PER_TOKEN else "per-tensor",
+                   "numerics": args.numerics,
                    "attention": "split-fp16 (hi+lo, 3 MFMAs per product) fp32-accurate MFMA", "parallelism": "single GPU",
                    "streams": used},
         "tokens_per_s": round(T / (ms_plain * 1e-3), 1),
