@@ -1847,7 +1847,8 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
   const size_t Td = static_cast<size_t>(T) * d, Tf = static_cast<size_t>(T) * f;
   hipStream_t s = ctx->stream;
   int slot;
-  auto linear = [&](const DevLinear& W, int lda, float* C, const char* site) -> int {
+  auto linear = [&](const DevLinear& W, int lda, float* C, const char* site, int epi = kEpiF32,
+                    float* tensor_absmax = nullptr) -> int {
     GemmI8Args g;
     g.A = a.xq;
     g.lda = lda;
@@ -1861,8 +1862,9 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
     g.bias = W.bias;
     g.C_f32 = C;
     g.ldc = W.N;
+    g.tensor_absmax = tensor_absmax;
     ESM_TRY(ctx->time_begin(site, &slot));
-    ESM_HIP(ctx, launch_gemm_i8(g, kEpiF32, s));
+    ESM_HIP(ctx, launch_gemm_i8(g, epi, s));
     return ctx->time_end(slot);
   };
 
@@ -1941,8 +1943,8 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
     ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
   }
   ESM_TRY(quant(a.ln, d, ldq_d, a.absmax + 2, f, a.absmax + 6));
-  ESM_TRY(linear(L.fc1, ldq_d, a.inter, "fc1"));
-  ESM_HIP(ctx, launch_gelu_x86(a.inter, a.inter, Tf, a.absmax + 3, s));
+  // fc1 + GeluAvx512 (and the GELU output's maximum) in the GEMM's epilogue.
+  ESM_TRY(linear(L.fc1, ldq_d, a.inter, "fc1", kEpiF32GeluX86, a.absmax + 3));
   if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));
   ESM_TRY(quant(a.inter, f, ldq_f, a.absmax + 3, d, a.absmax + 7));
   return linear(L.fc2, ldq_f, a.ybuf, "fc2");

@@ -32,6 +32,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "x86_math.hpp"
 
 namespace esm_gfx950 {
 namespace {
@@ -257,6 +258,7 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
             float v = __builtin_fmaf(static_cast<float>(acc[bm][bn][r]), as * ws[bn], bs[bn]);
             if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
             if constexpr (EPI == kEpiF32GeluAs) v = 0.5f * gelu2_as(v);
+            if constexpr (EPI == kEpiF32GeluX86) v = gelu_x86(v);
             if (rok && col < p.N) {
               const size_t o = static_cast<size_t>(row) * p.ldc + col;
               if constexpr (EPI == kEpiF32Resid) {
@@ -270,7 +272,8 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
               }
             }
           }
-          if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32) {
+          if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32GeluX86 ||
+                        EPI == kEpiF32) {
             if (p.row_absmax) {
               // Lanes sharing lg hold the same row; reduce over the 16 of them.
 #pragma unroll
@@ -281,7 +284,8 @@ __device__ __forceinline__ void epilogue(const GemmI8Args& p, const i32x4 (&acc)
             tmax = fmaxf(tmax, rmax);
           }
         }
-      if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32) {
+      if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32GeluX86 ||
+                    EPI == kEpiF32) {
         if (p.tensor_absmax) {
           tmax = wave_max(tmax);
           if ((threadIdx.x & 63) == 0) atomic_max_nonneg(p.tensor_absmax, tmax);
@@ -782,6 +786,7 @@ __device__ __forceinline__ void epilogue32(const GemmI8Args& p, const i32x16 (&a
               float v = __builtin_fmaf(static_cast<float>(acc[i][j][r]), asv[u] * ws[j], bs[j]);
               if constexpr (EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ) v = gelu_erf(v);
               if constexpr (EPI == kEpiF32GeluAs) v = 0.5f * gelu2_as(v);
+              if constexpr (EPI == kEpiF32GeluX86) v = gelu_x86(v);
               if (rok && col_ok(lc0 + j * 32)) {
                 const uint32_t off = lane_c + static_cast<uint32_t>(i * 32 + q * 8 + u) * ldc + j * 32;
                 if constexpr (EPI == kEpiF32GeluQ) {
@@ -1098,7 +1103,8 @@ __global__ __launch_bounds__((Tile<BLK_M, BLK_N>::kThreads), 1) void gemm_i8_v3_
     for (int w = 0; w < TL::kWaves; ++w) any |= s_risk[w];
     nan_risk = any != 0;
   }
-  constexpr bool kMaxable = EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32;
+  constexpr bool kMaxable =
+      EPI == kEpiF32Gelu || EPI == kEpiF32GeluQ || EPI == kEpiF32GeluAs || EPI == kEpiF32GeluX86 || EPI == kEpiF32;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
   if (kMaxable && (p.row_absmax || p.tensor_absmax)) {
     if (full)
@@ -1178,6 +1184,7 @@ hipError_t launch_v1(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiQkvRope: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRope>), grid, block, 0, s, p); break;
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluQ>), grid, block, 0, s, p); break;
     case kEpiF32GeluAs: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluAs>), grid, block, 0, s, p); break;
+    case kEpiF32GeluX86: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiF32GeluX86>), grid, block, 0, s, p); break;
     case kEpiQkvRopeF32: hipLaunchKernelGGL((gemm_i8_kernel<Cfg, kEpiQkvRopeF32>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
@@ -1199,6 +1206,9 @@ hipError_t launch_v3_tile(const GemmI8Args& p, int epi, hipStream_t s) {
     case kEpiF32GeluQ: hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluQ>), grid, block, 0, s, p); break;
     case kEpiF32GeluAs:
       hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluAs>), grid, block, 0, s, p);
+      break;
+    case kEpiF32GeluX86:
+      hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiF32GeluX86>), grid, block, 0, s, p);
       break;
     case kEpiQkvRopeF32:
       hipLaunchKernelGGL((gemm_i8_v3_kernel<BLK_M, BLK_N, kEpiQkvRopeF32>), grid, block, 0, s, p);

@@ -36,6 +36,9 @@ enum GemmEpilogue : int {
                       // 7.1.26 (gelu2_as / 2, the GELU of the fused GELU +
                       // quantisation passes and of the reference's AVX-512
                       // Gelu) instead of erff
+  kEpiF32GeluX86 = 10,  // as kEpiF32Gelu with the reference's GeluAvx512
+                        // (gelu_x86) on the dequantised value: the x86-exact
+                        // forward's fc1 + Gelu, bit for bit
 };
 
 // Split-fp16 word of an fp32 value x: low half fp16(x), high half
