@@ -361,7 +361,7 @@ template <bool LONG>
 __global__ __launch_bounds__(256, 4) void attn_x3_kernel(
     const uint32_t* __restrict__ q, int ldq, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ kl,
     const uint16_t* __restrict__ vh, const uint16_t* __restrict__ vl, int ldp, float s2, const int* __restrict__ cu,
-    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out) {
+    const AttnWork* __restrict__ work, float* __restrict__ out, int ld_out, float* __restrict__ part_max) {
   // Two chunk buffers, each [K hi | K lo | V hi | V lo] planes of 64 rows x
   // 128 bytes.
   __shared__ __attribute__((aligned(1024))) uint8_t sbuf[2 * kChunkBytes];
@@ -369,7 +369,12 @@ __global__ __launch_bounds__(256, 4) void attn_x3_kernel(
   const AttnWork w = work[blockIdx.x];
   const int start = cu[w.seq];
   const int L = cu[w.seq + 1] - start;
-  if (w.q0 >= L) return;  // padding item of the work list (uniform)
+  // part_max (optional): slot 4 * item + wave receives the largest |output|
+  // the wave stores (0 for a wave or item with no queries).
+  if (w.q0 >= L) {  // padding item of the work list (uniform)
+    if (part_max && threadIdx.x < 4) part_max[blockIdx.x * 4 + threadIdx.x] = 0.0f;
+    return;
+  }
   const int hoff = w.head * 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -569,7 +574,10 @@ __global__ __launch_bounds__(256, 4) void attn_x3_kernel(
   }
 
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave is done with the chunks
-  if (!active) return;
+  if (!active) {
+    if (part_max && lane == 0) part_max[blockIdx.x * 4 + wave] = 0.0f;
+    return;
+  }
   // Output: rows of o[qb][db] are positions db*16 + 4 lg .. +4, i.e. dims i,
   // i + 32, i + 1, i + 33 for i = 8 db + 2 lg. Each wave puts its 32 x 64
   // tile in natural order into its own 8 KB of the chunk buffers (free after
@@ -592,12 +600,20 @@ __global__ __launch_bounds__(256, 4) void attn_x3_kernel(
     }
   }
   const int unit = lane & 15;
+  float m = 0.0f;
 #pragma unroll
   for (int r4 = 0; r4 < 8; ++r4) {
     const int row = r4 * 4 + (lane >> 4);
     const float4 val = *reinterpret_cast<const float4*>(stage + soff(row, unit * 4));
     const int qi = qbase + row;
-    if (qi < L) *reinterpret_cast<float4*>(out + static_cast<size_t>(start + qi) * ld_out + hoff + unit * 4) = val;
+    if (qi < L) {
+      *reinterpret_cast<float4*>(out + static_cast<size_t>(start + qi) * ld_out + hoff + unit * 4) = val;
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(val.x), fabsf(val.y)), fmaxf(fabsf(val.z), fabsf(val.w))));
+    }
+  }
+  if (part_max) {
+    m = wave_max(m);
+    if (lane == 0) part_max[blockIdx.x * 4 + wave] = m;
   }
 }
 
@@ -700,15 +716,15 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 hipError_t launch_attention_x3(const uint32_t* q, int ldq, const uint16_t* kh, const uint16_t* kl, const uint16_t* vh,
                                const uint16_t* vl, int ldp, float q_prescale, const int* cu_seqlens,
                                const AttnWork* work, int num_work, float* out, int ld_out, int max_len,
-                               hipStream_t s) {
+                               hipStream_t s, float* part_max) {
   if (num_work <= 0) return hipSuccess;
   const float s2 = kLog2e / q_prescale;
   if (max_len > kAttnLongSeq)
     hipLaunchKernelGGL(attn_x3_kernel<true>, dim3(num_work), dim3(256), 0, s, q, ldq, kh, kl, vh, vl, ldp, s2,
-                       cu_seqlens, work, out, ld_out);
+                       cu_seqlens, work, out, ld_out, part_max);
   else
     hipLaunchKernelGGL(attn_x3_kernel<false>, dim3(num_work), dim3(256), 0, s, q, ldq, kh, kl, vh, vl, ldp, s2,
-                       cu_seqlens, work, out, ld_out);
+                       cu_seqlens, work, out, ld_out, part_max);
   return hipGetLastError();
 }
 

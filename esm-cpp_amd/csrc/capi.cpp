@@ -1615,13 +1615,20 @@ int layer_int8(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLayer& L
       // and V's hi and lo fp16 planes (d elements each).
       const auto* w = reinterpret_cast<const uint32_t*>(a.qkv);
       const auto* h16 = reinterpret_cast<const uint16_t*>(a.qkv);
+      // Per tensor, the attention kernel leaves its waves' maxima (in the
+      // FFN buffer, dead here) and one workgroup reduces them.
+      float* part = !tok && static_cast<size_t>(nwork) * 4 <= Tf ? a.inter : nullptr;
       ESM_HIP(ctx, launch_attention_x3(w, 3 * d, h16 + 2 * d, h16 + 3 * d, h16 + 4 * d, h16 + 5 * d, 6 * d, kQPrescale,
-                                       md.cu, md.work, nwork, a.attn, d, max_len, s));
+                                       md.cu, md.work, nwork, a.attn, d, max_len, s, part));
+      if (part)
+        ESM_HIP(ctx, launch_max_of(part, static_cast<size_t>(nwork) * 4, amax_attn, s));
+      else if (!tok)
+        ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
     } else {
       ESM_HIP(ctx, launch_attention_f32(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, md.work, nwork, a.attn,
                                         d, s));
+      if (!tok) ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
     }
-    if (!tok) ESM_HIP(ctx, launch_absmax(a.attn, static_cast<size_t>(T) * d, amax_attn, s));
   } else {
     const int qk16 = c.attention_mode == ESM_GFX950_ATTN_MODE_FP16 ? 1 : 0;
     ESM_HIP(ctx, launch_attention_mfma(a.qb, a.kb, a.vb, qk16, 0, d, md.cu, md.work, nwork, a.attn, d, amax_attn, s));

@@ -563,6 +563,22 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
   block_atomic_max_nonneg(absmax, m);
 }
 
+// One workgroup of 1024 threads: the largest of n non-negative floats.
+__global__ __launch_bounds__(1024) void max_of_kernel(const float* __restrict__ x, size_t n, float* out) {
+  __shared__ float s_max[16];
+  float m = 0.0f;
+  for (size_t i = threadIdx.x; i < n; i += 1024) m = fmaxf(m, x[i]);
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = s_max[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) r = fmaxf(r, s_max[w]);
+    *out = r;
+  }
+}
+
 __global__ void fill_kernel(float* x, size_t n, float v) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
@@ -835,6 +851,11 @@ hipError_t launch_absmax(const float* x, size_t n, float* absmax, hipStream_t s)
   if (g < 1) g = 1;
   if (g > 512) g = 512;  // two per CU: one atomic each
   hipLaunchKernelGGL(absmax_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, x, n, absmax);
+  return hipGetLastError();
+}
+
+hipError_t launch_max_of(const float* x, size_t n, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(max_of_kernel, dim3(1), dim3(1024), 0, s, x, n, out);
   return hipGetLastError();
 }
 

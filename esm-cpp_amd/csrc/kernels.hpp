@@ -191,11 +191,13 @@ hipError_t launch_attention_mfma(const uint16_t* q, const uint16_t* k,
 // out is written in natural dim order. Softmax logits are (q.k) / q_prescale.
 // max_len: the batch's longest sequence; past kAttnLongSeq tokens the
 // long-sequence variant runs (same results, bit for bit).
+// part_max (optional, 4 * num_work floats): each item's four waves' largest
+// |output|; launch_max_of over them gives the output's maximum.
 constexpr int kAttnLongSeq = 256;
 hipError_t launch_attention_x3(const uint32_t* q, int ldq, const uint16_t* kh, const uint16_t* kl, const uint16_t* vh,
                                const uint16_t* vl, int ldp, float q_prescale, const int* cu_seqlens,
                                const AttnWork* work, int num_work, float* out, int ld_out, int max_len,
-                               hipStream_t s);
+                               hipStream_t s, float* part_max = nullptr);
 // fp32 [rows, d] (row stride ld_x, d % 64 == 0) -> that layout: split words
 // of x * scale (words != null, row stride ld_out words) or hi / lo planes
 // (planes != null: hi at [r * ld_out + c], lo d elements further).
@@ -272,6 +274,9 @@ hipError_t launch_quant_tensor(const float* x, int ldx, int rows, int cols,
                                float* scales, hipStream_t s);
 hipError_t launch_absmax(const float* x, size_t n, float* absmax,
                          hipStream_t s);
+// *out = the largest of n non-negative floats x (NaNs ignored), one
+// workgroup; *out need not be cleared.
+hipError_t launch_max_of(const float* x, size_t n, float* out, hipStream_t s);
 hipError_t launch_fill_f32(float* x, size_t n, float v, hipStream_t s);
 // Activation observer gather: out[w] = |x[pos[w]]| (gelu != 0: |GELU(x[pos[w]])|
 // with the Abramowitz & Stegun erf of the fused GELU + quantisation kernel).
