@@ -371,7 +371,8 @@ int esm_gfx950_model_set_first_block_fc1_fp16(esm_gfx950_ctx* ctx, esm_gfx950_mo
  * quantisation pass reads those: 3 bytes per value instead of 4 each way. An
  * int8 code can then differ by one from the fp32 intermediate's only where
  * the rounding (relative 2^-16 at most) crosses a quantisation midpoint.
- * Observed forwards, per-tensor mode and the x86 numerics keep fp32. */
+ * Per-tensor mode and the x86 numerics keep fp32; observed forwards keep the
+ * setting. */
 int esm_gfx950_model_set_ffn_intermediate_bits(esm_gfx950_ctx* ctx, esm_gfx950_model* model, int bits);
 /* Model::LoadFromGguf (reference src/model.cpp:229-298): creates a model
  * from an esm.cpp GGUF v3 file (src/io/gguf.cpp) -- esm.* metadata for the
@@ -514,9 +515,10 @@ int esm_gfx950_observer_percentile(const esm_gfx950_observer* obs, const char* s
  * "layer{i}.ffn_ln_output" (before the first-block fp16 rounding) and
  * "layer{i}.inter_gelu" over the batch's [T, d] / [T, ffn] values in packed
  * row order (model.cpp:952-955,996-999,1023-1026,1047-1050). The batch runs as
- * one sequence group, and in per-token W8A8 with the fp32 FFN intermediate
- * (the observer samples fc1's fp32 output), so its logits are those of
- * esm_gfx950_model_set_ffn_intermediate_bits(32). T == 0 observes nothing. */
+ * one sequence group with the model's FFN intermediate width
+ * (esm_gfx950_model_set_ffn_intermediate_bits; at 24 bits "inter_gelu" samples
+ * GELU of the rounded values the quantisation reads), so its logits equal
+ * esm_gfx950_forward_packed's. T == 0 observes nothing. */
 int esm_gfx950_forward_with_observer(esm_gfx950_ctx* ctx, esm_gfx950_model* model, const int32_t* ids,
                                      const int32_t* cu_seqlens, int batch_size, int total_tokens, float* logits,
                                      esm_gfx950_observer* obs);
