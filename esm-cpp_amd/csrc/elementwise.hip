@@ -37,13 +37,19 @@ __device__ __forceinline__ float4 round_f16(float4 y) {
 // load is issued before any value is used: a chunk past `cols` re-reads
 // column 0 (in bounds) and is then zeroed, so no load sits in a branch that
 // would make the wave wait for it before issuing the next.
+// load_row_raw issues the loads alone and mask_row zeroes the chunks past
+// `cols` once they are used, so a caller can keep a row's loads in flight.
 template <int NV>
-__device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int cols, int lane, float4 (&v)[NV]) {
+__device__ __forceinline__ void load_row_raw(const float* __restrict__ xr, int cols, int lane, float4 (&v)[NV]) {
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = (j * 64 + lane) * 4;
     v[j] = *reinterpret_cast<const float4*>(xr + (c < cols ? c : 0));
   }
+}
+
+template <int NV>
+__device__ __forceinline__ void mask_row(int cols, int lane, float4 (&v)[NV]) {
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const bool ok = (j * 64 + lane) * 4 < cols;
@@ -54,14 +60,58 @@ __device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int c
   }
 }
 
+template <int NV>
+__device__ __forceinline__ void load_row_vec(const float* __restrict__ xr, int cols, int lane, float4 (&v)[NV]) {
+  load_row_raw<NV>(xr, cols, lane, v);
+  mask_row<NV>(cols, lane, v);
+}
+
 // ---- LayerNorm with the row cached in registers (d % 4 == 0, d <= NV*256).
-// With resid != null the row is first updated in place, x += resid (the
-// residual add that precedes the next LayerNorm, reference src/model.cpp:1013
-// and :1063), and the LayerNorm runs on the sum.
-// SPLIT: the residual arrives as split-K partial sums (SplitResid).
+// The LayerNorm of the row in v (residual already added), in place; returns
+// the row's largest |output|.
+template <int NV>
+__device__ __forceinline__ float ln_core(const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+                                         int d, int lane, int round16, float4 (&v)[NV]) {
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = wave_sum(sum) / static_cast<float>(d);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    const float a = v[j].x - mean, b = v[j].y - mean, e = v[j].z - mean, f = v[j].w - mean;
+    const float t = (a * a + b * b) + (e * e + f * f);
+    sq += c < d ? t : 0.0f;
+  }
+  const float var = wave_sum(sq) / static_cast<float>(d);
+  const float inv_std = 1.0f / sqrtf(var + eps);
+  float4 g[NV], bt[NV];
+  load_row_vec<NV>(gamma, d, lane, g);
+  load_row_vec<NV>(beta, d, lane, bt);
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * 64 + lane) * 4;
+    float4 y;
+    y.x = (v[j].x - mean) * inv_std * g[j].x + bt[j].x;
+    y.y = (v[j].y - mean) * inv_std * g[j].y + bt[j].y;
+    y.z = (v[j].z - mean) * inv_std * g[j].z + bt[j].z;
+    y.w = (v[j].w - mean) * inv_std * g[j].w + bt[j].w;
+    if (round16) y = round_f16(y);
+    v[j] = y;
+    if (c < d) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  }
+  return amax;
+}
+
 // One wave's row: the residual update, the LayerNorm into v, and the row's
-// absolute maximum (returned). The kernels below share this body, so every
-// pass over a row computes the same values.
+// absolute maximum (returned). With resid != null the row is first updated
+// in place, x += resid (the residual add that precedes the next LayerNorm,
+// reference src/model.cpp:1013 and :1063), and the LayerNorm runs on the
+// sum; SPLIT: the residual arrives as split-K partial sums (SplitResid). The
+// kernels below share ln_core, so every pass over a row computes the same
+// values.
 template <int NV, bool SPLIT>
 __device__ __forceinline__ float ln_row(float* __restrict__ x, const float* __restrict__ resid,
                                         const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
@@ -111,38 +161,9 @@ __device__ __forceinline__ float ln_row(float* __restrict__ x, const float* __re
       if (c < d) *reinterpret_cast<float4*>(xr + c) = v[j];
     }
   }
-  float sum = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) sum += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-  const float mean = wave_sum(sum) / static_cast<float>(d);
-  float sq = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (j * 64 + lane) * 4;
-    const float a = v[j].x - mean, b = v[j].y - mean, e = v[j].z - mean, f = v[j].w - mean;
-    const float t = (a * a + b * b) + (e * e + f * f);
-    sq += c < d ? t : 0.0f;
-  }
-  const float var = wave_sum(sq) / static_cast<float>(d);
-  const float inv_std = 1.0f / sqrtf(var + eps);
-  float4 g[NV], bt[NV];
-  load_row_vec<NV>(gamma, d, lane, g);
-  load_row_vec<NV>(beta, d, lane, bt);
-  float amax = 0.f;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = (j * 64 + lane) * 4;
-    float4 y;
-    y.x = (v[j].x - mean) * inv_std * g[j].x + bt[j].x;
-    y.y = (v[j].y - mean) * inv_std * g[j].y + bt[j].y;
-    y.z = (v[j].z - mean) * inv_std * g[j].z + bt[j].z;
-    y.w = (v[j].w - mean) * inv_std * g[j].w + bt[j].w;
-    if (round16) y = round_f16(y);
-    v[j] = y;
-    if (c < d) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-  }
-  return amax;
+  return ln_core<NV>(gamma, beta, eps, d, lane, round16, v);
 }
+
 
 // !QUANT: the LayerNorm stored to out (if not null). With a per-tensor
 // absmax the grid is bounded and walks the rows (one atomic per block: the
@@ -160,6 +181,24 @@ __global__ __launch_bounds__(256) void layernorm_vec_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   float4 v[NV];
+  if (!QUANT && tensor_absmax && !SPLIT && !resid && !out) {
+    // The maximum alone: the wave's next row is loaded while this one is
+    // reduced, so each wave keeps a row's loads in flight.
+    float am = 0.f;
+    const int step = gridDim.x * kRowsPerBlock;
+    int row = blockIdx.x * kRowsPerBlock + wave;
+    float4 nv[NV];
+    if (row < rows) load_row_raw<NV>(x + static_cast<size_t>(row) * d, d, lane, nv);
+    for (; row < rows; row += step) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) v[j] = nv[j];
+      mask_row<NV>(d, lane, v);
+      if (row + step < rows) load_row_raw<NV>(x + static_cast<size_t>(row + step) * d, d, lane, nv);
+      am = fmaxf(am, ln_core<NV>(gamma, beta, eps, d, lane, round16, v));
+    }
+    block_atomic_max_nonneg(tensor_absmax, am);
+    return;
+  }
   if (!QUANT && tensor_absmax) {
     float am = 0.f;
     for (int base = blockIdx.x * kRowsPerBlock; base < rows; base += gridDim.x * kRowsPerBlock) {
