@@ -1892,12 +1892,31 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
     }
     return ESM_GFX950_OK;
   };
+  // Without an observer (which samples the fp32 LayerNorm output), a
+  // LayerNorm and its quantisation run as two passes over hidden: the
+  // maxima (and the residual add), then the LayerNorm again, quantised; the
+  // same codes and scales as the LayerNorm output's launch_quant_tensor.
+  const bool ln_two_pass = !ob && layernorm_x86_rows_ok(d);
+  auto ln_quant = [&](const float* resid, const float* gamma, const float* beta, int r16, float* amax, int n_out,
+                      float* slot) -> int {
+    const bool tail = amx && T >= 32 && n_out % 32 == 0 && d % 64 == 0 && t_main < T;
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, resid, gamma, beta, c.layer_norm_eps, nullptr, T, d, amax, r16, s,
+                                      tail ? slot : nullptr, tail ? t_main : T));
+    ESM_HIP(ctx, launch_layernorm_x86_quant(a.hidden, gamma, beta, c.layer_norm_eps, T, d, amax, tail ? slot : nullptr,
+                                            tail ? t_main : T, a.xq, ldq_d, a.xs, r16, s));
+    return ESM_GFX950_OK;
+  };
 
   ESM_HIP(ctx, launch_fill_f32(a.absmax, 8, 0.0f, s));
-  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, 0, s));
-  if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
   // Q, K and V are three linears of N = d each in the reference.
-  ESM_TRY(quant(a.ln, d, ldq_d, a.absmax, d, a.absmax + 4));
+  if (ln_two_pass) {
+    ESM_TRY(ln_quant(resid_in, L.ln1_w, L.ln1_b, 0, a.absmax, d, a.absmax + 4));
+  } else {
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, resid_in, L.ln1_w, L.ln1_b, c.layer_norm_eps, a.ln, T, d, a.absmax, 0,
+                                      s));
+    if (ob) ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+    ESM_TRY(quant(a.ln, d, ldq_d, a.absmax, d, a.absmax + 4));
+  }
   const float q_scale = m->q_scale_folded ? 1.0f : 1.0f / std::sqrt(static_cast<float>(dh));
   {
     // ScaleInplace and RopeApplyVarlenAvx512 in the QKV GEMM's epilogue
@@ -1939,17 +1958,21 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
   ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
   ESM_TRY(quant(a.attn, d, ldq_d, a.absmax + 1, d, a.absmax + 5));
   ESM_TRY(linear(L.out, ldq_d, a.ybuf, "out"));
-  ESM_HIP(ctx, launch_layernorm_x86(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
-                                    round16, s));
-  if (ob && round16) {
-    // The observer sees the LayerNorm output before the fp16 rounding.
-    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr, 0,
-                                      s));
-    ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
-  } else if (ob) {
-    ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+  if (ln_two_pass) {
+    ESM_TRY(ln_quant(a.ybuf, L.ln2_w, L.ln2_b, round16, a.absmax + 2, f, a.absmax + 6));
+  } else {
+    ESM_HIP(ctx, launch_layernorm_x86(a.hidden, a.ybuf, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.ln, T, d, a.absmax + 2,
+                                      round16, s));
+    if (ob && round16) {
+      // The observer sees the LayerNorm output before the fp16 rounding.
+      ESM_HIP(ctx, launch_layernorm_x86(a.hidden, nullptr, L.ln2_w, L.ln2_b, c.layer_norm_eps, a.lm_a, T, d, nullptr,
+                                        0, s));
+      ESM_TRY(ob->capture(ctx, a.lm_a, Td, 0));
+    } else if (ob) {
+      ESM_TRY(ob->capture(ctx, a.ln, Td, 0));
+    }
+    ESM_TRY(quant(a.ln, d, ldq_d, a.absmax + 2, f, a.absmax + 6));
   }
-  ESM_TRY(quant(a.ln, d, ldq_d, a.absmax + 2, f, a.absmax + 6));
   // fc1 + GeluAvx512 (and the GELU output's maximum) in the GEMM's epilogue.
   ESM_TRY(linear(L.fc1, ldq_d, a.inter, "fc1", kEpiF32GeluX86, a.absmax + 3));
   if (ob) ESM_TRY(ob->capture(ctx, a.inter, Tf, 0));

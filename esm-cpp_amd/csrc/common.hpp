@@ -139,6 +139,12 @@ __device__ __forceinline__ float gelu2_as(float x) {
   return __builtin_fmaf(ax, erf_abs, x);
 }
 
+// Activation scale rule of the reference prefix (gemm_int8.cpp:434,476):
+// absmax/127, or 1 when the input is all zero.
+__device__ __forceinline__ float act_scale_from_absmax(float amax) {
+  return amax > 0.0f ? amax / 127.0f : 1.0f;
+}
+
 // Symmetric int8 quantisation of one value with a precomputed reciprocal
 // scale: clamp(rne(x * inv), -127, 127).
 __device__ __forceinline__ int quant_i8(float x, float inv) {

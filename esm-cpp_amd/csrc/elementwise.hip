@@ -16,12 +16,6 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave per row, 4 waves per block
 
-// Activation scale rule of the reference prefix (gemm_int8.cpp:434,476):
-// absmax/127, or 1 when the input is all zero.
-__device__ __forceinline__ float act_scale_from_absmax(float amax) {
-  return amax > 0.0f ? amax / 127.0f : 1.0f;
-}
-
 // Each value rounded to the nearest fp16 (ties to even) and widened back:
 // the reference's first-block fc1 escape (RoundToFp16Inplace, src/model.cpp:
 // 912-930, VCVTPS2PH round-to-nearest).

@@ -311,8 +311,20 @@ hipError_t launch_cast_f32(const float* x, size_t n, uint16_t* out,
 // AttentionVarlenAvx512 (head_dim 16, 32 or 64; q/k/v rows at t*ld + h*dh,
 // cu_seqlens on the device), LinearAvx512 (C = A W^T + bias with a kF32*
 // epilogue; GELU is GeluAvx512).
+// launch_layernorm_x86: out may be null for d = 320 or 1280
+// (layernorm_x86_rows_ok), the maxima alone; tail_absmax (same widths) also
+// receives max |out| of rows >= tail_row.
 hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma, const float* beta, float eps,
-                                float* out, int rows, int d, float* absmax, int round16, hipStream_t s);
+                                float* out, int rows, int d, float* absmax, int round16, hipStream_t s,
+                                float* tail_absmax = nullptr, int tail_row = 0x7fffffff);
+bool layernorm_x86_rows_ok(int d);
+// LayerNormAvx512 of x (no residual) quantised as QuantizeActPrefixAvx512 with
+// the per-tensor scale of *absmax, rows >= tail_row with *tail_absmax's: the
+// codes and scales of launch_layernorm_x86 then launch_quant_tensor (d = 320
+// or 1280, ldq >= d, the codes past d zeroed).
+hipError_t launch_layernorm_x86_quant(const float* x, const float* gamma, const float* beta, float eps, int rows,
+                                      int d, const float* absmax, const float* tail_absmax, int tail_row, int8_t* q,
+                                      int ldq, float* scales, int round16, hipStream_t s);
 hipError_t launch_gelu_x86(const float* x, float* out, size_t n, float* absmax, hipStream_t s);
 hipError_t launch_expf_glibc(const float* x, float* out, size_t n, hipStream_t s);
 hipError_t launch_rope_x86(float* x, int ld, const int* pos, int T, int heads, int head_dim, const float* cos_t,

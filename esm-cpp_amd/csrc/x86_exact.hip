@@ -200,17 +200,64 @@ __global__ __launch_bounds__(256) void layernorm_x86_kernel(float* __restrict__ 
 // The same for rows of exactly NB 64-element blocks (d = 64 NB: no leftover
 // blocks, no tail), with the operations above in the same order: every
 // load of a row goes out before its first use and no per-block branch
-// splits them.
+// splits them. ln_x86_row: the row's LayerNorm from its values xv, in place
+// (y, fp16-rounded when round16), shared by the kernels below so that every
+// pass over a row computes the same values.
+template <int NB>
+__device__ __forceinline__ void ln_x86_row(float (&xv)[NB], const float* __restrict__ gamma,
+                                           const float* __restrict__ beta, float eps, int lane, int round16) {
+  constexpr int d = NB * 64;
+  const float inv_d = 1.0f / static_cast<float>(d);
+  const float tsum = 0.0f, vtail = 0.0f;  // no tail elements
+
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NB; ++t) s = s + xv[t];
+  float a = s + __shfl_down(s, 16);
+  float v16 = a + __shfl_down(a, 32);
+  const float mean = (__shfl(red16_lanes(v16), 0) + tsum) * inv_d;
+
+  s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    const float df = xv[t] - mean;
+    s = __builtin_fmaf(df, df, s);
+  }
+  a = s + __shfl_down(s, 16);
+  v16 = a + __shfl_down(a, 32);
+  const float ve = __builtin_fmaf(__shfl(red16_lanes(v16), 0) + vtail, inv_d, eps);
+  const float sd = static_cast<float>(sqrt(static_cast<double>(ve)));
+  const float inv_std = static_cast<float>(1.0 / static_cast<double>(sd));
+
+  float gv[NB], bv[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    gv[t] = gamma[(t << 6) + lane];
+    bv[t] = beta[(t << 6) + lane];
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    float y = __builtin_fmaf((xv[t] - mean) * inv_std, gv[t], bv[t]);
+    if (round16) y = static_cast<float>(static_cast<_Float16>(y));
+    xv[t] = y;
+  }
+}
+
+// Rows walked grid-stride (one atomic per block for each maximum). out may
+// be null (the maxima alone); absmax gets max |y| of every row, tail_absmax
+// (if not null) that of rows >= tail_row (LinearAmx's separately quantised
+// last rows).
 template <int NB>
 __global__ __launch_bounds__(256) void layernorm_x86_rows_kernel(float* __restrict__ x,
                                                                   const float* __restrict__ resid,
                                                                   const float* __restrict__ gamma,
                                                                   const float* __restrict__ beta, float eps,
                                                                   float* __restrict__ out, int rows,
-                                                                  float* __restrict__ absmax, int round16) {
+                                                                  float* __restrict__ absmax, int round16,
+                                                                  float* __restrict__ tail_absmax, int tail_row) {
   constexpr int d = NB * 64;
   const int lane = threadIdx.x & 63;
-  float m = 0.0f;
+  float m = 0.0f, mt = 0.0f;
   for (int row = blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += gridDim.x * 4) {
     float* xr = x + static_cast<size_t>(row) * d;
     float xv[NB];
@@ -227,44 +274,51 @@ __global__ __launch_bounds__(256) void layernorm_x86_rows_kernel(float* __restri
         xr[(t << 6) + lane] = xv[t];
       }
     }
-    const float inv_d = 1.0f / static_cast<float>(d);
-    const float tsum = 0.0f, vtail = 0.0f;  // no tail elements
-
-    float s = 0.0f;
+    ln_x86_row<NB>(xv, gamma, beta, eps, lane, round16);
+    float rm = 0.0f;
 #pragma unroll
-    for (int t = 0; t < NB; ++t) s = s + xv[t];
-    float a = s + __shfl_down(s, 16);
-    float v16 = a + __shfl_down(a, 32);
-    const float mean = (__shfl(red16_lanes(v16), 0) + tsum) * inv_d;
-
-    s = 0.0f;
+    for (int t = 0; t < NB; ++t) rm = fmaxf(rm, fabsf(xv[t]));
+    m = fmaxf(m, rm);
+    if (row >= tail_row) mt = fmaxf(mt, rm);
+    if (out) {
+      float* yr = out + static_cast<size_t>(row) * d;
 #pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      const float df = xv[t] - mean;
-      s = __builtin_fmaf(df, df, s);
-    }
-    a = s + __shfl_down(s, 16);
-    v16 = a + __shfl_down(a, 32);
-    const float ve = __builtin_fmaf(__shfl(red16_lanes(v16), 0) + vtail, inv_d, eps);
-    const float sd = static_cast<float>(sqrt(static_cast<double>(ve)));
-    const float inv_std = static_cast<float>(1.0 / static_cast<double>(sd));
-
-    float* yr = out + static_cast<size_t>(row) * d;
-    float gv[NB], bv[NB];
-#pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      gv[t] = gamma[(t << 6) + lane];
-      bv[t] = beta[(t << 6) + lane];
-    }
-#pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      float y = __builtin_fmaf((xv[t] - mean) * inv_std, gv[t], bv[t]);
-      if (round16) y = static_cast<float>(static_cast<_Float16>(y));
-      yr[(t << 6) + lane] = y;
-      m = fmaxf(m, fabsf(y));
+      for (int t = 0; t < NB; ++t) yr[(t << 6) + lane] = xv[t];
     }
   }
   if (absmax) block_atomic_max_nonneg(absmax, m);
+  if (tail_absmax) block_atomic_max_nonneg(tail_absmax, mt);
+}
+
+// The same LayerNorm (no residual: x holds the sum already) quantised as
+// QuantizeActPrefixAvx512 with the per-tensor scale of *absmax (rows >=
+// tail_row: *tail_absmax), each code quant_i8 and the row's tail zeroed, as
+// quant_tensor_kernel forms them: the codes of launch_layernorm_x86 then
+// launch_quant_tensor, without the fp32 output. One wave per row.
+template <int NB>
+__global__ __launch_bounds__(256) void layernorm_x86_quant_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ gamma,
+                                                                   const float* __restrict__ beta, float eps, int rows,
+                                                                   const float* __restrict__ absmax,
+                                                                   const float* __restrict__ tail_absmax, int tail_row,
+                                                                   int8_t* __restrict__ q, int ldq,
+                                                                   float* __restrict__ scales, int round16) {
+  constexpr int d = NB * 64;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + static_cast<size_t>(row) * d;
+  float xv[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) xv[t] = xr[(t << 6) + lane];
+  ln_x86_row<NB>(xv, gamma, beta, eps, lane, round16);
+  const float scale = act_scale_from_absmax(row >= tail_row ? *tail_absmax : *absmax);
+  const float inv = 1.0f / scale;
+  int8_t* qr = q + static_cast<size_t>(row) * ldq;
+#pragma unroll
+  for (int t = 0; t < NB; ++t) qr[(t << 6) + lane] = static_cast<int8_t>(quant_i8(xv[t], inv));
+  for (int c = d + lane; c < ldq; c += 64) qr[c] = 0;
+  if (lane == 0) scales[row] = scale;
 }
 
 // --------------------------------------------------------------- GELU
@@ -719,21 +773,42 @@ int grid_for(size_t n, int block, int cap) {
 
 }  // namespace
 
+bool layernorm_x86_rows_ok(int d) { return d == 1280 || d == 320; }
+
+hipError_t launch_layernorm_x86_quant(const float* x, const float* gamma, const float* beta, float eps, int rows,
+                                      int d, const float* absmax, const float* tail_absmax, int tail_row, int8_t* q,
+                                      int ldq, float* scales, int round16, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (!absmax || (tail_row < rows && !tail_absmax) || ldq < d) return hipErrorInvalidValue;
+  const dim3 grid((rows + 3) / 4), block(256);
+  if (d == 1280)
+    hipLaunchKernelGGL(layernorm_x86_quant_kernel<20>, grid, block, 0, s, x, gamma, beta, eps, rows, absmax,
+                       tail_absmax, tail_row, q, ldq, scales, round16);
+  else if (d == 320)
+    hipLaunchKernelGGL(layernorm_x86_quant_kernel<5>, grid, block, 0, s, x, gamma, beta, eps, rows, absmax,
+                       tail_absmax, tail_row, q, ldq, scales, round16);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
 hipError_t launch_layernorm_x86(float* x, const float* resid, const float* gamma, const float* beta, float eps,
-                                float* out, int rows, int d, float* absmax, int round16, hipStream_t s) {
+                                float* out, int rows, int d, float* absmax, int round16, hipStream_t s,
+                                float* tail_absmax, int tail_row) {
   if (rows <= 0 || d <= 0) return hipSuccess;
   const dim3 grid(grid_for(static_cast<size_t>(rows), 4, 1024)), block(256);  // rows walked grid-stride
   const int nb = d >> 6;
   if (d == 1280) {  // ESM-2 650M
     hipLaunchKernelGGL(layernorm_x86_rows_kernel<20>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, absmax,
-                       round16);
+                       round16, tail_absmax, tail_row);
     return hipGetLastError();
   }
   if (d == 320) {  // ESM-2 8M
     hipLaunchKernelGGL(layernorm_x86_rows_kernel<5>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, absmax,
-                       round16);
+                       round16, tail_absmax, tail_row);
     return hipGetLastError();
   }
+  if (!out || tail_absmax) return hipErrorInvalidValue;  // the generic kernel stores every row
   if (nb <= 5)
     hipLaunchKernelGGL(layernorm_x86_kernel<5>, grid, block, 0, s, x, resid, gamma, beta, eps, out, rows, d, absmax,
                        round16);
