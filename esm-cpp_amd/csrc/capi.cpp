@@ -1951,11 +1951,17 @@ int layer_int8_x86(esm_gfx950_ctx* ctx, const esm_gfx950_model* m, const DevLaye
     }
   }
   ESM_TRY(ctx->time_begin("attention", &slot));
+  // Each work item's largest |output| goes to the LayerNorm buffer (dead
+  // here) and one workgroup reduces them: the output's maximum.
+  float* part = static_cast<size_t>(P.nwork) <= Td ? a.ln : nullptr;
   ESM_HIP(ctx, launch_attention_x86(a.qkv, a.qkv + d, a.qkv + 2 * d, 3 * d, dh, md.cu, P.B, H, P.maxL, a.attn, d, s,
-                                    x86_score_scratch(P, a, Tf, H), md.work, P.nwork));
+                                    x86_score_scratch(P, a, Tf, H), md.work, P.nwork, part));
   ESM_TRY(ctx->time_end(slot));
   if (ob) ESM_TRY(ob->capture(ctx, a.attn, Td, 0));
-  ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
+  if (part)
+    ESM_HIP(ctx, launch_max_of(part, static_cast<size_t>(P.nwork), a.absmax + 1, s));
+  else
+    ESM_HIP(ctx, launch_absmax(a.attn, Td, a.absmax + 1, s));
   ESM_TRY(quant(a.attn, d, ldq_d, a.absmax + 1, d, a.absmax + 5));
   ESM_TRY(linear(L.out, ldq_d, a.ybuf, "out"));
   if (ln_two_pass) {

@@ -336,9 +336,11 @@ bool attention_x86_supported(int head_dim);
 // The scratch must fit 32-bit float offsets per head (cu's total below 2^32).
 // work: null (every (64-query tile, head, sequence) of a 3-D grid), or
 // build_work's list at 64-query tiles without XCD queues (nwork items).
+// part_max (with work only, nwork floats): each item's largest |output|.
 hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
                                 int batch, int heads, int max_len, float* out, int ldo, hipStream_t s,
-                                float* scores = nullptr, const AttnWork* work = nullptr, int nwork = 0);
+                                float* scores = nullptr, const AttnWork* work = nullptr, int nwork = 0,
+                                float* part_max = nullptr);
 size_t attention_x86_score_floats(const int* cu, int batch, int heads);
 hipError_t launch_linear_x86(const float* A, int lda, const float* W, int ldw, const float* bias, float* C, int ldc,
                              int M, int N, int K, int epi, hipStream_t s);

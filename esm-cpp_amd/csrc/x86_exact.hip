@@ -455,7 +455,8 @@ template <int DH, bool SC>
 __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, int ld, const int* __restrict__ cu,
                                                       int heads, float* __restrict__ out, int ldo,
-                                                      float* __restrict__ scores, const AttnWork* __restrict__ work) {
+                                                      float* __restrict__ scores, const AttnWork* __restrict__ work,
+                                                      float* __restrict__ part_max) {
   __shared__ __attribute__((aligned(16))) float ks[kX86Keys][DH];
   __shared__ __attribute__((aligned(16))) float vs[kX86Keys][DH];
   int b = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * 64;
@@ -466,7 +467,12 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
     q0 = w.q0;
   }
   const int s0 = cu[b], L = cu[b + 1] - s0;
-  if (q0 >= L) return;
+  // part_max (optional): slot blockIdx.x receives the largest |output| the
+  // workgroup stores (0 for an item past its sequence).
+  if (q0 >= L) {
+    if (part_max && threadIdx.x == 0) part_max[blockIdx.x] = 0.0f;
+    return;
+  }
   const int lane = threadIdx.x;
   const int i = min(q0 + lane, L - 1);
   const bool active = q0 + lane < L;
@@ -598,11 +604,18 @@ __global__ __launch_bounds__(64, 3) void attn_x86_kernel(const float* __restrict
       }
     }
   }
+  float m = 0.0f;
   if (active) {
     float* orow = out + static_cast<size_t>(s0 + q0 + lane) * ldo + static_cast<size_t>(h) * DH;
 #pragma unroll
     for (int d4 = 0; d4 < DH / 4; ++d4)
       *reinterpret_cast<float4*>(orow + d4 * 4) = float4{o[d4 * 4], o[d4 * 4 + 1], o[d4 * 4 + 2], o[d4 * 4 + 3]};
+#pragma unroll
+    for (int d = 0; d < DH; ++d) m = fmaxf(m, fabsf(o[d]));
+  }
+  if (part_max) {
+    m = wave_max(m);
+    if (lane == 0) part_max[blockIdx.x] = m;
   }
 }
 
@@ -859,17 +872,18 @@ size_t attention_x86_score_floats(const int* cu, int batch, int heads) {
 
 hipError_t launch_attention_x86(const float* q, const float* k, const float* v, int ld, int head_dim, const int* cu,
                                 int batch, int heads, int max_len, float* out, int ldo, hipStream_t s,
-                                float* scores, const AttnWork* work, int nwork) {
+                                float* scores, const AttnWork* work, int nwork, float* part_max) {
   if (batch <= 0 || max_len <= 0) return hipSuccess;
   if (work && nwork <= 0) return hipSuccess;
+  if (part_max && !work) return hipErrorInvalidValue;  // one slot per work item
   const dim3 grid = work ? dim3(nwork) : dim3((max_len + 63) / 64, heads, batch), block(64);
 #define ESM_ATTN_X86(DH)                                                                                           \
   if (scores)                                                                                                      \
     hipLaunchKernelGGL((attn_x86_kernel<DH, true>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, scores,   \
-                       work);                                                                                      \
+                       work, part_max);                                                                            \
   else                                                                                                             \
     hipLaunchKernelGGL((attn_x86_kernel<DH, false>), grid, block, 0, s, q, k, v, ld, cu, heads, out, ldo, nullptr, \
-                       work);
+                       work, part_max);
   switch (head_dim) {
     case 16: ESM_ATTN_X86(16) break;
     case 32: ESM_ATTN_X86(32) break;
