@@ -608,7 +608,7 @@ __global__ __launch_bounds__(256, 4) void attn_x3_kernel(
     const int qi = qbase + row;
     if (qi < L) {
       *reinterpret_cast<float4*>(out + static_cast<size_t>(start + qi) * ld_out + hoff + unit * 4) = val;
-      m = fmaxf(m, fmaxf(fmaxf(fabsf(val.x), fabsf(val.y)), fmaxf(fabsf(val.z), fabsf(val.w))));
+      if (part_max) m = fmaxf(m, fmaxf(fmaxf(fabsf(val.x), fabsf(val.y)), fmaxf(fabsf(val.z), fabsf(val.w))));
     }
   }
   if (part_max) {
