@@ -442,8 +442,12 @@ __global__ __launch_bounds__(256) void gelu_quant_rows_r24_kernel(
       // (e & 1) + 2 odd), the high plane's 16 bits of e
       const uint32_t sel = 0x0cu | ((static_cast<uint32_t>(e & 1) + 2u * odd) << 8) | ((4u + 2u * (e & 1)) << 16) |
                            ((5u + 2u * (e & 1)) << 24);
+      // Past the row's end the input is zeroed before the GELU (gelu2_as(0)
+      // is +0), a select rather than a branch around the GELU, so that the
+      // eight independent GELUs of a vector stay in one basic block and
+      // their latencies overlap.
       const float x = __uint_as_float(__builtin_amdgcn_perm(hw[e >> 1], lw[e >> 1], sel));
-      v[j][e] = ok ? gelu2_as(x) : 0.0f;
+      v[j][e] = gelu2_as(ok ? x : 0.0f);
       amax = fmaxf(amax, fabsf(v[j][e]));
     }
   }
