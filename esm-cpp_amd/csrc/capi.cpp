@@ -886,15 +886,29 @@ extern "C" int esm_gfx950_attention_varlen_avx512(esm_gfx950_ctx* ctx, const flo
   const int T = cu_seqlens[batch_size];
   if (T == 0) return ESM_GFX950_OK;
   ESM_REQUIRE(ctx, q && k && v && out, "attention_varlen_avx512: null pointer");
+  // The forward's form of the kernel: a work list of 64-query items,
+  // longest sequences first, and the score cache (when its per-head offsets
+  // fit 32 bits). Scratch: cu, the work list, the scores.
   int maxL = 0;
   for (int b = 0; b < batch_size; ++b) maxL = std::max(maxL, cu_seqlens[b + 1] - cu_seqlens[b]);
+  std::vector<AttnWork> work;
+  build_work(cu_seqlens, batch_size, num_heads, kAttnF32QTile, &work);
+  const size_t cu_bytes = (static_cast<size_t>(batch_size + 1) * 4 + 15) & ~static_cast<size_t>(15);
+  const size_t work_bytes = (work.size() * sizeof(AttnWork) + 255) & ~static_cast<size_t>(255);
+  const size_t n_scores = attention_x86_score_floats(cu_seqlens, batch_size, num_heads);
+  const bool cache = n_scores / static_cast<size_t>(num_heads) < (static_cast<size_t>(1) << 32);
   void* sp = nullptr;
-  ESM_TRY(ctx->get_scratch(static_cast<size_t>(batch_size + 1) * 4, &sp));
-  ESM_HIP(ctx, hipMemcpyAsync(sp, cu_seqlens, static_cast<size_t>(batch_size + 1) * 4, hipMemcpyHostToDevice,
+  ESM_TRY(ctx->get_scratch(cu_bytes + work_bytes + (cache ? n_scores * 4 : 0), &sp));
+  char* base = static_cast<char*>(sp);
+  ESM_HIP(ctx, hipMemcpyAsync(base, cu_seqlens, static_cast<size_t>(batch_size + 1) * 4, hipMemcpyHostToDevice,
+                              ctx->stream));
+  ESM_HIP(ctx, hipMemcpyAsync(base + cu_bytes, work.data(), work.size() * sizeof(AttnWork), hipMemcpyHostToDevice,
                               ctx->stream));
   const int ld = num_heads * head_dim;
-  ESM_HIP(ctx, launch_attention_x86(q, k, v, ld, head_dim, static_cast<int*>(sp), batch_size, num_heads, maxL, out, ld,
-                                    ctx->stream));
+  ESM_HIP(ctx, launch_attention_x86(q, k, v, ld, head_dim, reinterpret_cast<int*>(base), batch_size, num_heads, maxL,
+                                    out, ld, ctx->stream,
+                                    cache ? reinterpret_cast<float*>(base + cu_bytes + work_bytes) : nullptr,
+                                    reinterpret_cast<AttnWork*>(base + cu_bytes), static_cast<int>(work.size())));
   ESM_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ESM_GFX950_OK;
 }

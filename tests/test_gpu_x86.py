@@ -131,6 +131,42 @@ def test_attention_avx512_config2(dev, oracle):
     assert_bits(out.numpy(), oracle.x86_attention_varlen(q, k, v, cu, H, dh), "attention config 2")
 
 
+def test_attention_avx512_zero_weights_against_nonfinite_v(dev, oracle):
+    """The reference skips a zero weight (attention.cpp:392), so a key whose
+    weight is exactly 0 adds nothing even when its V row holds an Inf or a
+    NaN, while the queries that give it a weight carry the Inf / NaN. Every
+    Q row is constant: 1 for half the queries, 1e-4 for the others; the
+    marked keys (inside whole 16-key chunks) are -88 / 64 in every dim, so
+    for the first half their score lies 88.0-88.3 below the maximum, where
+    the reference's chunk exponential returns exactly 0 (2^-127 built from a
+    zero exponent field), and for the second half every weight is about
+    1 / L. Lengths give 128-query items with both halves, with one half,
+    and short ones."""
+    lengths = [200, 70, 130, 40]
+    cu = cu_from_lengths(lengths)
+    T, H, dh = int(cu[-1]), 2, 64
+    r = rng(77)
+    small = r.random(T) < 0.5
+    q = np.repeat(np.where(small, 1e-4, 1.0)[:, None], H * dh, axis=1).astype(np.float32)
+    k = (r.standard_normal((T, H * dh)) * 0.01).astype(np.float32)
+    v = r.standard_normal((T, H * dh)).astype(np.float32)
+    marked = [int(cu[0]) + 5, int(cu[0]) + 150, int(cu[1]) + 3, int(cu[2]) + 17, int(cu[3]) + 31]
+    for t in marked:
+        k[t] = -88.0 / dh
+    v[marked[0]] = np.inf
+    v[marked[1], :dh] = np.nan
+    v[marked[2], dh:] = -np.inf
+    v[marked[3], 7] = np.inf
+    v[marked[4], dh + 1] = np.nan
+    out = dev.empty((T, H * dh), np.float32)
+    dev.attention_varlen_avx512(dev.array(q), dev.array(k), dev.array(v), cu, H, dh, out)
+    want = oracle.x86_attention_varlen(q, k, v, cu, H, dh)
+    # The case is the intended one: the first half's outputs stay finite,
+    # the second half's are not.
+    assert np.isfinite(want[~small]).all() and not np.isfinite(want[small]).all()
+    assert_bits(out.numpy(), want, "zero weights against non-finite V")
+
+
 def _x86_model(dev, w, int8, numerics):
     m = eg.Model(dev, w, int8=int8, act_mode=eg.ACT_PER_TENSOR)
     m.set_numerics(numerics)
