@@ -302,7 +302,10 @@ int esm_gfx950_linear_f32_avx512(esm_gfx950_ctx* ctx, const float* A, const floa
 int esm_gfx950_rope_apply_varlen_avx512(esm_gfx950_ctx* ctx, float* x, const float* cos, const float* sin,
                                         const int* cu_seqlens, int batch_size, int num_heads, int head_dim);
 /* AttentionVarlenAvx512 (src/kernels/attention.cpp:240-430, 770-811),
- * head_dim 16, 32 or 64. */
+ * head_dim 16, 32 or 64. Runs the forward's kernel: the context's op
+ * scratch grows to hold every score once, num_heads x sum over sequences of
+ * roundup(L, 64) x L floats (391 MB for config 2's 256 sequences of
+ * 20 heads). */
 int esm_gfx950_attention_varlen_avx512(esm_gfx950_ctx* ctx, const float* q, const float* k, const float* v,
                                        const int* cu_seqlens, int batch_size, int num_heads, int head_dim,
                                        float* out);
